@@ -1,0 +1,508 @@
+"""The HIP backend: the reference's backend protocol on MI355X kernels.
+
+Implements the functions that ``diffrast_amd.ops`` and ``DepthPeeler`` call on a backend module,
+with the signatures of the reference backends (src/diffrast/backends/triton.py:14-92,
+reference.py:38-265): ``rasterize``, ``rasterize_layer``, ``interpolate``, ``texture``,
+``antialias``, plus what the reference's ops layer takes from its reference backend directly
+(ops.py:259-300, topology.py:16): ``texture_construct_mip``, ``pack``, ``edge_neighbours``, and
+the batched range mode ``rasterize_ranges`` that replaces the per-item loop of ops.py:69-74 and
+peeling.py:80-92.
+
+Each op is a ``torch.autograd.Function`` whose forward and backward call the C ABI of
+libdiffrast_hip.so on the current stream of the tensors' device. Inputs arrive validated by
+``ops.py`` (float32 / int32, shapes checked) and are made contiguous here. The backward passes
+are kernels and cannot be differentiated again (``first_order``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Sequence
+
+import torch
+from torch import Tensor
+
+from diffrast_amd.backends import _lib
+from diffrast_amd.backends._autograd import first_order
+from diffrast_amd.backends._lib import call, ptr, ref
+
+IMPLEMENTED: frozenset[str] = frozenset({"rasterize", "interpolate", "texture", "antialias"})
+
+# A key with every bit set marks a pixel that no triangle covers (uint64 max, stored in int64).
+EMPTY_KEY = -1
+
+FILTERS = {"nearest": 0, "linear": 1, "linear-mipmap-nearest": 2, "linear-mipmap-linear": 3}
+BOUNDARIES = {"wrap": 0, "clamp": 1, "zero": 2, "cube": 3}
+
+
+def _dense(t: Tensor | None) -> Tensor | None:
+    return None if t is None else t.contiguous()
+
+
+def _saveable(t: Tensor | None) -> Tensor | None:
+    # Inference tensors cannot be saved for backward (reference _triton_interpolate.py:214-215).
+    return t.clone() if t is not None and t.is_inference() else t
+
+
+def _stream(t: Tensor) -> int:
+    return _lib.stream(t.device)
+
+
+# ---------------------------------------------------------------------------------------------
+# Rasterize
+# ---------------------------------------------------------------------------------------------
+
+
+class _Geometry:
+    """DrRasterGeometry of one call, kept alive with the tensors it points to."""
+
+    def __init__(self, pos: Tensor, tri: Tensor, resolution, ranges=None, range_prefix=None,
+                 batch=None, num_instances=None):
+        height, width = resolution
+        self.pos, self.tri = pos, tri
+        self.ranges, self.range_prefix = ranges, range_prefix
+        shared = pos.ndim == 2
+        self.batch = int(batch if batch is not None else pos.shape[0])
+        num_tri = int(tri.shape[0])
+        self.struct = _lib.RasterGeometry(
+            pos=ptr(pos),
+            pos_batch_stride=0 if (shared or (pos.shape[0] == 1 and self.batch > 1))
+            else pos.shape[1] * 4,
+            tri=ptr(tri),
+            num_tri=num_tri,
+            batch=self.batch,
+            height=int(height),
+            width=int(width),
+            ranges=ptr(ranges),
+            range_prefix=ptr(range_prefix),
+            num_instances=int(num_instances if num_instances is not None else self.batch * num_tri),
+        )
+        self.shape = (self.batch, int(height), int(width))
+
+
+def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
+    """Visibility keys [batch, height, width] (int64 holding the uint64 key bits)."""
+    device = geo.pos.device
+    keys = torch.empty(geo.shape, dtype=torch.int64, device=device)
+    size = ctypes.c_size_t()
+    call("dr_raster_workspace_size", ref(geo.struct), ctypes.byref(size))
+    workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
+    counts = (ctypes.c_uint32 * 3)()
+    prev = None if previous is None else previous.contiguous()
+    stream = _lib.stream(device)
+    call("dr_raster_visibility_begin", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),
+         size.value, counts, stream)
+    if counts[1]:
+        entries = torch.empty(counts[1], dtype=torch.int32, device=device)
+        call("dr_raster_visibility_finish", ref(geo.struct), ptr(prev), ptr(keys),
+             ptr(workspace), size.value, ptr(entries), counts, stream)
+    return keys
+
+
+class _Resolve(torch.autograd.Function):
+    """rast / rast_db from keys; gradients to pos (reference.py:69-114)."""
+
+    @staticmethod
+    def forward(ctx, pos, keys, geo, grad_db):
+        batch, height, width = geo.shape
+        rast = pos.new_empty(batch, height, width, 4)
+        rast_db = pos.new_empty(batch, height, width, 4)
+        call("dr_resolve_forward", ref(geo.struct), ptr(keys), ptr(rast), ptr(rast_db),
+             _stream(pos))
+        ctx.geo = geo
+        ctx.grad_db = grad_db
+        ctx.save_for_backward(_saveable(pos), keys)
+        if not grad_db:
+            ctx.mark_non_differentiable(rast_db)
+        return rast, rast_db
+
+    @staticmethod
+    @first_order("rasterize")
+    def backward(ctx, grad_rast, grad_rast_db):
+        pos, keys = ctx.saved_tensors
+        if not ctx.needs_input_grad[0]:
+            return None, None, None, None
+        geo = ctx.geo
+        grad_pos = torch.zeros_like(pos, memory_format=torch.contiguous_format)
+        if grad_rast is None:
+            grad_rast = pos.new_zeros(*geo.shape, 4)
+        grad_db = _dense(grad_rast_db) if ctx.grad_db else None
+        # The geometry points at the forward's tensors, which are still alive (saved).
+        struct = _lib.RasterGeometry.from_buffer_copy(geo.struct)
+        struct.pos = ptr(pos)
+        call("dr_resolve_backward", ref(struct), ptr(keys), ptr(grad_rast.contiguous()),
+             ptr(grad_db), ptr(grad_pos), _stream(pos))
+        return grad_pos, None, None, None
+
+
+def _empty_layer(pos: Tensor, batch: int, resolution) -> tuple[Tensor, Tensor, Tensor]:
+    empty = pos.new_zeros(batch, *resolution, 4)
+    keys = torch.full((batch, *resolution), EMPTY_KEY, dtype=torch.int64, device=pos.device)
+    return empty, empty.clone(), keys
+
+
+def rasterize(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad_db: bool):
+    """(reference: triton.py:14-18)"""
+    rast, rast_db, _ = rasterize_layer(pos, tri, resolution, grad_db, None)
+    return rast, rast_db
+
+
+def rasterize_layer(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad_db: bool,
+                    previous: Tensor | None):
+    """One depth layer behind ``previous`` (the keys returned for the layer before) and its
+    keys (reference: triton.py:21-40, reference.py:45-66)."""
+    if tri.shape[0] == 0 or pos.shape[0] == 0:
+        return _empty_layer(pos, pos.shape[0], resolution)
+    pos, tri = pos.contiguous(), tri.contiguous()
+    geo = _Geometry(pos, tri, resolution)
+    keys = _visibility(geo, previous)
+    rast, rast_db = _Resolve.apply(pos, keys, geo, grad_db)
+    return rast, rast_db, keys
+
+
+def rasterize_ranges(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad_db: bool,
+                     ranges: Tensor, previous: Tensor | None = None):
+    """Range mode in one launch: image i draws ``tri[start_i : start_i + count_i]`` of the
+    shared ``pos`` ([vertices, 4]); ids count from the start of ``tri``, as after the
+    reference's join_ranges (ops.py:490-508). Returns ``(rast, rast_db, keys)``."""
+    table = [(int(s), int(c)) for s, c in ranges.tolist()]
+    batch = len(table)
+    if batch == 0 or tri.shape[0] == 0:
+        return _empty_layer(pos, batch, resolution)
+    counts = [c for _, c in table]
+    prefix = [0]
+    for c in counts:
+        prefix.append(prefix[-1] + c)
+    if prefix[-1] == 0:
+        return _empty_layer(pos, batch, resolution)
+    device = pos.device
+    pos, tri = pos.contiguous(), tri.contiguous()
+    ranges_dev = torch.tensor(table, dtype=torch.int32).to(device, non_blocking=True)
+    prefix_dev = torch.tensor(prefix, dtype=torch.int64).to(device, non_blocking=True)
+    geo = _Geometry(pos, tri, resolution, ranges=ranges_dev, range_prefix=prefix_dev,
+                    batch=batch, num_instances=prefix[-1])
+    keys = _visibility(geo, previous)
+    rast, rast_db = _Resolve.apply(pos, keys, geo, grad_db)
+    return rast, rast_db, keys
+
+
+# ---------------------------------------------------------------------------------------------
+# Interpolate
+# ---------------------------------------------------------------------------------------------
+
+
+def _interp_args(attr, rast, rast_db, tri, diff_dev, num_diff):
+    batch, height, width, _ = rast.shape
+    shared = attr.ndim == 2 or attr.shape[0] == 1
+    return _lib.InterpolateArgs(
+        attr=ptr(attr), attr_batch_stride=0 if shared else attr.shape[-2] * attr.shape[-1],
+        num_vertices=attr.shape[-2], channels=attr.shape[-1], rast=ptr(rast),
+        rast_db=ptr(rast_db), tri=ptr(tri), num_tri=tri.shape[0], batch=batch, height=height,
+        width=width, num_diff=num_diff, diff=ptr(diff_dev))
+
+
+class _Interpolate(torch.autograd.Function):
+    """(reference: _triton_interpolate.py:185-254, reference.py:117-146)"""
+
+    @staticmethod
+    def forward(ctx, attr, rast, rast_db, tri, diff):
+        attr, rast, tri = attr.contiguous(), rast.contiguous(), tri.contiguous()
+        rast_db = _dense(rast_db) if diff else None
+        batch, height, width, _ = rast.shape
+        diff_dev = torch.tensor(diff, dtype=torch.int32).to(rast.device) if diff else None
+        out = attr.new_empty(batch, height, width, attr.shape[-1])
+        out_da = attr.new_empty(batch, height, width, 2 * len(diff))
+        args = _interp_args(attr, rast, rast_db, tri, diff_dev, len(diff))
+        call("dr_interpolate_forward", ref(args), ptr(out), ptr(out_da) if diff else None,
+             _stream(rast))
+        ctx.diff = diff
+        ctx.save_for_backward(_saveable(attr), _saveable(rast), _saveable(rast_db), tri,
+                              diff_dev)
+        if not diff:
+            ctx.mark_non_differentiable(out_da)
+        return out, out_da
+
+    @staticmethod
+    @first_order("interpolate")
+    def backward(ctx, grad_out, grad_out_da):
+        attr, rast, rast_db, tri, diff_dev = ctx.saved_tensors
+        need_attr, need_rast, need_db = ctx.needs_input_grad[:3]
+        if not (need_attr or need_rast or need_db):
+            return None, None, None, None, None
+        diff = ctx.diff
+        if grad_out is None:
+            grad_out = attr.new_zeros(*rast.shape[:3], attr.shape[-1])
+        grad_out = grad_out.contiguous()
+        grad_da = _dense(grad_out_da) if diff else None
+        grad_attr = torch.zeros_like(attr) if need_attr else None
+        grad_rast = torch.empty_like(rast) if need_rast else None
+        grad_db = torch.empty_like(rast_db) if (need_db and diff) else None
+        args = _interp_args(attr, rast, rast_db, tri, diff_dev, len(diff))
+        call("dr_interpolate_backward", ref(args), ptr(grad_out), ptr(grad_da), ptr(grad_attr),
+             ptr(grad_rast), ptr(grad_db), _stream(rast))
+        return grad_attr, grad_rast, grad_db, None, None
+
+
+def interpolate(attr: Tensor, rast: Tensor, tri: Tensor, rast_db: Tensor | None,
+                diff_attrs: Sequence[int]):
+    """(reference: triton.py:50-56)"""
+    return _Interpolate.apply(attr, rast, rast_db, tri, tuple(int(c) for c in diff_attrs))
+
+
+# ---------------------------------------------------------------------------------------------
+# Texture
+# ---------------------------------------------------------------------------------------------
+
+
+def _chain_sizes(height: int, width: int, max_mip_level: int | None) -> list[tuple[int, int]]:
+    """Sizes of the box-filtered chain: halve rounding up until 1x1 (reference.py:433-446)."""
+    sizes = [(height, width)]
+    while max(sizes[-1]) > 1 and (max_mip_level is None or len(sizes) <= max_mip_level):
+        h, w = sizes[-1]
+        sizes.append(((h + 1) // 2, (w + 1) // 2))
+    return sizes
+
+
+def _tables(sizes, faces):
+    heights = tuple(h for h, _ in sizes)
+    widths = tuple(w for _, w in sizes)
+    offsets, total = [], 0
+    for h, w in sizes:
+        offsets.append(total)
+        total += faces * h * w
+    return heights, widths, tuple(offsets), total
+
+
+def _level_arrays(heights, widths, offsets):
+    n = len(heights)
+    return ((ctypes.c_int32 * n)(*heights), (ctypes.c_int32 * n)(*widths),
+            (ctypes.c_int64 * n)(*offsets))
+
+
+class _MipChain(torch.autograd.Function):
+    """Packed buffer [tex_batch, texels, channels] of tex and its box-filtered levels; the
+    backward pass folds level gradients down into tex (reference.py:433-519)."""
+
+    @staticmethod
+    def forward(ctx, tex, tables):
+        faces = 6 if tex.ndim == 5 else 1
+        heights, widths, offsets = tables
+        tex_batch, channels = tex.shape[0], tex.shape[-1]
+        total = offsets[-1] + faces * heights[-1] * widths[-1]
+        base = faces * heights[0] * widths[0]
+        packed = tex.new_empty(tex_batch, total, channels)
+        packed[:, :base].copy_(tex.reshape(tex_batch, base, channels))
+        call("dr_mip_build", ptr(packed), tex_batch, channels, total, faces, len(heights),
+             *_level_arrays(heights, widths, offsets), _stream(tex))
+        ctx.meta = (tex.shape, faces, tables, total, base)
+        return packed
+
+    @staticmethod
+    @first_order("texture")
+    def backward(ctx, grad_packed):
+        shape, faces, (heights, widths, offsets), total, base = ctx.meta
+        grad = grad_packed.contiguous().clone()
+        call("dr_mip_build_backward", ptr(grad), shape[0], shape[-1], total, faces,
+             len(heights), *_level_arrays(heights, widths, offsets), _stream(grad))
+        return grad[:, :base].reshape(shape), None
+
+
+def _mip_chain(tex: Tensor, max_mip_level: int | None):
+    faces = 6 if tex.ndim == 5 else 1
+    heights, widths, offsets, _ = _tables(_chain_sizes(tex.shape[-3], tex.shape[-2],
+                                                       max_mip_level), faces)
+    tables = (heights, widths, offsets)
+    return _MipChain.apply(tex, tables), tables
+
+
+class _Texture(torch.autograd.Function):
+    """(reference: _triton_texture.py:429-508, reference.py:149-194, _cube.py)"""
+
+    @staticmethod
+    def forward(ctx, texels, uv, uv_da, bias, tables, filter_mode, boundary_mode):
+        texels, uv = texels.contiguous(), uv.contiguous()
+        uv_da, bias = _dense(uv_da), _dense(bias)
+        batch, height, width = uv.shape[:3]
+        out = texels.new_empty(batch, height, width, texels.shape[-1])
+        args = _texture_args(texels, uv, uv_da, bias, tables, filter_mode, boundary_mode)
+        call("dr_texture_forward", ref(args), ptr(out), _stream(uv))
+        ctx.meta = (tables, filter_mode, boundary_mode)
+        ctx.save_for_backward(_saveable(texels), _saveable(uv), _saveable(uv_da),
+                              _saveable(bias))
+        return out
+
+    @staticmethod
+    @first_order("texture")
+    def backward(ctx, grad_out):
+        texels, uv, uv_da, bias = ctx.saved_tensors
+        tables, filter_mode, boundary_mode = ctx.meta
+        need_tex, need_uv, need_da, need_bias = ctx.needs_input_grad[:4]
+        grad_texels = torch.zeros_like(texels) if need_tex else None
+        coord_grad = filter_mode != "nearest"
+        grad_uv = torch.empty_like(uv) if (need_uv and coord_grad) else None
+        grad_da = torch.empty_like(uv_da) if (need_da and uv_da is not None) else None
+        grad_bias = torch.empty_like(bias) if (need_bias and bias is not None) else None
+        if grad_texels is None and grad_uv is None and grad_da is None and grad_bias is None:
+            return None, None, None, None, None, None, None
+        args = _texture_args(texels, uv, uv_da, bias, tables, filter_mode, boundary_mode)
+        call("dr_texture_backward", ref(args), ptr(grad_out.contiguous()), ptr(grad_texels),
+             ptr(grad_uv), ptr(grad_da), ptr(grad_bias), _stream(uv))
+        return grad_texels, grad_uv, grad_da, grad_bias, None, None, None
+
+
+def _texture_args(texels, uv, uv_da, bias, tables, filter_mode, boundary_mode):
+    heights, widths, offsets = tables
+    n = len(heights)
+    if n > _lib.MAX_LEVELS:
+        raise ValueError(f"at most {_lib.MAX_LEVELS} mip levels are supported, got {n}.")
+    args = _lib.TextureArgs()
+    args.texels = ptr(texels)
+    args.tex_batch = texels.shape[0]
+    args.channels = texels.shape[-1]
+    args.num_texels = texels.shape[1]
+    args.num_levels = n
+    args.faces = 6 if boundary_mode == "cube" else 1
+    for k in range(n):
+        args.level_height[k] = heights[k]
+        args.level_width[k] = widths[k]
+        args.level_offset[k] = offsets[k]
+    args.uv = ptr(uv)
+    args.uv_da = ptr(uv_da)
+    args.bias = ptr(bias)
+    args.batch, args.height, args.width = uv.shape[:3]
+    args.filter = FILTERS[filter_mode]
+    args.boundary = BOUNDARIES[boundary_mode]
+    return args
+
+
+def pack(levels: Sequence[Tensor]):
+    """Join ``tex`` and mip levels into one buffer [tex_batch, texels, channels] and its size
+    tables (reference.py:504-519). A level shared across the batch is repeated when the base
+    level is not. The tables are tuples of Python ints."""
+    batch, channels = levels[0].shape[0], levels[0].shape[-1]
+    faces = 6 if levels[0].ndim == 5 else 1
+    sizes = [(level.shape[-3], level.shape[-2]) for level in levels]
+    heights, widths, offsets, _ = _tables(sizes, faces)
+    parts = [level.expand(batch, *level.shape[1:]).reshape(batch, -1, channels)
+             for level in levels]
+    texels = parts[0] if len(parts) == 1 else torch.cat(parts, 1)
+    return texels, heights, widths, offsets
+
+
+def texture_construct_mip(tex: Tensor, max_mip_level: int | None) -> list[Tensor]:
+    """Mip levels 1 and up of ``tex`` as views of one packed buffer, differentiable with
+    respect to ``tex`` (reference.py:197-199)."""
+    packed, (heights, widths, offsets) = _mip_chain(tex, max_mip_level)
+    faces = 6 if tex.ndim == 5 else 1
+    levels = []
+    for k in range(1, len(heights)):
+        count = faces * heights[k] * widths[k]
+        shape = (tex.shape[0], *((6,) if faces == 6 else ()), heights[k], widths[k], tex.shape[-1])
+        levels.append(packed[:, offsets[k]:offsets[k] + count].reshape(shape))
+    return levels
+
+
+def texture(tex: Tensor, uv: Tensor, uv_da: Tensor | None, filter_mode: str, boundary_mode: str,
+            max_mip_level: int | None, mip_level_bias: Tensor | None = None,
+            mip: Sequence[Tensor] | None = None, packed=None):
+    """(reference: triton.py:59-79, reference.py:149-194)"""
+    mipmapped = "mipmap" in filter_mode
+    if not mipmapped:
+        faces = 6 if boundary_mode == "cube" else 1
+        h, w = tex.shape[-3], tex.shape[-2]
+        texels = tex.reshape(tex.shape[0], faces * h * w, tex.shape[-1])
+        tables = ((h,), (w,), (0,))
+        return _Texture.apply(texels, uv, None, None, tables, filter_mode, boundary_mode)
+    count = None if max_mip_level is None else max_mip_level + 1
+    if packed is not None:
+        texels, heights, widths, offsets = packed
+        tables = (tuple(heights[:count]), tuple(widths[:count]), tuple(offsets[:count]))
+    elif mip is not None:
+        levels = [tex, *mip][:count]
+        texels, heights, widths, offsets = pack(levels)
+        tables = (heights, widths, offsets)
+    else:
+        texels, tables = _mip_chain(tex, max_mip_level)
+    return _Texture.apply(texels, uv, uv_da, mip_level_bias, tables, filter_mode, boundary_mode)
+
+
+# ---------------------------------------------------------------------------------------------
+# Antialias
+# ---------------------------------------------------------------------------------------------
+
+
+def edge_neighbours(tri: Tensor) -> Tensor:
+    """Partner of each edge, int32 [triangles, 3], -1 when unshared or non-manifold
+    (reference.py:768-787), from a GPU hash table."""
+    tri = tri.contiguous()
+    out = torch.empty(tri.shape[0], 3, dtype=torch.int32, device=tri.device)
+    if tri.shape[0] == 0:
+        return out
+    size = ctypes.c_size_t()
+    call("dr_edge_hash_workspace_size", tri.shape[0], ctypes.byref(size))
+    workspace = torch.empty(size.value, dtype=torch.uint8, device=tri.device)
+    call("dr_edge_neighbours", ptr(tri), tri.shape[0], ptr(workspace), size.value, ptr(out),
+         _stream(tri))
+    return out
+
+
+def silhouette_mask(pos: Tensor, tri: Tensor, neighbours: Tensor) -> Tensor:
+    """Silhouette bits per (pos batch, triangle), uint8 (reference.py:790-814)."""
+    pos3 = pos if pos.ndim == 3 else pos[None]
+    pos3 = pos3.contiguous()
+    mask = torch.empty(pos3.shape[0], tri.shape[0], dtype=torch.uint8, device=pos.device)
+    call("dr_silhouette_mask", ptr(pos3), pos3.shape[1] * 4, pos3.shape[0], ptr(tri),
+         tri.shape[0], ptr(neighbours), ptr(mask), _stream(pos))
+    return mask
+
+
+def _aa_args(color, rast, pos, tri, mask, boost):
+    batch, height, width, channels = color.shape
+    per_view = pos.ndim == 3 and pos.shape[0] > 1
+    return _lib.AntialiasArgs(
+        color=ptr(color), channels=channels, batch=batch, height=height, width=width,
+        rast=ptr(rast), pos=ptr(pos), pos_batch_stride=pos.shape[-2] * 4 if per_view else 0,
+        tri=ptr(tri), num_tri=tri.shape[0], silhouette=ptr(mask),
+        silhouette_batch_stride=tri.shape[0] if per_view else 0, boost=boost)
+
+
+class _Antialias(torch.autograd.Function):
+    """(reference: _triton_antialias.py:271-320, reference.py:202-265)"""
+
+    @staticmethod
+    def forward(ctx, color, rast, pos, tri, mask, boost):
+        color, rast, pos, tri = (t.contiguous() for t in (color, rast, pos, tri))
+        out = torch.empty_like(color)
+        args = _aa_args(color, rast, pos, tri, mask, boost)
+        call("dr_antialias_forward", ref(args), ptr(out), _stream(color))
+        ctx.boost = boost
+        ctx.save_for_backward(_saveable(color), _saveable(rast), _saveable(pos), tri, mask)
+        return out
+
+    @staticmethod
+    @first_order("antialias")
+    def backward(ctx, grad_out):
+        color, rast, pos, tri, mask = ctx.saved_tensors
+        need_color, _, need_pos = ctx.needs_input_grad[:3]
+        grad_color = torch.empty_like(color) if need_color else None
+        grad_pos = torch.zeros_like(pos) if need_pos else None
+        if grad_color is None and grad_pos is None:
+            return None, None, None, None, None, None
+        args = _aa_args(color, rast, pos, tri, mask, ctx.boost)
+        call("dr_antialias_backward", ref(args), ptr(grad_out.contiguous()), ptr(grad_color),
+             ptr(grad_pos), _stream(color))
+        return grad_color, None, grad_pos, None, None, None
+
+
+def antialias(color: Tensor, rast: Tensor, pos: Tensor, tri: Tensor, pos_gradient_boost: float,
+              neighbours: Tensor | None = None) -> Tensor:
+    """(reference: triton.py:82-92, reference.py:202-265)"""
+    if tri.shape[0] == 0:
+        return color.clone()
+    tri = tri.contiguous()
+    if neighbours is None:
+        neighbours = edge_neighbours(tri)
+    neighbours = neighbours.to(torch.int32).contiguous()
+    with torch.no_grad():
+        mask = silhouette_mask(pos.detach(), tri, neighbours)
+    return _Antialias.apply(color, rast, pos, tri, mask, float(pos_gradient_boost))

@@ -1,0 +1,712 @@
+// Rasterize for gfx950: visibility as 64-bit (depth, triangle) keys, then resolve.
+//
+// Visibility decides, per pixel, the nearest triangle that covers the pixel centre, with the
+// coverage test of the reference backend (src/diffrast/backends/reference.py:293-365) and its
+// tie-break (lower triangle row on equal depth, reference.py:368-397). Every triangle instance
+// (image, triangle) gets one thread in the setup kernel, which culls it (a non-finite
+// coordinate, or every w <= 0: the interpolated w is then never positive) and bounds its
+// pixels. Triangles whose bounding box holds at most kSmallPixels pixel centres -- nearly all
+// of a dense mesh -- are rasterized right there; the others are binned into 16x16 tiles
+// (counts, a three-phase scan, a scatter into per-tile lists) and rasterized by one 256-thread
+// workgroup per tile chunk, which stages up to 256 triangles in LDS and keeps the best key of
+// its pixel in a register. Both paths merge into the key buffer with 64-bit atomic min.
+//
+// The resolve kernels turn keys into rast / rast_db (reference.py:69-114) and carry gradients
+// back to the vertices.
+#include "common.h"
+
+namespace dr {
+namespace {
+
+constexpr int kTile = 16;            // tile edge in pixels; a tile is one 256-thread workgroup
+constexpr int kChunk = 256;          // triangles per tile work item
+constexpr int kSmallPixels = 16;     // bounding boxes up to this many pixels skip binning
+constexpr int kScanBlock = 1024;     // elements per scan block (256 threads x 4)
+constexpr float kAreaTolerance = 2.384185791015625e-07f;  // 2 * float32 epsilon
+
+struct Workspace {
+  int4* records;             // binned triangles: (image, row, tx0 | tx1 << 16, ty0 | ty1 << 16)
+  uint32_t* tile_counts;     // [tiles]
+  uint32_t* tile_offsets;    // [tiles + 1] exclusive prefix of tile_counts
+  uint32_t* tile_cursor;     // [tiles] fill positions for the scatter
+  uint32_t* chunk_offsets;   // [tiles + 1] exclusive prefix of ceil(count / kChunk)
+  uint2* block_sums;         // [scan blocks] (entries, chunks)
+  uint32_t* counters;        // [0] binned triangles, [1] entries, [2] chunks
+  int tiles_x, tiles_y;
+  int64_t tiles;
+  int scan_blocks;
+  size_t bytes;
+};
+
+size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
+
+Workspace layout(const DrRasterGeometry& g, char* base) {
+  Workspace w{};
+  w.tiles_x = (g.width + kTile - 1) / kTile;
+  w.tiles_y = (g.height + kTile - 1) / kTile;
+  w.tiles = (int64_t)g.batch * w.tiles_x * w.tiles_y;
+  w.scan_blocks = (int)((w.tiles + 1 + kScanBlock - 1) / kScanBlock);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off = align_up(off + bytes);
+    return p;
+  };
+  w.counters = (uint32_t*)take(16);
+  w.tile_counts = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
+  w.tile_offsets = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
+  w.tile_cursor = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
+  w.chunk_offsets = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
+  w.block_sums = (uint2*)take(sizeof(uint2) * (w.scan_blocks + 1));
+  w.records = (int4*)take(sizeof(int4) * (size_t)(g.num_instances > 0 ? g.num_instances : 1));
+  w.bytes = off;
+  return w;
+}
+
+// ---- geometry helpers -------------------------------------------------------------------
+
+// (image, triangle row) of triangle instance i.
+__device__ __forceinline__ void instance(const DrRasterGeometry& g, int64_t i, int& b, int& t) {
+  if (g.ranges == nullptr) {
+    b = (int)(i / g.num_tri);
+    t = (int)(i - (int64_t)b * g.num_tri);
+    return;
+  }
+  int lo = 0, hi = g.batch;  // largest b with range_prefix[b] <= i
+  while (hi - lo > 1) {
+    int mid = (lo + hi) >> 1;
+    if (g.range_prefix[mid] <= i) lo = mid; else hi = mid;
+  }
+  b = lo;
+  t = g.ranges[2 * b] + (int)(i - g.range_prefix[b]);
+}
+
+struct Tri {
+  float x[3], y[3], z[3], w[3];
+  float reach_x, reach_y;  // max_k |x_k| + |w_k| and likewise for y (reference.py:321-326)
+};
+
+__device__ __forceinline__ void load_tri(const DrRasterGeometry& g, int b, int t, Tri& T,
+                                         int (&v)[3]) {
+  const int32_t* row = g.tri + 3 * (int64_t)t;
+  v[0] = row[0];
+  v[1] = row[1];
+  v[2] = row[2];
+  const float* base = g.pos + (int64_t)b * g.pos_batch_stride;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    float4 p = load4(base + 4 * (int64_t)v[k]);
+    T.x[k] = p.x;
+    T.y[k] = p.y;
+    T.z[k] = p.z;
+    T.w[k] = p.w;
+  }
+  T.reach_x = fmaxf(fmaxf(fabsf(T.x[0]) + fabsf(T.w[0]), fabsf(T.x[1]) + fabsf(T.w[1])),
+                    fabsf(T.x[2]) + fabsf(T.w[2]));
+  T.reach_y = fmaxf(fmaxf(fabsf(T.y[0]) + fabsf(T.w[0]), fabsf(T.y[1]) + fabsf(T.w[1])),
+                    fabsf(T.y[2]) + fabsf(T.w[2]));
+}
+
+// Fill-rule test of one edge (reference.py:338-365).
+__device__ __forceinline__ bool inside_edge(float e, float ai, float ci, float wi, float aj,
+                                            float cj, float wj, bool positive) {
+  float q = e;
+  if (e == 0.0f) {
+    float gx = ci * wj - cj * wi;
+    float gy = aj * wi - ai * wj;
+    q = (gx == 0.0f) ? gy : gx;
+  }
+  return positive ? (q > 0.0f) : (q < 0.0f);
+}
+
+// Coverage of pixel centre (px, py) and depth there: the reference's operations in its order
+// (reference.py:301-335), one rounding each. The triangle is known to be finite.
+__device__ __forceinline__ bool covers(const float* x, const float* y, const float* z,
+                                       const float* w, float reach_x, float reach_y, float px,
+                                       float py, float& depth) {
+  const float a0 = x[0] - px * w[0];
+  const float a1 = x[1] - px * w[1];
+  const float a2 = x[2] - px * w[2];
+  const float c0 = y[0] - py * w[0];
+  const float c1 = y[1] - py * w[1];
+  const float c2 = y[2] - py * w[2];
+  const float e0 = a1 * c2 - a2 * c1;
+  const float e1 = a2 * c0 - a0 * c2;
+  const float e2 = a0 * c1 - a1 * c0;
+  const float s = e0 + e1 + e2;
+  const bool positive = s > 0.0f;
+  if (!inside_edge(e0, a1, c1, w[1], a2, c2, w[2], positive)) return false;
+  if (!inside_edge(e1, a2, c2, w[2], a0, c0, w[0], positive)) return false;
+  if (!inside_edge(e2, a0, c0, w[0], a1, c1, w[1], positive)) return false;
+  const float span_x = fabsf(a0) + fabsf(a1) + fabsf(a2);
+  const float span_y = fabsf(c0) + fabsf(c1) + fabsf(c2);
+  if (!(fabsf(s) > (reach_x * span_y + span_x * (reach_y + span_y)) * kAreaTolerance))
+    return false;
+  const float ew = e0 * w[0] + e1 * w[1] + e2 * w[2];
+  if (positive ? !(ew > 0.0f) : !(ew < 0.0f)) return false;
+  depth = (e0 * z[0] + e1 * z[1] + e2 * z[2]) / ew;
+  return depth >= -1.0f && depth <= 1.0f;
+}
+
+__device__ __forceinline__ bool finite_tri(const Tri& T) {
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+    ok = ok && isfinite(T.x[k]) && isfinite(T.y[k]) && isfinite(T.z[k]) && isfinite(T.w[k]);
+  return ok;
+}
+
+// Pixel-centre range [lo, hi] along one axis that may be covered, or lo > hi for none.
+// p(n) = (n + 1) * size / 2 - 1/2 is the continuous pixel index of NDC coordinate n; the
+// margin covers the float32 error of the projection and of the pixel centres, which grows
+// with the image size.
+__device__ __forceinline__ void axis_range(float n0, float n1, float n2, int size, int& lo,
+                                           int& hi) {
+  const float half = 0.5f * (float)size;
+  const float p0 = (n0 + 1.0f) * half - 0.5f;
+  const float p1 = (n1 + 1.0f) * half - 0.5f;
+  const float p2 = (n2 + 1.0f) * half - 0.5f;
+  const float margin = 0.015625f + 4e-6f * (float)size;
+  float a = fminf(fminf(p0, p1), p2) - margin;
+  float c = fmaxf(fmaxf(p0, p1), p2) + margin;
+  a = fmaxf(a, -1.0f);
+  c = fminf(c, (float)size);
+  lo = max((int)ceilf(a), 0);
+  hi = min((int)floorf(c), size - 1);
+}
+
+// Whether a visibility key may enter this layer; merges it into the key buffer.
+__device__ __forceinline__ void merge_key(uint64_t* keys, const uint64_t* prev, int64_t pixel,
+                                          uint64_t key) {
+  if (prev != nullptr && key <= prev[pixel]) return;
+  if (key < keys[pixel]) atomicMin((unsigned long long*)(keys + pixel), (unsigned long long)key);
+}
+
+// ---- kernels ----------------------------------------------------------------------------
+
+__global__ void fill_keys(uint64_t* keys, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i < n; i += (int64_t)gridDim.x * blockDim.x) keys[i] = kEmptyKey;
+}
+
+__global__ void fill_u32(uint32_t* p, int64_t n, uint32_t value) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = value;
+}
+
+__global__ __launch_bounds__(256) void setup_kernel(DrRasterGeometry g, const uint64_t* prev,
+                                                    uint64_t* keys, Workspace ws) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  bool binned = false;
+  int b = 0, t = 0, x_lo = 0, x_hi = -1, y_lo = 0, y_hi = -1;
+  if (i < g.num_instances) {
+    instance(g, i, b, t);
+    Tri T;
+    int v[3];
+    load_tri(g, b, t, T, v);
+    const bool any_front = T.w[0] > 0.0f || T.w[1] > 0.0f || T.w[2] > 0.0f;
+    if (finite_tri(T) && any_front) {
+      if (T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
+        axis_range(T.x[0] / T.w[0], T.x[1] / T.w[1], T.x[2] / T.w[2], g.width, x_lo, x_hi);
+        axis_range(T.y[0] / T.w[0], T.y[1] / T.w[1], T.y[2] / T.w[2], g.height, y_lo, y_hi);
+      } else {
+        // Crossing the camera plane: the projection is unbounded, so take the whole image.
+        x_lo = 0;
+        x_hi = g.width - 1;
+        y_lo = 0;
+        y_hi = g.height - 1;
+      }
+      if (x_lo <= x_hi && y_lo <= y_hi) {
+        const int64_t count = (int64_t)(x_hi - x_lo + 1) * (y_hi - y_lo + 1);
+        if (count <= kSmallPixels) {
+          const int64_t image = (int64_t)b * g.height;
+          for (int y = y_lo; y <= y_hi; ++y) {
+            const float py = pixel_centre(y, g.height);
+            for (int x = x_lo; x <= x_hi; ++x) {
+              float depth;
+              if (covers(T.x, T.y, T.z, T.w, T.reach_x, T.reach_y, pixel_centre(x, g.width), py,
+                         depth))
+                merge_key(keys, prev, (image + y) * g.width + x, depth_key(depth, (uint32_t)t));
+            }
+          }
+        } else {
+          binned = true;
+        }
+      }
+    }
+  }
+  // Append binned triangles with one counter atomic per wave.
+  const uint64_t mask = __ballot(binned);
+  if (mask == 0) return;
+  const int lane = lane_id();
+  const int leader = __ffsll((unsigned long long)mask) - 1;
+  uint32_t base = 0;
+  if (lane == leader) base = atomicAdd(ws.counters, (uint32_t)__popcll(mask));
+  base = __shfl(base, leader);
+  if (!binned) return;
+  const uint32_t rec = base + (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
+  const int tx0 = x_lo / kTile, tx1 = x_hi / kTile, ty0 = y_lo / kTile, ty1 = y_hi / kTile;
+  ws.records[rec] = make_int4(b, t, (int)((uint32_t)tx0 | ((uint32_t)tx1 << 16)),
+                             (int)((uint32_t)ty0 | ((uint32_t)ty1 << 16)));
+  uint32_t* counts = ws.tile_counts + (int64_t)b * ws.tiles_x * ws.tiles_y;
+  for (int ty = ty0; ty <= ty1; ++ty)
+    for (int tx = tx0; tx <= tx1; ++tx) atomicAdd(counts + ty * ws.tiles_x + tx, 1u);
+}
+
+// Inclusive scan of (entries, chunks) pairs over the 256 threads of a block.
+__device__ __forceinline__ uint2 block_inclusive_scan(uint2 v, uint2* lds) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x / DR_WAVE;
+#pragma unroll
+  for (int d = 1; d < DR_WAVE; d <<= 1) {
+    uint32_t ax = __shfl_up(v.x, d), ay = __shfl_up(v.y, d);
+    if (lane >= d) {
+      v.x += ax;
+      v.y += ay;
+    }
+  }
+  if (lane == DR_WAVE - 1) lds[wave] = v;
+  __syncthreads();
+  uint2 offset = make_uint2(0, 0);
+  for (int k = 0; k < wave; ++k) {
+    offset.x += lds[k].x;
+    offset.y += lds[k].y;
+  }
+  __syncthreads();
+  return make_uint2(v.x + offset.x, v.y + offset.y);
+}
+
+__device__ __forceinline__ uint2 scan_item(const uint32_t* counts, int64_t i, int64_t n) {
+  uint32_t c = i < n ? counts[i] : 0u;
+  return make_uint2(c, (c + kChunk - 1) / kChunk);
+}
+
+// Phase 1: per-block totals.
+__global__ __launch_bounds__(256) void scan_reduce(const uint32_t* counts, int64_t n,
+                                                   uint2* block_sums) {
+  __shared__ uint2 lds[4];
+  const int64_t base = (int64_t)blockIdx.x * kScanBlock + threadIdx.x * 4;
+  uint2 s = make_uint2(0, 0);
+  for (int k = 0; k < 4; ++k) {
+    uint2 v = scan_item(counts, base + k, n);
+    s.x += v.x;
+    s.y += v.y;
+  }
+  uint2 total = block_inclusive_scan(s, lds);
+  if (threadIdx.x == 255) block_sums[blockIdx.x] = total;
+}
+
+// Phase 2: exclusive scan of the block totals in one block; totals go to the counters.
+__global__ __launch_bounds__(256) void scan_blocks(uint2* block_sums, int blocks,
+                                                   uint32_t* counters) {
+  __shared__ uint2 lds[4];
+  __shared__ uint2 step_total;
+  uint2 carry = make_uint2(0, 0);
+  for (int start = 0; start < blocks; start += 256) {
+    const int i = start + threadIdx.x;
+    const uint2 v = i < blocks ? block_sums[i] : make_uint2(0, 0);
+    const uint2 inc = block_inclusive_scan(v, lds);
+    if (i < blocks) block_sums[i] = make_uint2(carry.x + inc.x - v.x, carry.y + inc.y - v.y);
+    if (threadIdx.x == 255) step_total = inc;
+    __syncthreads();
+    carry.x += step_total.x;
+    carry.y += step_total.y;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    counters[1] = carry.x;
+    counters[2] = carry.y;
+  }
+}
+
+// Phase 3: exclusive offsets per tile (and the totals at index n).
+__global__ __launch_bounds__(256) void scan_apply(const uint32_t* counts, int64_t n,
+                                                  const uint2* block_sums, uint32_t* offsets,
+                                                  uint32_t* cursor, uint32_t* chunk_offsets) {
+  __shared__ uint2 lds[4];
+  const int64_t base = (int64_t)blockIdx.x * kScanBlock + threadIdx.x * 4;
+  uint2 items[4];
+  uint2 s = make_uint2(0, 0);
+  for (int k = 0; k < 4; ++k) {
+    items[k] = scan_item(counts, base + k, n);
+    s.x += items[k].x;
+    s.y += items[k].y;
+  }
+  uint2 inc = block_inclusive_scan(s, lds);
+  uint2 run = make_uint2(block_sums[blockIdx.x].x + inc.x - s.x,
+                         block_sums[blockIdx.x].y + inc.y - s.y);
+  for (int k = 0; k < 4; ++k) {
+    const int64_t i = base + k;
+    if (i <= n) {
+      offsets[i] = run.x;
+      chunk_offsets[i] = run.y;
+      if (i < n) cursor[i] = run.x;
+    }
+    run.x += items[k].x;
+    run.y += items[k].y;
+  }
+}
+
+__global__ __launch_bounds__(256) void scatter_kernel(Workspace ws, uint32_t num_records,
+                                                      uint32_t* entries) {
+  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= num_records) return;
+  const int4 rec = ws.records[r];
+  const uint32_t rx = (uint32_t)rec.z, ry = (uint32_t)rec.w;
+  const int tx0 = (int)(rx & 0xffffu), tx1 = (int)(rx >> 16);
+  const int ty0 = (int)(ry & 0xffffu), ty1 = (int)(ry >> 16);
+  uint32_t* cursor = ws.tile_cursor + (int64_t)rec.x * ws.tiles_x * ws.tiles_y;
+  for (int ty = ty0; ty <= ty1; ++ty)
+    for (int tx = tx0; tx <= tx1; ++tx) entries[atomicAdd(cursor + ty * ws.tiles_x + tx, 1u)] = r;
+}
+
+__global__ __launch_bounds__(256) void tile_kernel(DrRasterGeometry g, const uint64_t* prev,
+                                                   uint64_t* keys, Workspace ws,
+                                                   const uint32_t* entries) {
+  __shared__ float sx[3][kChunk], sy[3][kChunk], sz[3][kChunk], sw[3][kChunk];
+  __shared__ float s_reach_x[kChunk], s_reach_y[kChunk];
+  __shared__ uint32_t s_tri[kChunk];
+  __shared__ int64_t s_tile;
+
+  // Tile of this work item: the last tile whose first chunk is at or before blockIdx.x.
+  if (threadIdx.x == 0) {
+    int64_t lo = 0, hi = ws.tiles;
+    while (hi - lo > 1) {
+      int64_t mid = (lo + hi) >> 1;
+      if (ws.chunk_offsets[mid] <= blockIdx.x) lo = mid; else hi = mid;
+    }
+    s_tile = lo;
+  }
+  __syncthreads();
+  const int64_t tile = s_tile;
+  const uint32_t chunk = blockIdx.x - ws.chunk_offsets[tile];
+  const uint32_t first = ws.tile_offsets[tile] + chunk * kChunk;
+  const uint32_t end = min(ws.tile_offsets[tile + 1], first + kChunk);
+  const int n = (int)(end - first);
+
+  const int per_image = ws.tiles_x * ws.tiles_y;
+  const int b = (int)(tile / per_image);
+  const int in_image = (int)(tile - (int64_t)b * per_image);
+  const int x = (in_image % ws.tiles_x) * kTile + (threadIdx.x % kTile);
+  const int y = (in_image / ws.tiles_x) * kTile + (threadIdx.x / kTile);
+
+  if ((int)threadIdx.x < n) {
+    const int4 rec = ws.records[entries[first + threadIdx.x]];
+    Tri T;
+    int v[3];
+    load_tri(g, rec.x, rec.y, T, v);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      sx[k][threadIdx.x] = T.x[k];
+      sy[k][threadIdx.x] = T.y[k];
+      sz[k][threadIdx.x] = T.z[k];
+      sw[k][threadIdx.x] = T.w[k];
+    }
+    s_reach_x[threadIdx.x] = T.reach_x;
+    s_reach_y[threadIdx.x] = T.reach_y;
+    s_tri[threadIdx.x] = (uint32_t)rec.y;
+  }
+  __syncthreads();
+  if (x >= g.width || y >= g.height) return;
+
+  const int64_t pixel = ((int64_t)b * g.height + y) * g.width + x;
+  const uint64_t floor_key = prev != nullptr ? prev[pixel] : 0ull;
+  const float px = pixel_centre(x, g.width), py = pixel_centre(y, g.height);
+  uint64_t best = kEmptyKey;
+  for (int j = 0; j < n; ++j) {
+    const float X[3] = {sx[0][j], sx[1][j], sx[2][j]};
+    const float Y[3] = {sy[0][j], sy[1][j], sy[2][j]};
+    const float Z[3] = {sz[0][j], sz[1][j], sz[2][j]};
+    const float Wv[3] = {sw[0][j], sw[1][j], sw[2][j]};
+    float depth;
+    if (covers(X, Y, Z, Wv, s_reach_x[j], s_reach_y[j], px, py, depth)) {
+      const uint64_t key = depth_key(depth, s_tri[j]);
+      if (key < best && (prev == nullptr || key > floor_key)) best = key;
+    }
+  }
+  if (best != kEmptyKey && best < keys[pixel])
+    atomicMin((unsigned long long*)(keys + pixel), (unsigned long long)best);
+}
+
+// ---- resolve ----------------------------------------------------------------------------
+
+// Per-pixel quantities of the visible triangle, in the reference's operation order
+// (reference.py:84-111 with _edge_functions / _edge_derivatives, reference.py:274-290).
+struct Resolved {
+  float a[3], c[3], e[3], area, b[3], num, den, depth, dex[3], dey[3], sum_dx, sum_dy;
+  float db_dx[3], db_dy[3];
+};
+
+__device__ __forceinline__ void resolve_pixel(const Tri& T, float px, float py, Resolved& R) {
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    R.a[k] = T.x[k] - px * T.w[k];
+    R.c[k] = T.y[k] - py * T.w[k];
+  }
+  R.e[0] = R.a[1] * R.c[2] - R.a[2] * R.c[1];
+  R.e[1] = R.a[2] * R.c[0] - R.a[0] * R.c[2];
+  R.e[2] = R.a[0] * R.c[1] - R.a[1] * R.c[0];
+  R.area = R.e[0] + R.e[1] + R.e[2];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) R.b[k] = R.e[k] / R.area;
+  R.num = R.b[0] * T.z[0] + R.b[1] * T.z[1] + R.b[2] * T.z[2];
+  R.den = R.b[0] * T.w[0] + R.b[1] * T.w[1] + R.b[2] * T.w[2];
+  R.depth = R.num / R.den;
+  // d e / d px = c x w and d e / d py = w x a.
+  R.dex[0] = R.c[1] * T.w[2] - R.c[2] * T.w[1];
+  R.dex[1] = R.c[2] * T.w[0] - R.c[0] * T.w[2];
+  R.dex[2] = R.c[0] * T.w[1] - R.c[1] * T.w[0];
+  R.dey[0] = T.w[1] * R.a[2] - T.w[2] * R.a[1];
+  R.dey[1] = T.w[2] * R.a[0] - T.w[0] * R.a[2];
+  R.dey[2] = T.w[0] * R.a[1] - T.w[1] * R.a[0];
+  R.sum_dx = R.dex[0] + R.dex[1] + R.dex[2];
+  R.sum_dy = R.dey[0] + R.dey[1] + R.dey[2];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    R.db_dx[k] = (R.dex[k] - R.b[k] * R.sum_dx) / R.area;
+    R.db_dy[k] = (R.dey[k] - R.b[k] * R.sum_dy) / R.area;
+  }
+}
+
+__global__ __launch_bounds__(256) void resolve_forward_kernel(DrRasterGeometry g,
+                                                              const uint64_t* keys, float* rast,
+                                                              float* rast_db, float scale_x,
+                                                              float scale_y) {
+  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)g.batch * g.height * g.width;
+  if (pixel >= total) return;
+  const uint64_t key = keys[pixel];
+  if (key == kEmptyKey) {
+    store4(rast + 4 * pixel, make_float4(0.f, 0.f, 0.f, 0.f));
+    if (rast_db) store4(rast_db + 4 * pixel, make_float4(0.f, 0.f, 0.f, 0.f));
+    return;
+  }
+  const int t = (int)(uint32_t)key;
+  const int x = (int)(pixel % g.width);
+  const int64_t rest = pixel / g.width;
+  const int y = (int)(rest % g.height);
+  const int b = (int)(rest / g.height);
+  Tri T;
+  int v[3];
+  load_tri(g, b, t, T, v);
+  Resolved R;
+  resolve_pixel(T, pixel_centre(x, g.width), pixel_centre(y, g.height), R);
+  store4(rast + 4 * pixel, make_float4(R.b[0], R.b[1], R.depth, (float)(t + 1)));
+  if (rast_db)
+    store4(rast_db + 4 * pixel, make_float4(R.db_dx[0] * scale_x, R.db_dy[0] * scale_y,
+                                            R.db_dx[1] * scale_x, R.db_dy[1] * scale_y));
+}
+
+__device__ __forceinline__ void cross3(const float* u, const float* v, float* out) {
+  out[0] = u[1] * v[2] - u[2] * v[1];
+  out[1] = u[2] * v[0] - u[0] * v[2];
+  out[2] = u[0] * v[1] - u[1] * v[0];
+}
+
+// Reverse mode of resolve_pixel for the gradient of (b0, b1, depth) and, optionally, rast_db.
+// For u x v with upstream G: grad u = v x G, grad v = G x u.
+__global__ __launch_bounds__(256) void resolve_backward_kernel(
+    DrRasterGeometry g, const uint64_t* keys, const float* grad_rast, const float* grad_db,
+    float* grad_pos, float scale_x, float scale_y) {
+  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)g.batch * g.height * g.width;
+  int64_t merge_key_id = -1;
+  float vals[12];
+#pragma unroll
+  for (int i = 0; i < 12; ++i) vals[i] = 0.0f;
+  int v[3] = {0, 0, 0};
+  int pos_b = 0;
+  if (pixel < total) {
+    const uint64_t key = keys[pixel];
+    if (key != kEmptyKey) {
+      const int t = (int)(uint32_t)key;
+      const int x = (int)(pixel % g.width);
+      const int64_t rest = pixel / g.width;
+      const int y = (int)(rest % g.height);
+      const int b = (int)(rest / g.height);
+      pos_b = g.pos_batch_stride != 0 ? b : 0;
+      Tri T;
+      load_tri(g, b, t, T, v);
+      const float px = pixel_centre(x, g.width), py = pixel_centre(y, g.height);
+      Resolved R;
+      resolve_pixel(T, px, py, R);
+      const float4 gr = load4(grad_rast + 4 * pixel);
+      float gb[3] = {gr.x, gr.y, 0.0f};
+      float gw[3] = {0.f, 0.f, 0.f}, gz[3];
+      // depth = num / den
+      const float g_num = gr.z / R.den;
+      const float g_den = -gr.z * R.depth / R.den;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        gb[k] += g_num * T.z[k] + g_den * T.w[k];
+        gz[k] = g_num * R.b[k];
+        gw[k] = g_den * R.b[k];
+      }
+      float g_area = 0.0f;
+      float g_dex[3] = {0.f, 0.f, 0.f}, g_dey[3] = {0.f, 0.f, 0.f};
+      if (grad_db != nullptr) {
+        const float4 gd = load4(grad_db + 4 * pixel);
+        const float gx[3] = {gd.x * scale_x, gd.z * scale_x, 0.0f};
+        const float gy[3] = {gd.y * scale_y, gd.w * scale_y, 0.0f};
+        // db_dx_k = (dex_k - b_k Sx) / area, Sx = sum dex.
+        float dot_x = 0.f, dot_y = 0.f;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          dot_x += gx[k] * R.b[k];
+          dot_y += gy[k] * R.b[k];
+          gb[k] -= (gx[k] * R.sum_dx + gy[k] * R.sum_dy) / R.area;
+          g_area -= (gx[k] * R.db_dx[k] + gy[k] * R.db_dy[k]) / R.area;
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          g_dex[k] = (gx[k] - dot_x) / R.area;
+          g_dey[k] = (gy[k] - dot_y) / R.area;
+        }
+      }
+      // b_k = e_k / area
+      float dot_b = 0.f;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) dot_b += gb[k] * R.b[k];
+      g_area -= dot_b / R.area;
+      float ge[3];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) ge[k] = gb[k] / R.area + g_area;
+      // e = a x c; dex = c x w; dey = w x a.
+      float ga[3], gc[3], tmp[3];
+      cross3(R.c, ge, ga);
+      cross3(ge, R.a, gc);
+      cross3(T.w, g_dex, tmp);  // grad c from dex = c x w
+      for (int k = 0; k < 3; ++k) gc[k] += tmp[k];
+      cross3(g_dex, R.c, tmp);  // grad w from dex
+      for (int k = 0; k < 3; ++k) gw[k] += tmp[k];
+      cross3(R.a, g_dey, tmp);  // grad w from dey = w x a
+      for (int k = 0; k < 3; ++k) gw[k] += tmp[k];
+      cross3(g_dey, T.w, tmp);  // grad a from dey
+      for (int k = 0; k < 3; ++k) ga[k] += tmp[k];
+      // a = x - px w, c = y - py w
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        vals[4 * k + 0] = ga[k];
+        vals[4 * k + 1] = gc[k];
+        vals[4 * k + 2] = gz[k];
+        vals[4 * k + 3] = gw[k] - px * ga[k] - py * gc[k];
+      }
+      merge_key_id = (int64_t)pos_b * g.num_tri + t;
+    }
+  }
+  const int64_t stride = g.pos_batch_stride;
+  float* base = grad_pos + (int64_t)pos_b * stride;
+  wave_merged_scatter<12>(merge_key_id, vals, 4, [&](const float (&s)[12]) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      float* p = base + 4 * (int64_t)v[k];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (s[4 * k + c] != 0.0f) atomic_add(p + c, s[4 * k + c]);
+    }
+  });
+}
+
+}  // namespace
+}  // namespace dr
+
+using namespace dr;
+
+static bool valid_geometry(const DrRasterGeometry* g) {
+  if (!g || g->batch < 0 || g->num_tri < 0 || g->height <= 0 || g->width <= 0) return false;
+  if ((g->batch > 0 && g->num_tri > 0) && (!g->pos || !g->tri)) return false;
+  if (g->ranges && !g->range_prefix) return false;
+  if (g->num_tri > (1 << 24) || g->num_instances < 0) return false;
+  // Tile coordinates are stored in 16 bits.
+  if ((g->width + 15) / 16 > 0xffff || (g->height + 15) / 16 > 0xffff) return false;
+  return true;
+}
+
+extern "C" int dr_raster_workspace_size(const DrRasterGeometry* g, size_t* bytes) {
+  if (!valid_geometry(g) || !bytes) return DR_ERR_ARGUMENT;
+  *bytes = layout(*g, nullptr).bytes;
+  return DR_OK;
+}
+
+extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                                          uint64_t* keys, void* workspace,
+                                          size_t workspace_bytes, uint32_t counts[3],
+                                          void* stream) {
+  if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
+  counts[0] = counts[1] = counts[2] = 0;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t pixels = (int64_t)g->batch * g->height * g->width;
+  if (pixels == 0) return DR_OK;
+  Workspace ws = layout(*g, (char*)workspace);
+  if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
+  if (g->num_instances >= (int64_t)1 << 32) return DR_ERR_ARGUMENT;
+  const int fill_blocks = (int)std::min<int64_t>(blocks_for(pixels, 256), 65536);
+  fill_keys<<<fill_blocks, 256, 0, s>>>(keys, pixels);
+  fill_u32<<<(int)std::min<int64_t>(blocks_for(ws.tiles + 1, 256), 65536), 256, 0, s>>>(
+      ws.tile_counts, ws.tiles + 1, 0u);
+  fill_u32<<<1, 64, 0, s>>>(ws.counters, 4, 0u);
+  if (g->num_instances > 0) {
+    setup_kernel<<<blocks_for(g->num_instances, 256), 256, 0, s>>>(*g, prev_keys, keys, ws);
+    scan_reduce<<<ws.scan_blocks, 256, 0, s>>>(ws.tile_counts, ws.tiles, ws.block_sums);
+    scan_blocks<<<1, 256, 0, s>>>(ws.block_sums, ws.scan_blocks, ws.counters);
+    scan_apply<<<ws.scan_blocks, 256, 0, s>>>(ws.tile_counts, ws.tiles, ws.block_sums,
+                                              ws.tile_offsets, ws.tile_cursor,
+                                              ws.chunk_offsets);
+  }
+  int status = launch_status();
+  if (status != DR_OK) return status;
+  uint32_t host[4] = {0, 0, 0, 0};
+  if (hipMemcpyAsync(host, ws.counters, sizeof(host), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return DR_ERR_HIP;
+  counts[0] = host[0];
+  counts[1] = host[1];
+  counts[2] = host[2];
+  return DR_OK;
+}
+
+extern "C" int dr_raster_visibility_finish(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                                           uint64_t* keys, void* workspace,
+                                           size_t workspace_bytes, uint32_t* entries,
+                                           const uint32_t counts[3], void* stream) {
+  if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
+  if (counts[1] == 0) return DR_OK;
+  if (!entries) return DR_ERR_ARGUMENT;
+  Workspace ws = layout(*g, (char*)workspace);
+  if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
+  hipStream_t s = (hipStream_t)stream;
+  scatter_kernel<<<blocks_for(counts[0], 256), 256, 0, s>>>(ws, counts[0], entries);
+  tile_kernel<<<counts[2], 256, 0, s>>>(*g, prev_keys, keys, ws, entries);
+  return launch_status();
+}
+
+static void resolve_scales(const DrRasterGeometry* g, float& sx, float& sy) {
+  // The reference multiplies by the Python float 2 / size, which PyTorch rounds to float32.
+  sx = (float)(2.0 / (double)g->width);
+  sy = (float)(2.0 / (double)g->height);
+}
+
+extern "C" int dr_resolve_forward(const DrRasterGeometry* g, const uint64_t* keys, float* rast,
+                                  float* rast_db, void* stream) {
+  if (!valid_geometry(g) || !rast) return DR_ERR_ARGUMENT;
+  const int64_t pixels = (int64_t)g->batch * g->height * g->width;
+  if (pixels == 0) return DR_OK;
+  float sx, sy;
+  resolve_scales(g, sx, sy);
+  resolve_forward_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
+      *g, keys, rast, rast_db, sx, sy);
+  return launch_status();
+}
+
+extern "C" int dr_resolve_backward(const DrRasterGeometry* g, const uint64_t* keys,
+                                   const float* grad_rast, const float* grad_rast_db,
+                                   float* grad_pos, void* stream) {
+  if (!valid_geometry(g) || !grad_rast || !grad_pos) return DR_ERR_ARGUMENT;
+  const int64_t pixels = (int64_t)g->batch * g->height * g->width;
+  if (pixels == 0) return DR_OK;
+  float sx, sy;
+  resolve_scales(g, sx, sy);
+  resolve_backward_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
+      *g, keys, grad_rast, grad_rast_db, grad_pos, sx, sy);
+  return launch_status();
+}

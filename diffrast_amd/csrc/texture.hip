@@ -1,0 +1,749 @@
+// Texture sampling for gfx950: 2D textures and cube maps, nearest / bilinear / mipmapped
+// lookups with wrap, clamp or zero boundaries, their gradients, and the mip chain.
+//
+// The arithmetic follows the reference backend: texel coordinates and boundaries
+// (src/diffrast/backends/reference.py:555-672), level of detail and level blending
+// (reference.py:491-501, 522-552), cube-map projection and the integer edge fold
+// (src/diffrast/backends/_cube.py:44-143). One thread per pixel computes the tap addresses
+// of its one or two levels once and loops over channels. All levels live in one packed
+// buffer [tex_batch, texels, channels], so a mipmapped lookup is two bilinear lookups
+// wherever the pixel's levels are.
+//
+// The backward pass writes the coordinate, derivative and bias gradients per pixel and adds
+// texel gradients with fp32 atomics. The mip chain is built level by level with exact area
+// weights (reference.py:449-488), and its adjoint is a gather, so it needs no atomics.
+#include "common.h"
+
+namespace dr {
+namespace {
+
+constexpr float kFootprintLimit = 1e18f;  // reference.py:402
+constexpr float kDerivativeLimit = 1e18f; // _cube.py:36
+constexpr float kMinFootprint = 1e-30f;   // reference.py:501
+constexpr float kLn2 = 0.693147180559945309f;
+
+// ---- cube geometry (_cube.py) -----------------------------------------------------------
+
+// Per face: major axis, s axis and t axis as integer 3-vectors (_cube.py:31-33).
+__constant__ int kMajor[6][3] = {{1, 0, 0}, {-1, 0, 0}, {0, 1, 0}, {0, -1, 0}, {0, 0, 1}, {0, 0, -1}};
+__constant__ int kSAxis[6][3] = {{0, 0, -1}, {0, 0, 1}, {1, 0, 0}, {1, 0, 0}, {1, 0, 0}, {-1, 0, 0}};
+__constant__ int kTAxis[6][3] = {{0, -1, 0}, {0, -1, 0}, {0, 0, 1}, {0, 0, -1}, {0, -1, 0}, {0, -1, 0}};
+
+__device__ __forceinline__ int floor_div2(int v) { return v >= 0 ? v / 2 : -((-v + 1) / 2); }
+
+// Fold a texel one step outside its face onto the neighbouring face (_cube.py:105-143).
+// Returns false beyond a corner, where no texel exists.
+__device__ __forceinline__ bool cube_fold(int& face, int& row, int& col, int size) {
+  const bool over_col = col < 0 || col >= size;
+  const bool over_row = row < 0 || row >= size;
+  const int sc = 2 * col + 1 - size, tc = 2 * row + 1 - size;
+  int point[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    int p = size * kMajor[face][k] + sc * kSAxis[face][k] + tc * kTAxis[face][k];
+    p = min(max(p, -size), size);
+    if (over_col || over_row) p -= kMajor[face][k];
+    point[k] = p;
+  }
+  int axis = 0;
+  int best = abs(point[0]);
+  if (abs(point[1]) > best) { axis = 1; best = abs(point[1]); }
+  if (abs(point[2]) > best) axis = 2;
+  face = 2 * axis + (point[axis] < 0 ? 1 : 0);
+  int s_dot = 0, t_dot = 0;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    s_dot += point[k] * kSAxis[face][k];
+    t_dot += point[k] * kTAxis[face][k];
+  }
+  col = max(floor_div2(s_dot + size - 1), 0);
+  row = max(floor_div2(t_dot + size - 1), 0);
+  return !(over_col && over_row);
+}
+
+struct CubeProj {
+  bool valid, undefined;
+  int face;
+  float length, ma, rs, rt;
+  float dn[3];
+  float da[3][2];       // clamped, scaled derivatives
+  bool da_pass[3][2];   // inside the clamp
+  float d_ma[2], d_sc[2], d_tc[2];
+  float st[2];
+  float st_da[4];       // ds/dx, ds/dy, dt/dx, dt/dy
+};
+
+// Face selection and face coordinates of a direction (_cube.py:44-102).
+__device__ __forceinline__ void cube_project(const float* dir, const float* dir_da, CubeProj& P) {
+  float d[3] = {dir[0], dir[1], dir[2]};
+  const float ax0 = fabsf(d[0]), ay0 = fabsf(d[1]), az0 = fabsf(d[2]);
+  P.valid = isfinite(d[0]) && isfinite(d[1]) && isfinite(d[2]) &&
+            fmaxf(fmaxf(ax0, ay0), az0) >= 1.17549435e-38f;
+  if (!P.valid) {
+    d[0] = 0.0f;
+    d[1] = 0.0f;
+    d[2] = 1.0f;
+  }
+  const float ax = fabsf(d[0]), ay = fabsf(d[1]), az = fabsf(d[2]);
+  const bool x_major = ax >= ay && ax >= az;
+  const bool y_major = !x_major && ay >= az;
+  const int axis = x_major ? 0 : (y_major ? 1 : 2);
+  P.face = 2 * axis + (d[axis] < 0.0f ? 1 : 0);
+  P.length = fmaxf(fmaxf(ax, ay), az);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) P.dn[k] = d[k] / P.length;
+  const int* M = kMajor[P.face];
+  const int* S = kSAxis[P.face];
+  const int* T = kTAxis[P.face];
+  P.ma = P.dn[0] * (float)M[0] + P.dn[1] * (float)M[1] + P.dn[2] * (float)M[2];
+  const float sc = P.dn[0] * (float)S[0] + P.dn[1] * (float)S[1] + P.dn[2] * (float)S[2];
+  const float tc = P.dn[0] * (float)T[0] + P.dn[1] * (float)T[1] + P.dn[2] * (float)T[2];
+  P.rs = sc / P.ma;
+  P.rt = tc / P.ma;
+  P.st[0] = 0.5f * (P.rs + 1.0f);
+  P.st[1] = 0.5f * (P.rt + 1.0f);
+  P.undefined = false;
+  if (dir_da == nullptr) return;
+  bool any_nan = false;
+  for (int i = 0; i < 6; ++i) any_nan = any_nan || isnan(dir_da[i]);
+  P.undefined = P.valid && any_nan;
+  const bool use = P.valid && !P.undefined;
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float v = (use ? dir_da[2 * k + j] : 0.0f) / P.length;
+      P.da_pass[k][j] = v >= -kDerivativeLimit && v <= kDerivativeLimit;
+      P.da[k][j] = fminf(fmaxf(v, -kDerivativeLimit), kDerivativeLimit);
+    }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    P.d_ma[j] = P.da[0][j] * (float)M[0] + P.da[1][j] * (float)M[1] + P.da[2][j] * (float)M[2];
+    P.d_sc[j] = P.da[0][j] * (float)S[0] + P.da[1][j] * (float)S[1] + P.da[2][j] * (float)S[2];
+    P.d_tc[j] = P.da[0][j] * (float)T[0] + P.da[1][j] * (float)T[1] + P.da[2][j] * (float)T[2];
+  }
+  const float nan = __int_as_float(0x7fc00000);
+  P.st_da[0] = P.undefined ? nan : 0.5f * (P.d_sc[0] - P.rs * P.d_ma[0]) / P.ma;
+  P.st_da[1] = P.undefined ? nan : 0.5f * (P.d_sc[1] - P.rs * P.d_ma[1]) / P.ma;
+  P.st_da[2] = P.undefined ? nan : 0.5f * (P.d_tc[0] - P.rt * P.d_ma[0]) / P.ma;
+  P.st_da[3] = P.undefined ? nan : 0.5f * (P.d_tc[1] - P.rt * P.d_ma[1]) / P.ma;
+}
+
+// Gradient of cube_project: from d(loss)/d(st) and d(loss)/d(st_da) to the direction and
+// its derivatives. grad_dir gets 3 values, grad_dir_da 6 (or is nullptr).
+__device__ __forceinline__ void cube_project_backward(const CubeProj& P, float g_s, float g_t,
+                                                      const float* g_sda, float* grad_dir,
+                                                      float* grad_dir_da) {
+  const int* M = kMajor[P.face];
+  const int* S = kSAxis[P.face];
+  const int* T = kTAxis[P.face];
+  float g_rs = 0.5f * g_s, g_rt = 0.5f * g_t, g_ma = 0.0f;
+  float g_dsc[2] = {0.f, 0.f}, g_dtc[2] = {0.f, 0.f}, g_dma[2] = {0.f, 0.f};
+  if (g_sda != nullptr && !P.undefined) {
+    const float gds[2] = {g_sda[0], g_sda[1]}, gdt[2] = {g_sda[2], g_sda[3]};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float ds = P.st_da[j], dt = P.st_da[2 + j];
+      g_rs += gds[j] * (-0.5f * P.d_ma[j] / P.ma);
+      g_rt += gdt[j] * (-0.5f * P.d_ma[j] / P.ma);
+      g_ma -= (gds[j] * ds + gdt[j] * dt) / P.ma;
+      g_dsc[j] = 0.5f * gds[j] / P.ma;
+      g_dtc[j] = 0.5f * gdt[j] / P.ma;
+      g_dma[j] = -0.5f * (gds[j] * P.rs + gdt[j] * P.rt) / P.ma;
+    }
+  }
+  if (grad_dir_da != nullptr) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float g = g_dsc[j] * (float)S[k] + g_dtc[j] * (float)T[k] + g_dma[j] * (float)M[k];
+        g = (P.valid && !P.undefined && P.da_pass[k][j]) ? g / P.length : 0.0f;
+        grad_dir_da[2 * k + j] = g;
+      }
+  }
+  g_ma -= (g_rs * P.rs + g_rt * P.rt) / P.ma;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const float g_dn = (g_rs * (float)S[k] + g_rt * (float)T[k]) / P.ma + g_ma * (float)M[k];
+    grad_dir[k] = P.valid ? g_dn / P.length : 0.0f;
+  }
+}
+
+// ---- 2D coordinates, taps and levels ----------------------------------------------------
+
+struct Axis {
+  float x;     // continuous texel coordinate
+  bool bad;    // not finite (then x = 0)
+  bool pass;   // gradient reaches the input coordinate
+};
+
+// coord * size - shift, wrapped or saturated as for the boundary (reference.py:615-633).
+__device__ __forceinline__ Axis texel_axis(float coord, int size, float shift, int boundary) {
+  Axis A;
+  float c = coord;
+  if (boundary == DR_BOUNDARY_WRAP) c = c - floorf(c);
+  A.x = c * (float)size - shift;
+  A.pass = true;
+  if (boundary == DR_BOUNDARY_CLAMP || boundary == DR_BOUNDARY_ZERO) {
+    if (A.x < -1.0f) { A.x = -1.0f; A.pass = false; }
+    if (A.x > (float)size) { A.x = (float)size; A.pass = false; }
+  }
+  A.bad = !isfinite(A.x);
+  if (A.bad) {
+    A.x = 0.0f;
+    A.pass = false;
+  }
+  return A;
+}
+
+__device__ __forceinline__ int wrap_index(int i, int n) {
+  int r = i % n;
+  return r < 0 ? r + n : r;
+}
+
+// Texel index (in texels from the start of the image's packed buffer) of integer tap
+// (row, col) of a level; false when the tap reads zero (reference.py:636-672).
+__device__ __forceinline__ bool tap(int row, int col, int face, int h, int w, int64_t offset,
+                                    int boundary, int64_t& index) {
+  bool valid = true;
+  if (boundary == DR_BOUNDARY_CUBE) {
+    valid = cube_fold(face, row, col, w);
+  } else if (boundary == DR_BOUNDARY_WRAP) {
+    row = wrap_index(row, h);
+    col = wrap_index(col, w);
+  } else {
+    if (boundary == DR_BOUNDARY_ZERO) valid = row >= 0 && row < h && col >= 0 && col < w;
+    row = min(max(row, 0), h - 1);
+    col = min(max(col, 0), w - 1);
+  }
+  if (face >= 0) row += face * h;
+  index = offset + (int64_t)row * w + col;
+  return valid;
+}
+
+struct Bilinear {
+  int64_t index[4];
+  bool valid[4];
+  float fx, fy;
+  bool bad;
+  bool pass_x, pass_y;
+  float size_x, size_y;
+  // Cube corners: taps beyond two edges count as the mean of the other three.
+  bool cube;
+  float corner[4];  // 1 where (left|right) & (above|below) for taps 00, 01, 10, 11
+};
+
+__device__ __forceinline__ Bilinear bilinear_setup(float s, float t, int face, int h, int w,
+                                                   int64_t offset, int boundary) {
+  Bilinear L;
+  const Axis X = texel_axis(s, w, 0.5f, boundary);
+  const Axis Y = texel_axis(t, h, 0.5f, boundary);
+  const float x0 = floorf(X.x), y0 = floorf(Y.x);
+  L.fx = X.x - x0;
+  L.fy = Y.x - y0;
+  L.bad = X.bad || Y.bad;
+  L.pass_x = X.pass;
+  L.pass_y = Y.pass;
+  L.size_x = (float)w;
+  L.size_y = (float)h;
+  const int col = (int)x0, row = (int)y0;
+  L.valid[0] = tap(row, col, face, h, w, offset, boundary, L.index[0]);
+  L.valid[1] = tap(row, col + 1, face, h, w, offset, boundary, L.index[1]);
+  L.valid[2] = tap(row + 1, col, face, h, w, offset, boundary, L.index[2]);
+  L.valid[3] = tap(row + 1, col + 1, face, h, w, offset, boundary, L.index[3]);
+  L.cube = boundary == DR_BOUNDARY_CUBE;
+  if (L.cube) {
+    const bool left = col < 0, right = col + 1 >= w, above = row < 0, below = row + 1 >= h;
+    L.corner[0] = (left && above) ? 1.0f : 0.0f;
+    L.corner[1] = (right && above) ? 1.0f : 0.0f;
+    L.corner[2] = (left && below) ? 1.0f : 0.0f;
+    L.corner[3] = (right && below) ? 1.0f : 0.0f;
+  }
+  return L;
+}
+
+__device__ __forceinline__ void fetch4(const float* texels, const Bilinear& L, int C, int c,
+                                       float (&t)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) t[k] = L.valid[k] ? texels[L.index[k] * C + c] : 0.0f;
+}
+
+// Value of one channel (reference.py:601-611).
+__device__ __forceinline__ float bilinear_value(const Bilinear& L, const float (&t)[4]) {
+  const float fx = L.fx, fy = L.fy;
+  float out = (1.0f - fy) * ((1.0f - fx) * t[0] + fx * t[1]) +
+              fy * ((1.0f - fx) * t[2] + fx * t[3]);
+  if (L.cube) {
+    const float missing = (1.0f - fy) * ((1.0f - fx) * L.corner[0] + fx * L.corner[1]) +
+                          fy * ((1.0f - fx) * L.corner[2] + fx * L.corner[3]);
+    out = out + missing * (t[0] + t[1] + t[2] + t[3]) / 3.0f;
+  }
+  return out;
+}
+
+// Gradient of one channel's value: texel weights and d/dfx, d/dfy.
+__device__ __forceinline__ void bilinear_grad(const Bilinear& L, const float (&t)[4],
+                                              float (&wgt)[4], float& dfx, float& dfy) {
+  const float fx = L.fx, fy = L.fy;
+  wgt[0] = (1.0f - fy) * (1.0f - fx);
+  wgt[1] = (1.0f - fy) * fx;
+  wgt[2] = fy * (1.0f - fx);
+  wgt[3] = fy * fx;
+  dfx = (1.0f - fy) * (t[1] - t[0]) + fy * (t[3] - t[2]);
+  dfy = ((1.0f - fx) * t[2] + fx * t[3]) - ((1.0f - fx) * t[0] + fx * t[1]);
+  if (L.cube) {
+    const float missing = (1.0f - fy) * ((1.0f - fx) * L.corner[0] + fx * L.corner[1]) +
+                          fy * ((1.0f - fx) * L.corner[2] + fx * L.corner[3]);
+    const float share = (t[0] + t[1] + t[2] + t[3]) / 3.0f;
+    const float dm_dfx = (1.0f - fy) * (L.corner[1] - L.corner[0]) + fy * (L.corner[3] - L.corner[2]);
+    const float dm_dfy = ((1.0f - fx) * L.corner[2] + fx * L.corner[3]) -
+                         ((1.0f - fx) * L.corner[0] + fx * L.corner[1]);
+    dfx += dm_dfx * share;
+    dfy += dm_dfy * share;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wgt[k] += missing / 3.0f;
+  }
+}
+
+// Level of detail from the footprint (reference.py:491-501). uv_da = (du/dx, du/dy, dv/dx,
+// dv/dy); width and height are those of the base level.
+__device__ __forceinline__ float footprint_lod(const float* da, int height, int width) {
+  const float W = (float)width, H = (float)height, L = kFootprintLimit;
+  const float cx0 = fminf(fmaxf(da[0] * W, -L), L), cy0 = fminf(fmaxf(da[2] * H, -L), L);
+  const float cx1 = fminf(fmaxf(da[1] * W, -L), L), cy1 = fminf(fmaxf(da[3] * H, -L), L);
+  const float len_x = cx0 * cx0 + cy0 * cy0;
+  const float len_y = cx1 * cx1 + cy1 * cy1;
+  if (isnan(da[0]) || isnan(da[1]) || isnan(da[2]) || isnan(da[3]))
+    return __int_as_float(0x7fc00000);
+  return 0.5f * log2f(fmaxf(fmaxf(len_x, len_y), kMinFootprint));
+}
+
+__device__ __forceinline__ void footprint_lod_grad(const float* da, int height, int width,
+                                                   float g, float* grad) {
+  const float W = (float)width, H = (float)height, L = kFootprintLimit;
+  const float v[4] = {da[0] * W, da[1] * W, da[2] * H, da[3] * H};  // du/dx, du/dy, dv/dx, dv/dy
+  float c[4];
+  bool pass[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    pass[i] = v[i] >= -L && v[i] <= L;
+    c[i] = fminf(fmaxf(v[i], -L), L);
+  }
+  const float len_x = c[0] * c[0] + c[2] * c[2];
+  const float len_y = c[1] * c[1] + c[3] * c[3];
+  const float m = fmaxf(len_x, len_y);
+  float g_m = m >= kMinFootprint ? g * 0.5f / (m * kLn2) : 0.0f;
+  // torch.maximum splits the gradient evenly between equal arguments.
+  const float share_x = len_x > len_y ? 1.0f : (len_x == len_y ? 0.5f : 0.0f);
+  const float share_y = 1.0f - share_x;
+  const float g_x = g_m * share_x, g_y = g_m * share_y;
+  const float scale[4] = {W, W, H, H};
+  const float gl[4] = {g_x, g_y, g_x, g_y};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) grad[i] = pass[i] ? gl[i] * 2.0f * c[i] * scale[i] : 0.0f;
+}
+
+// Everything a pixel's lookup needs, shared by the forward and backward kernels.
+struct Lookup {
+  bool dir_invalid;  // cube direction that selects nothing: reads zero, no gradient
+  bool bad;          // NaN output, no gradient
+  int face;
+  float s, t;
+  int levels;        // 1 or 2 bilinear lookups (0 for nearest)
+  int level[2];
+  float level_weight[2];
+  bool lod_grad;     // the blend factor passes a gradient to the level of detail
+  float lod_raw;
+  bool mip;
+  CubeProj P;
+};
+
+__device__ __forceinline__ void lookup_setup(const DrTextureArgs& a, int64_t pixel, Lookup& K) {
+  const bool cube = a.boundary == DR_BOUNDARY_CUBE;
+  const bool mip = a.filter == DR_FILTER_MIP_NEAREST || a.filter == DR_FILTER_MIP_LINEAR;
+  K.mip = mip;
+  K.dir_invalid = false;
+  K.face = -1;
+  const float* da = nullptr;
+  float st_da[4];
+  if (cube) {
+    cube_project(a.uv + 3 * pixel, (mip && a.uv_da) ? a.uv_da + 6 * pixel : nullptr, K.P);
+    K.dir_invalid = !K.P.valid;
+    K.face = K.P.face;
+    K.s = K.P.st[0];
+    K.t = K.P.st[1];
+    if (mip && a.uv_da) {
+      for (int i = 0; i < 4; ++i) st_da[i] = K.P.st_da[i];
+      da = st_da;
+    }
+  } else {
+    K.s = a.uv[2 * pixel];
+    K.t = a.uv[2 * pixel + 1];
+    if (mip && a.uv_da) da = a.uv_da + 4 * pixel;
+  }
+  K.bad = false;
+  K.lod_grad = false;
+  K.level[0] = K.level[1] = 0;
+  K.level_weight[0] = 1.0f;
+  K.level_weight[1] = 0.0f;
+  if (!mip) {
+    K.levels = a.filter == DR_FILTER_NEAREST ? 0 : 1;
+    return;
+  }
+  float lod = 0.0f;
+  if (da) lod = lod + footprint_lod(da, a.level_height[0], a.level_width[0]);
+  if (a.bias) lod = lod + a.bias[pixel];
+  K.lod_raw = lod;
+  const int top = a.num_levels - 1;
+  K.bad = isnan(lod);
+  if (K.bad) lod = 0.0f;
+  const bool inside = lod >= 0.0f && lod <= (float)top;
+  lod = fminf(fmaxf(lod, 0.0f), (float)top);
+  const bool blend = a.filter == DR_FILTER_MIP_LINEAR;
+  const int lower = (int)floorf(lod + (blend ? 0.0f : 0.5f));
+  K.level[0] = lower;
+  if (blend) {
+    K.levels = 2;
+    K.level[1] = min(lower + 1, top);
+    const float frac = lod - (float)lower;
+    K.level_weight[0] = 1.0f - frac;
+    K.level_weight[1] = frac;
+    K.lod_grad = inside && !K.bad;
+  } else {
+    K.levels = 1;
+  }
+}
+
+__device__ __forceinline__ Bilinear level_setup(const DrTextureArgs& a, const Lookup& K, int l) {
+  const int k = K.level[l];
+  return bilinear_setup(K.s, K.t, K.face, a.level_height[k], a.level_width[k],
+                        a.level_offset[k], a.boundary);
+}
+
+// Nearest: the texel containing the coordinate (reference.py:555-573).
+__device__ __forceinline__ bool nearest_setup(const DrTextureArgs& a, const Lookup& K,
+                                              int64_t& index, bool& valid) {
+  const int h = a.level_height[0], w = a.level_width[0];
+  const Axis X = texel_axis(K.s, w, 0.0f, a.boundary);
+  const Axis Y = texel_axis(K.t, h, 0.0f, a.boundary);
+  const int boundary = a.boundary == DR_BOUNDARY_CUBE ? DR_BOUNDARY_CLAMP : a.boundary;
+  valid = tap((int)floorf(Y.x), (int)floorf(X.x), K.face, h, w, a.level_offset[0], boundary,
+              index);
+  return X.bad || Y.bad;
+}
+
+__global__ __launch_bounds__(256) void forward_kernel(DrTextureArgs a, float* out) {
+  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (pixel >= (int64_t)a.batch * a.height * a.width) return;
+  const int C = a.channels;
+  float* o = out + pixel * C;
+  Lookup K;
+  lookup_setup(a, pixel, K);
+  if (K.dir_invalid) {
+    for (int c = 0; c < C; ++c) o[c] = 0.0f;
+    return;
+  }
+  const int64_t image = pixel / ((int64_t)a.height * a.width);
+  const float* texels = a.texels + (a.tex_batch > 1 ? image * a.num_texels * C : 0);
+  const float nan = __int_as_float(0x7fc00000);
+  if (K.levels == 0) {
+    int64_t index;
+    bool valid;
+    const bool bad = nearest_setup(a, K, index, valid);
+    for (int c = 0; c < C; ++c) o[c] = bad ? nan : (valid ? texels[index * C + c] : 0.0f);
+    return;
+  }
+  Bilinear L0 = level_setup(a, K, 0);
+  bool bad = K.bad || L0.bad;
+  if (K.levels == 1) {
+    for (int c = 0; c < C; ++c) {
+      float t[4];
+      fetch4(texels, L0, C, c, t);
+      o[c] = bad ? nan : bilinear_value(L0, t);
+    }
+    return;
+  }
+  Bilinear L1 = level_setup(a, K, 1);
+  bad = bad || L1.bad;
+  const float frac = K.level_weight[1];
+  for (int c = 0; c < C; ++c) {
+    float t[4], u[4];
+    fetch4(texels, L0, C, c, t);
+    fetch4(texels, L1, C, c, u);
+    o[c] = bad ? nan : bilinear_value(L0, t) * (1.0f - frac) + bilinear_value(L1, u) * frac;
+  }
+}
+
+__device__ __forceinline__ void add_texel(float* grad, int64_t index, int C, int c, float v) {
+  if (v != 0.0f) atomic_add(grad + index * C + c, v);
+}
+
+__global__ __launch_bounds__(256) void backward_kernel(DrTextureArgs a, const float* grad_out,
+                                                       float* grad_texels, float* grad_uv,
+                                                       float* grad_uv_da, float* grad_bias) {
+  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (pixel >= (int64_t)a.batch * a.height * a.width) return;
+  const int C = a.channels;
+  const bool cube = a.boundary == DR_BOUNDARY_CUBE;
+  const int uv_n = cube ? 3 : 2, da_n = cube ? 6 : 4;
+  const float* g = grad_out + pixel * C;
+  Lookup K;
+  lookup_setup(a, pixel, K);
+  const int64_t image = pixel / ((int64_t)a.height * a.width);
+  const int64_t tex_off = a.tex_batch > 1 ? image * a.num_texels * C : 0;
+  const float* texels = a.texels + tex_off;
+  float* gtex = grad_texels ? grad_texels + tex_off : nullptr;
+
+  float g_s = 0.0f, g_t = 0.0f, g_lod = 0.0f;
+  bool live = !K.dir_invalid;
+  if (live && K.levels == 0) {
+    int64_t index;
+    bool valid;
+    const bool bad = nearest_setup(a, K, index, valid);
+    if (!bad && valid && gtex)
+      for (int c = 0; c < C; ++c) add_texel(gtex, index, C, c, g[c]);
+    live = false;  // no coordinate gradient
+  } else if (live) {
+    Bilinear L[2];
+    L[0] = level_setup(a, K, 0);
+    bool bad = K.bad || L[0].bad;
+    if (K.levels == 2) {
+      L[1] = level_setup(a, K, 1);
+      bad = bad || L[1].bad;
+    }
+    if (bad) {
+      live = false;
+    } else {
+      float g_fx[2] = {0.f, 0.f}, g_fy[2] = {0.f, 0.f};
+      for (int c = 0; c < C; ++c) {
+        const float gc = g[c];
+        float value[2] = {0.f, 0.f};
+        for (int l = 0; l < K.levels; ++l) {
+          float t[4], wgt[4], dfx, dfy;
+          fetch4(texels, L[l], C, c, t);
+          if (K.levels == 2) value[l] = bilinear_value(L[l], t);
+          bilinear_grad(L[l], t, wgt, dfx, dfy);
+          const float gl = gc * K.level_weight[l];
+          g_fx[l] += gl * dfx;
+          g_fy[l] += gl * dfy;
+          if (gtex)
+            for (int k = 0; k < 4; ++k)
+              if (L[l].valid[k]) add_texel(gtex, L[l].index[k], C, c, gl * wgt[k]);
+        }
+        if (K.levels == 2) g_lod += gc * (value[1] - value[0]);
+      }
+      for (int l = 0; l < K.levels; ++l) {
+        if (L[l].pass_x) g_s += g_fx[l] * L[l].size_x;
+        if (L[l].pass_y) g_t += g_fy[l] * L[l].size_y;
+      }
+      if (!K.lod_grad) g_lod = 0.0f;
+    }
+  }
+  // Coordinate, derivative and bias gradients (zero where nothing passes).
+  float g_da[4] = {0.f, 0.f, 0.f, 0.f};
+  const bool has_da = K.mip && a.uv_da != nullptr;
+  if (live && has_da && g_lod != 0.0f) {
+    const float* da = cube ? K.P.st_da : a.uv_da + 4 * pixel;
+    footprint_lod_grad(da, a.level_height[0], a.level_width[0], g_lod, g_da);
+  }
+  if (grad_bias) grad_bias[pixel] = live ? g_lod : 0.0f;
+  if (cube) {
+    float gdir[3] = {0.f, 0.f, 0.f}, gdir_da[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (live) cube_project_backward(K.P, g_s, g_t, has_da ? g_da : nullptr, gdir, gdir_da);
+    if (grad_uv)
+      for (int k = 0; k < 3; ++k) grad_uv[3 * pixel + k] = gdir[k];
+    if (grad_uv_da)
+      for (int k = 0; k < 6; ++k) grad_uv_da[6 * pixel + k] = gdir_da[k];
+  } else {
+    if (grad_uv) {
+      grad_uv[2 * pixel] = live ? g_s : 0.0f;
+      grad_uv[2 * pixel + 1] = live ? g_t : 0.0f;
+    }
+    if (grad_uv_da)
+      for (int k = 0; k < 4; ++k) grad_uv_da[4 * pixel + k] = live ? g_da[k] : 0.0f;
+  }
+  (void)uv_n;
+  (void)da_n;
+}
+
+// ---- mip chain --------------------------------------------------------------------------
+
+// Weight of source texel i in destination texel r along an axis of n source texels: the
+// overlap of their extents when n texels are split into ceil(n / 2) equal bins, over the bin
+// width (reference.py:449-488). Exact integers scaled by 1 / n.
+__device__ __forceinline__ float axis_weight(int r, int i, int n) {
+  if (n == 1) return (r == 0 && i == 0) ? 1.0f : 0.0f;
+  if ((n & 1) == 0) return (i >> 1) == r ? 0.5f : 0.0f;
+  const int m = (n + 1) / 2;
+  const int overlap = min((r + 1) * n, (i + 1) * m) - max(r * n, i * m);
+  return overlap > 0 ? (float)overlap / (float)n : 0.0f;
+}
+
+// First source texel and tap count of destination texel r along an axis.
+__device__ __forceinline__ void axis_taps(int r, int n, int& first, int& count) {
+  if (n == 1) { first = 0; count = 1; return; }
+  if ((n & 1) == 0) { first = 2 * r; count = 2; return; }
+  const int m = (n + 1) / 2;
+  first = (int)((int64_t)r * n / m);
+  count = min(3, n - first);
+}
+
+struct MipLevels {
+  int h[DR_MAX_LEVELS], w[DR_MAX_LEVELS];
+  int64_t off[DR_MAX_LEVELS];
+};
+
+// Level k + 1 from level k, one thread per destination texel and channel group.
+__global__ __launch_bounds__(256) void mip_down_kernel(float* texels, int C, int64_t num_texels,
+                                                       int faces, MipLevels L, int k,
+                                                       int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const int h = L.h[k], w = L.w[k], h2 = L.h[k + 1], w2 = L.w[k + 1];
+  const int c = (int)(i % C);
+  int64_t rest = i / C;
+  const int col = (int)(rest % w2);
+  rest /= w2;
+  const int row = (int)(rest % h2);
+  rest /= h2;
+  const int face = (int)(rest % faces);
+  const int64_t image = rest / faces;
+  const float* src = texels + image * num_texels * C + (L.off[k] + (int64_t)face * h * w) * C;
+  float* dst = texels + image * num_texels * C + (L.off[k + 1] + (int64_t)face * h2 * w2) * C;
+  int r0, nr, c0, nc;
+  axis_taps(row, h, r0, nr);
+  axis_taps(col, w, c0, nc);
+  float sum = 0.0f;
+  for (int ri = 0; ri < nr; ++ri) {
+    const float wr = axis_weight(row, r0 + ri, h);
+    for (int ci = 0; ci < nc; ++ci) {
+      const float wc = axis_weight(col, c0 + ci, w);
+      sum += (wr * wc) * src[((int64_t)(r0 + ri) * w + (c0 + ci)) * C + c];
+    }
+  }
+  dst[((int64_t)row * w2 + col) * C + c] = sum;
+}
+
+// Adjoint of mip_down_kernel: source texel (i, j) of level k gathers the gradient of the
+// destination texels of level k + 1 whose bins overlap it.
+__global__ __launch_bounds__(256) void mip_up_kernel(float* grad, int C, int64_t num_texels,
+                                                     int faces, MipLevels L, int k,
+                                                     int64_t count) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= count) return;
+  const int h = L.h[k], w = L.w[k], h2 = L.h[k + 1], w2 = L.w[k + 1];
+  const int c = (int)(idx % C);
+  int64_t rest = idx / C;
+  const int j = (int)(rest % w);
+  rest /= w;
+  const int i = (int)(rest % h);
+  rest /= h;
+  const int face = (int)(rest % faces);
+  const int64_t image = rest / faces;
+  float* src = grad + image * num_texels * C + (L.off[k] + (int64_t)face * h * w) * C;
+  const float* dst =
+      grad + image * num_texels * C + (L.off[k + 1] + (int64_t)face * h2 * w2) * C;
+  // Destination rows (cols) that can overlap source row i (col j).
+  const int r_mid = (h & 1) ? (int)((int64_t)i * h2 / h) : i / 2;
+  const int c_mid = (w & 1) ? (int)((int64_t)j * w2 / w) : j / 2;
+  float sum = 0.0f;
+  for (int r = max(r_mid - 1, 0); r <= min(r_mid + 1, h2 - 1); ++r) {
+    const float wr = axis_weight(r, i, h);
+    if (wr == 0.0f) continue;
+    for (int cc = max(c_mid - 1, 0); cc <= min(c_mid + 1, w2 - 1); ++cc) {
+      const float wc = axis_weight(cc, j, w);
+      if (wc == 0.0f) continue;
+      sum += (wr * wc) * dst[((int64_t)r * w2 + cc) * C + c];
+    }
+  }
+  src[((int64_t)i * w + j) * C + c] += sum;
+}
+
+bool valid_levels(int num_levels, const int32_t* h, const int32_t* w, const int64_t* off) {
+  if (num_levels < 1 || num_levels > DR_MAX_LEVELS || !h || !w || !off) return false;
+  for (int k = 0; k < num_levels; ++k)
+    if (h[k] <= 0 || w[k] <= 0 || off[k] < 0) return false;
+  for (int k = 0; k + 1 < num_levels; ++k)
+    if (h[k + 1] != (h[k] + 1) / 2 || w[k + 1] != (w[k] + 1) / 2) return false;
+  return true;
+}
+
+MipLevels copy_levels(int n, const int32_t* h, const int32_t* w, const int64_t* off) {
+  MipLevels L{};
+  for (int k = 0; k < n; ++k) {
+    L.h[k] = h[k];
+    L.w[k] = w[k];
+    L.off[k] = off[k];
+  }
+  return L;
+}
+
+bool valid_args(const DrTextureArgs* a) {
+  if (!a || !a->texels || !a->uv || a->batch < 0 || a->height <= 0 || a->width <= 0) return false;
+  if (a->channels <= 0 || a->tex_batch < 1 || a->num_levels < 1 || a->num_levels > DR_MAX_LEVELS)
+    return false;
+  if (a->filter < 0 || a->filter > 3 || a->boundary < 0 || a->boundary > 3) return false;
+  if ((a->boundary == DR_BOUNDARY_CUBE) != (a->faces == 6)) return false;
+  if (a->faces != 1 && a->faces != 6) return false;
+  for (int k = 0; k < a->num_levels; ++k)
+    if (a->level_height[k] <= 0 || a->level_width[k] <= 0) return false;
+  return true;
+}
+
+}  // namespace
+}  // namespace dr
+
+using namespace dr;
+
+extern "C" int dr_texture_forward(const DrTextureArgs* a, float* out, void* stream) {
+  if (!valid_args(a) || !out) return DR_ERR_ARGUMENT;
+  const int64_t pixels = (int64_t)a->batch * a->height * a->width;
+  if (pixels == 0) return DR_OK;
+  forward_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(*a, out);
+  return launch_status();
+}
+
+extern "C" int dr_texture_backward(const DrTextureArgs* a, const float* grad_out,
+                                   float* grad_texels, float* grad_uv, float* grad_uv_da,
+                                   float* grad_bias, void* stream) {
+  if (!valid_args(a) || !grad_out) return DR_ERR_ARGUMENT;
+  const int64_t pixels = (int64_t)a->batch * a->height * a->width;
+  if (pixels == 0) return DR_OK;
+  backward_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
+      *a, grad_out, grad_texels, grad_uv, a->uv_da ? grad_uv_da : nullptr,
+      a->bias ? grad_bias : nullptr);
+  return launch_status();
+}
+
+extern "C" int dr_mip_build(float* texels, int32_t tex_batch, int32_t channels,
+                            int64_t num_texels, int32_t faces, int32_t num_levels,
+                            const int32_t* level_height, const int32_t* level_width,
+                            const int64_t* level_offset, void* stream) {
+  if (!texels || tex_batch < 1 || channels < 1 || (faces != 1 && faces != 6) ||
+      !valid_levels(num_levels, level_height, level_width, level_offset))
+    return DR_ERR_ARGUMENT;
+  const MipLevels L = copy_levels(num_levels, level_height, level_width, level_offset);
+  for (int k = 0; k + 1 < num_levels; ++k) {
+    const int64_t count = (int64_t)tex_batch * faces * L.h[k + 1] * L.w[k + 1] * channels;
+    mip_down_kernel<<<blocks_for(count, 256), 256, 0, (hipStream_t)stream>>>(
+        texels, channels, num_texels, faces, L, k, count);
+  }
+  return launch_status();
+}
+
+extern "C" int dr_mip_build_backward(float* grad_texels, int32_t tex_batch, int32_t channels,
+                                     int64_t num_texels, int32_t faces, int32_t num_levels,
+                                     const int32_t* level_height, const int32_t* level_width,
+                                     const int64_t* level_offset, void* stream) {
+  if (!grad_texels || tex_batch < 1 || channels < 1 || (faces != 1 && faces != 6) ||
+      !valid_levels(num_levels, level_height, level_width, level_offset))
+    return DR_ERR_ARGUMENT;
+  const MipLevels L = copy_levels(num_levels, level_height, level_width, level_offset);
+  for (int k = num_levels - 2; k >= 0; --k) {
+    const int64_t count = (int64_t)tex_batch * faces * L.h[k] * L.w[k] * channels;
+    mip_up_kernel<<<blocks_for(count, 256), 256, 0, (hipStream_t)stream>>>(
+        grad_texels, channels, num_texels, faces, L, k, count);
+  }
+  return launch_status();
+}

@@ -1,0 +1,231 @@
+/*
+ * diffrast_hip.h -- C ABI of libdiffrast_hip.so, the MI355X (gfx950) kernels behind the
+ * diffrast render pipeline: rasterize, interpolate, texture and antialias, forward and
+ * backward.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t (passed as void*),
+ * enqueues its kernels on that stream and returns 0 or an error code (dr_error_string).
+ * The library allocates no device memory and keeps no mutable global state: the caller
+ * allocates every output, gradient and workspace buffer (the *_workspace_size queries give
+ * sizes) and zeroes the targets of gradient accumulation. Calls are re-entrant and ordered
+ * by their stream. All float data is float32; every array is dense (C-contiguous).
+ *
+ * Each entry point cites the interface of the reference diffrast (github.com/sennecools/
+ * diffrast) that it replaces. The reference's GPU path is Python: its backend modules
+ * (src/diffrast/backends/triton.py) are called by src/diffrast/ops.py; the functions below
+ * are what that backend module binds, through ctypes, in diffrast_amd/backends/_lib.py.
+ */
+#ifndef DIFFRAST_HIP_H
+#define DIFFRAST_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  DR_OK = 0,
+  DR_ERR_ARGUMENT = 1001,  /* a size, pointer or mode is out of range */
+  DR_ERR_CAPACITY = 1002,  /* a workspace or buffer is smaller than required */
+  DR_ERR_HIP = 1003,       /* the HIP runtime reported an error (see dr_error_string) */
+};
+
+/* Message for a code returned by any entry point (static storage). */
+const char* dr_error_string(int code);
+/* ABI version; bumped whenever a struct below changes. */
+int dr_abi_version(void);
+/* sizeof of the argument structs, in the order DrRasterGeometry, DrInterpolateArgs,
+ * DrTextureArgs, DrAntialiasArgs (which = 0..3); -1 otherwise. Lets bindings check layout. */
+int dr_struct_size(int which);
+
+/* ---------------------------------------------------------------------------------------
+ * Rasterize: visibility (nearest triangle per pixel, as a 64-bit key) and resolve
+ * (rast, rast_db and their gradient).
+ *
+ * Replaces the reference backend entry rasterize_layer(pos, tri, resolution, grad_db,
+ * previous) (src/diffrast/backends/triton.py:21-40, reference.py:45-66) and the range-mode
+ * loop of src/diffrast/ops.py:69-74 / peeling.py:80-92, which become one launch here.
+ *
+ * A key packs the depth z/w (order-preserving, -0 folded into +0) in the high 32 bits and
+ * the triangle row in the low 32 bits; UINT64_MAX means empty. Layers of a depth peel are
+ * keys strictly greater than the previous layer's key at the same pixel.
+ * ------------------------------------------------------------------------------------- */
+typedef struct DrRasterGeometry {
+  const float* pos;            /* float4 (x, y, z, w) per vertex */
+  int64_t pos_batch_stride;    /* floats between the vertex arrays of two images; 0: shared */
+  const int32_t* tri;          /* [num_tri, 3] vertex indices, already range-checked */
+  int32_t num_tri;
+  int32_t batch;               /* number of images */
+  int32_t height;
+  int32_t width;
+  const int32_t* ranges;       /* NULL (every image draws all of tri), or [batch, 2] of
+                                  (start, count) per image, on the device (range mode) */
+  const int64_t* range_prefix; /* with ranges: [batch + 1] exclusive prefix sum of counts */
+  int64_t num_instances;       /* batch * num_tri, or range_prefix[batch] */
+} DrRasterGeometry;
+
+/* Bytes of the visibility workspace for this geometry. */
+int dr_raster_workspace_size(const DrRasterGeometry* g, size_t* bytes);
+
+/* Visibility, first part: clears keys, rasterizes triangles with a small bounding box
+ * directly, and bins the others into 16x16 tiles (counts and scan). Waits for the stream and
+ * returns in counts[0..2] the number of binned triangles, tile entries and tile work chunks.
+ * prev_keys (nullable) is the previous depth layer. */
+int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                               uint64_t* keys, void* workspace, size_t workspace_bytes,
+                               uint32_t counts[3], void* stream);
+
+/* Visibility, second part: fills the per-tile lists (entries holds counts[1] uint32) and
+ * rasterizes the binned triangles tile by tile. Nothing to do when counts[1] == 0. */
+int dr_raster_visibility_finish(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                                uint64_t* keys, void* workspace, size_t workspace_bytes,
+                                uint32_t* entries, const uint32_t counts[3], void* stream);
+
+/* rast [batch, h, w, 4] = (u, v, z/w, id + 1) and rast_db [batch, h, w, 4] = (du/dx, du/dy,
+ * dv/dx, dv/dy) from keys; zeros where a key is empty. rast_db may be NULL.
+ * (reference.py:69-114; Triton resolve _triton_resolve.py:84-116) */
+int dr_resolve_forward(const DrRasterGeometry* g, const uint64_t* keys, float* rast,
+                       float* rast_db, void* stream);
+
+/* Accumulates into grad_pos (same layout as pos; batch 1 when pos is shared) the gradient
+ * of rast[..., 0:3] (grad_rast) and, if grad_rast_db is not NULL, of rast_db.
+ * (_triton_resolve.py:156-244) */
+int dr_resolve_backward(const DrRasterGeometry* g, const uint64_t* keys, const float* grad_rast,
+                        const float* grad_rast_db, float* grad_pos, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Interpolate. Replaces interpolate(attr, rast, tri, rast_db, diff_attrs)
+ * (src/diffrast/backends/triton.py:50-56, reference.py:117-146).
+ * ------------------------------------------------------------------------------------- */
+typedef struct DrInterpolateArgs {
+  const float* attr;           /* [attr_batch, num_vertices, channels] */
+  int64_t attr_batch_stride;   /* floats; 0 when shared by all images */
+  int32_t num_vertices;
+  int32_t channels;
+  const float* rast;           /* [batch, h, w, 4] */
+  const float* rast_db;        /* [batch, h, w, 4]; may be NULL when num_diff == 0 */
+  const int32_t* tri;          /* [num_tri, 3] */
+  int32_t num_tri;
+  int32_t batch;
+  int32_t height;
+  int32_t width;
+  int32_t num_diff;            /* channels with screen-space derivatives */
+  const int32_t* diff;         /* [num_diff] channel indices, on the device */
+} DrInterpolateArgs;
+
+/* out [batch, h, w, channels], out_da [batch, h, w, 2 * num_diff] (NULL if num_diff == 0). */
+int dr_interpolate_forward(const DrInterpolateArgs* a, float* out, float* out_da, void* stream);
+
+/* Gradients: grad_attr is accumulated (zeroed by the caller; layout of attr); grad_rast
+ * [batch, h, w, 4] and grad_rast_db [batch, h, w, 4] are written. Any output may be NULL;
+ * grad_out_da may be NULL (no gradient reaches out_da). */
+int dr_interpolate_backward(const DrInterpolateArgs* a, const float* grad_out,
+                            const float* grad_out_da, float* grad_attr, float* grad_rast,
+                            float* grad_rast_db, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Texture. Replaces texture(tex, uv, uv_da, filter_mode, boundary_mode, max_mip_level,
+ * mip_level_bias, mip, packed) (src/diffrast/backends/triton.py:59-79, reference.py:149-194,
+ * cube maps _cube.py:44-143) and the mip chain / packing of reference.py:405-519.
+ *
+ * Texels of every level live in one packed buffer [tex_batch, num_texels, channels]; level k
+ * starts at texel level_offset[k] and holds faces * level_height[k] * level_width[k] texels
+ * (faces = 6 for a cube map, face f at rows [f h, (f + 1) h)).
+ * ------------------------------------------------------------------------------------- */
+#define DR_MAX_LEVELS 32
+enum { DR_FILTER_NEAREST = 0, DR_FILTER_LINEAR = 1, DR_FILTER_MIP_NEAREST = 2,
+       DR_FILTER_MIP_LINEAR = 3 };
+enum { DR_BOUNDARY_WRAP = 0, DR_BOUNDARY_CLAMP = 1, DR_BOUNDARY_ZERO = 2, DR_BOUNDARY_CUBE = 3 };
+
+typedef struct DrTextureArgs {
+  const float* texels;         /* packed levels */
+  int32_t tex_batch;           /* 1 (shared) or batch */
+  int32_t channels;
+  int64_t num_texels;          /* texels per batch entry of the packed buffer */
+  int32_t num_levels;          /* levels a lookup may use (<= DR_MAX_LEVELS) */
+  int32_t faces;               /* 1, or 6 for a cube map */
+  int32_t level_height[DR_MAX_LEVELS];
+  int32_t level_width[DR_MAX_LEVELS];
+  int64_t level_offset[DR_MAX_LEVELS];
+  const float* uv;             /* [batch, h, w, 2], or 3 direction components for a cube */
+  const float* uv_da;          /* [batch, h, w, 4] (6 for a cube) or NULL */
+  const float* bias;           /* [batch, h, w] mip level bias or NULL */
+  int32_t batch;
+  int32_t height;
+  int32_t width;
+  int32_t filter;              /* DR_FILTER_* */
+  int32_t boundary;            /* DR_BOUNDARY_* */
+} DrTextureArgs;
+
+/* out [batch, h, w, channels]. */
+int dr_texture_forward(const DrTextureArgs* a, float* out, void* stream);
+
+/* grad_texels (packed layout, zeroed by the caller) is accumulated; grad_uv, grad_uv_da and
+ * grad_bias (each nullable) are written. */
+int dr_texture_backward(const DrTextureArgs* a, const float* grad_out, float* grad_texels,
+                        float* grad_uv, float* grad_uv_da, float* grad_bias, void* stream);
+
+/* Builds levels 1 .. num_levels-1 of the packed buffer in place from level 0, halving each
+ * size (rounding up) with exact area weights (reference.py:433-488). */
+int dr_mip_build(float* texels, int32_t tex_batch, int32_t channels, int64_t num_texels,
+                 int32_t faces, int32_t num_levels, const int32_t* level_height,
+                 const int32_t* level_width, const int64_t* level_offset, void* stream);
+
+/* Adjoint of dr_mip_build: adds the gradient held in levels num_levels-1 .. 1 of the packed
+ * gradient buffer down into level 0, in place. */
+int dr_mip_build_backward(float* grad_texels, int32_t tex_batch, int32_t channels,
+                          int64_t num_texels, int32_t faces, int32_t num_levels,
+                          const int32_t* level_height, const int32_t* level_width,
+                          const int64_t* level_offset, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Antialias. Replaces antialias(color, rast, pos, tri, pos_gradient_boost, neighbours)
+ * (src/diffrast/backends/triton.py:82-92, reference.py:202-265, 675-765) and the edge
+ * adjacency and silhouette classification (reference.py:768-814, topology.py:19-72).
+ * ------------------------------------------------------------------------------------- */
+
+/* Bytes of workspace for dr_edge_neighbours. */
+int dr_edge_hash_workspace_size(int32_t num_tri, size_t* bytes);
+
+/* neighbours [num_tri, 3] int32: for edge k (opposite vertex k) of each triangle, the number
+ * 3 t' + k' of the same edge in the only other triangle that uses it, or -1 when no other
+ * triangle or more than one does. Built with a GPU hash table (reference.py:768-787). */
+int dr_edge_neighbours(const int32_t* tri, int32_t num_tri, void* workspace,
+                       size_t workspace_bytes, int32_t* neighbours, void* stream);
+
+/* mask [pos_batch, num_tri] uint8, bit k set when edge k is a silhouette: unshared,
+ * non-manifold, or folded in this projection (reference.py:790-814). */
+int dr_silhouette_mask(const float* pos, int64_t pos_batch_stride, int32_t pos_batch,
+                       const int32_t* tri, int32_t num_tri, const int32_t* neighbours,
+                       uint8_t* mask, void* stream);
+
+typedef struct DrAntialiasArgs {
+  const float* color;          /* [batch, h, w, channels] */
+  int32_t channels;
+  int32_t batch;
+  int32_t height;
+  int32_t width;
+  const float* rast;           /* [batch, h, w, 4] */
+  const float* pos;            /* float4 per vertex */
+  int64_t pos_batch_stride;    /* floats; 0 when shared */
+  const int32_t* tri;
+  int32_t num_tri;
+  const uint8_t* silhouette;   /* dr_silhouette_mask output */
+  int64_t silhouette_batch_stride; /* num_tri, or 0 when pos is shared */
+  float boost;                 /* pos_gradient_boost */
+} DrAntialiasArgs;
+
+/* out [batch, h, w, channels] = color blended across silhouette edges. */
+int dr_antialias_forward(const DrAntialiasArgs* a, float* out, void* stream);
+
+/* grad_color (written, nullable) and grad_pos (accumulated, nullable; layout of pos). */
+int dr_antialias_backward(const DrAntialiasArgs* a, const float* grad_out, float* grad_color,
+                          float* grad_pos, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DIFFRAST_HIP_H */

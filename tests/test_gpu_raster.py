@@ -1,0 +1,337 @@
+"""Rasterize on the GPU against the CPU oracle: ids bit-exact, values and gradients to tolerance.
+
+The oracle (oracle/reference.py) restates the reference backend's visibility arithmetic op for
+op, so every pixel of every depth layer must pick the same triangle. Barycentrics, depth and
+rast_db must agree within 1e-5 relative (normalised by max(|value|, 1)), gradients within 1e-4.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import diffrast_amd as dr
+from diffrast_amd.backends import hip
+from helpers import mixed_mesh, random_mesh, rel_error, tiny_mesh
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+
+VALUE_TOL = 1e-5
+GRAD_TOL = 1e-4
+
+
+def gpu_layers(pos, tri, res, count, grad_db=True):
+    state, out = None, []
+    for _ in range(count):
+        rast, db, state = hip.rasterize_layer(pos.cuda(), tri.cuda(), res, grad_db, state)
+        out.append((rast.cpu(), db.cpu()))
+    return out
+
+
+def oracle_layers(pos, tri, res, count):
+    state, out = None, []
+    for _ in range(count):
+        rast, db, state = R.rasterize_layer(pos, tri, res, True, state)
+        out.append((rast, db))
+    return out
+
+
+def assert_layers_match(pos, tri, res, count=1):
+    ours = gpu_layers(pos, tri, res, count)
+    ref = oracle_layers(pos, tri, res, count)
+    for layer, ((r, d), (er, ed)) in enumerate(zip(ours, ref)):
+        assert torch.equal(r[..., 3], er[..., 3]), f"layer {layer}: ids differ at " \
+            f"{(r[..., 3] != er[..., 3]).sum().item()} pixels"
+        assert rel_error(r[..., :3], er[..., :3]) < VALUE_TOL, f"layer {layer} rast"
+        assert rel_error(d, ed) < VALUE_TOL, f"layer {layer} rast_db"
+    return ref
+
+
+def test_golden_fixtures_bit_exact_ids():
+    g = np.load(__import__("pathlib").Path(__file__).parent / "golden" / "raster.npz")
+    for name in ("random", "crossing", "clipped", "tiny"):
+        pos = torch.from_numpy(g[f"{name}/pos"])
+        tri = torch.from_numpy(g[f"{name}/tri"])
+        res = tuple(int(v) for v in g[f"{name}/res"])
+        ours = gpu_layers(pos, tri, res, 4)
+        for layer, (rast, db) in enumerate(ours):
+            expected = torch.from_numpy(g[f"{name}/rast{layer}"])
+            assert torch.equal(rast[..., 3], expected[..., 3]), (name, layer)
+            assert rel_error(rast[..., :3], expected[..., :3]) < VALUE_TOL, (name, layer)
+            if layer == 0:
+                assert rel_error(db, torch.from_numpy(g[f"{name}/db0"])) < VALUE_TOL, name
+
+
+@pytest.mark.parametrize("resolution", [(16, 16), (37, 61), (128, 96)])
+def test_random_meshes(resolution):
+    pos, tri = random_mesh(200, torch.Generator().manual_seed(0))
+    ref = assert_layers_match(pos, tri, resolution)
+    assert (ref[0][0][..., 3] > 0).float().mean() > 0.5
+
+
+def test_batch_of_views():
+    pos, tri = random_mesh(50, torch.Generator().manual_seed(1), batch=4)
+    assert_layers_match(pos, tri, (48, 64))
+
+
+def test_triangles_crossing_the_camera_plane():
+    pos, tri = random_mesh(60, torch.Generator().manual_seed(2), w_range=(-1.0, 2.0))
+    ref = assert_layers_match(pos, tri, (64, 64))
+    assert (ref[0][0][..., 3] > 0).any()
+
+
+def test_depth_clipping_and_culling():
+    pos, tri = random_mesh(100, torch.Generator().manual_seed(3), z_range=2.0, xy_range=3.0)
+    assert_layers_match(pos, tri, (64, 64))
+
+
+def test_many_overlapping_triangles_in_one_tile():
+    # More triangles per tile than one work chunk holds.
+    pos, tri = random_mesh(700, torch.Generator().manual_seed(4), xy_range=0.9)
+    assert_layers_match(pos, tri, (16, 16), count=3)
+
+
+@pytest.mark.parametrize("size", [0.03, 3e-4])
+def test_tiny_triangles(size):
+    pos, tri = tiny_mesh(3000, torch.Generator().manual_seed(6), size, batch=2)
+    assert_layers_match(pos, tri, (64, 64))
+
+
+def test_mixed_triangle_sizes():
+    pos, tri = mixed_mesh(torch.Generator().manual_seed(7))
+    assert_layers_match(pos, tri, (96, 80), count=2)
+
+
+@pytest.mark.parametrize("w_range", [(1.0, 2.0), (-1.0, 2.0)])
+def test_every_pixel_of_every_layer(w_range):
+    gen = torch.Generator().manual_seed(9)
+    xy = torch.rand(2, 900, 2, generator=gen) * 3 - 1.5
+    z = torch.rand(2, 900, 1, generator=gen) * 2.4 - 1.2
+    w = torch.rand(2, 900, 1, generator=gen) * (w_range[1] - w_range[0]) + w_range[0]
+    pos = torch.cat([xy * w, z * w, w], -1)
+    tri = torch.arange(900, dtype=torch.int32).view(300, 3)
+    for resolution in ((64, 64), (37, 61), (255, 257)):
+        ref = assert_layers_match(pos, tri, resolution, count=4)
+        assert (ref[3][0][..., 3] > 0).any()
+
+
+def test_equal_depths_resolve_in_index_order():
+    quad = [[-0.2, -0.2, 0.25, 1.0], [0.2, -0.2, 0.25, 1.0], [0.0, 0.2, 0.25, 1.0]]
+    pos = torch.tensor([quad * 3])
+    tri = torch.tensor([[6, 7, 8], [0, 1, 2], [3, 4, 5]], dtype=torch.int32)
+    layers = gpu_layers(pos, tri, (8, 8), 4)
+    covered = layers[0][0][..., 3] > 0
+    assert covered.any()
+    for (rast, _), expected in zip(layers, [1, 2, 3, 0]):
+        assert (rast[..., 3][covered] == expected).all()
+
+
+def test_negative_and_zero_depth_ordering():
+    def flat(z):
+        return [[-1.0, -1.0, z, 1.0], [3.0, -1.0, z, 1.0], [-1.0, 3.0, z, 1.0]]
+
+    pos = torch.tensor([flat(0.5) + flat(-0.0) + flat(-0.5) + flat(0.0)])
+    tri = torch.arange(12, dtype=torch.int32).view(4, 3)
+    (rast, _), = gpu_layers(pos, tri, (8, 8), 1)
+    assert (rast[..., 3] == 3).all()
+    layers = gpu_layers(pos, tri, (8, 8), 4)
+    ref = oracle_layers(pos, tri, (8, 8), 4)
+    for (r, _), (e, _) in zip(layers, ref):
+        assert torch.equal(r[..., 3], e[..., 3])
+
+
+def test_empty_and_fully_culled_meshes():
+    pos = torch.tensor([[[-0.5, -0.5, 0.0, -1.0], [0.5, -0.5, 0.0, -1.0], [0.0, 0.5, 0.0, -1.0]]])
+    tri = torch.tensor([[0, 1, 2]], dtype=torch.int32)
+    for t in (tri, tri[:0]):
+        (rast, db), = gpu_layers(pos, t, (16, 16), 1)
+        assert (rast == 0).all() and (db == 0).all()
+
+
+@pytest.mark.parametrize("value", [float("nan"), float("inf")])
+def test_non_finite_vertices_are_culled(value):
+    pos, tri = random_mesh(200, torch.Generator().manual_seed(8))
+    pos[0, ::7, 3] = value  # breaks some triangles, not all
+    ref = assert_layers_match(pos, tri, (64, 64))
+    (rast, db), = gpu_layers(pos, tri, (64, 64), 1)
+    assert torch.isfinite(rast).all() and torch.isfinite(db).all()
+    assert (ref[0][0][..., 3] > 0).any()
+
+
+def test_collinear_and_repeated_index_triangles_are_not_drawn():
+    gen = torch.Generator().manual_seed(0)
+    ends = torch.randint(-9, 10, (4000, 2, 2), generator=gen).float() / 10
+    xy = torch.cat([ends, ends.mean(1, keepdim=True)], 1).reshape(1, -1, 2)
+    w = 1 + torch.rand(1, xy.shape[1], 1, generator=gen)
+    pos = torch.cat([xy * w, torch.zeros_like(w), w], -1)
+    tri = torch.arange(pos.shape[1], dtype=torch.int32).view(-1, 3)
+    (rast, _), = gpu_layers(pos, tri, (100, 100), 1)
+    assert (rast[..., 3] == 0).all()
+    i, j = torch.randint(0, pos.shape[1], (2, 3000), generator=gen)
+    rep = torch.cat([torch.stack([i, i, j], -1), torch.stack([i, j, i], -1)]).int()
+    (rast, _), = gpu_layers(pos, rep, (100, 100), 1)
+    assert (rast[..., 3] == 0).all()
+
+
+def lattice(cols, rows, resolution, w=1.0, z=0.0):
+    """Vertices projecting exactly onto pixel centres (computed like the rasterizer's)."""
+    height, width = resolution
+    x = (cols.float() * 2 + 1) / width - 1
+    y = (rows.float() * 2 + 1) / height - 1
+    w = torch.as_tensor(w, dtype=torch.float32).expand(x.shape)
+    return torch.stack([x * w, y * w, z * w, w], -1)[None]
+
+
+def grid_triangles(nx, ny, gen):
+    idx = torch.arange((nx + 1) * (ny + 1)).view(ny + 1, nx + 1)
+    a, b, c, d = (t.flatten() for t in (idx[:-1, :-1], idx[:-1, 1:], idx[1:, 1:], idx[1:, :-1]))
+    flip = (torch.rand(nx * ny, generator=gen) < 0.5)[:, None]
+    first = torch.where(flip, torch.stack([a, b, d], -1), torch.stack([a, b, c], -1))
+    second = torch.where(flip, torch.stack([b, c, d], -1), torch.stack([a, c, d], -1))
+    tri = torch.cat([first, second])
+    order = torch.stack([torch.randperm(3, generator=gen) for _ in range(tri.shape[0])])
+    return tri.gather(1, order).int()
+
+
+@pytest.mark.parametrize("resolution", [(100, 100), (255, 255), (600, 800)])
+def test_meshes_through_pixel_centres_cover_every_pixel_once(resolution):
+    gen = torch.Generator().manual_seed(2)
+    height, width = resolution
+    cell = 20
+    nx, ny = (width + 1) // cell + 1, (height + 1) // cell + 1
+    rows, cols = torch.meshgrid(torch.arange(ny + 1) * cell - 1, torch.arange(nx + 1) * cell - 1,
+                                indexing="ij")
+    w = torch.rand(rows.numel(), generator=gen) + 0.5
+    pos = lattice(cols.flatten(), rows.flatten(), resolution, w=w)
+    tri = grid_triangles(nx, ny, gen)
+    first, second = gpu_layers(pos, tri, resolution, 2)
+    assert (first[0][..., 3] > 0).all(), "holes"
+    assert (second[0][..., 3] == 0).all(), "pixels covered twice"
+
+
+def test_quad_diagonal_goes_to_the_triangle_on_its_right():
+    for size in (8, 100, 255, 1000):
+        pos = torch.tensor([[[-1.0, -1.0, 0.0, 1.0], [1.0, -1.0, 0.0, 1.0], [1.0, 1.0, 0.0, 1.0],
+                             [-1.0, 1.0, 0.0, 1.0]]])
+        tri = torch.tensor([[0, 1, 2], [0, 2, 3]], dtype=torch.int32)
+        (rast, _), = gpu_layers(pos, tri, (size, size), 1)
+        row, col = torch.meshgrid(torch.arange(size), torch.arange(size), indexing="ij")
+        expected = torch.where(col >= row, 1.0, 2.0)
+        assert torch.equal(rast[0, ..., 3], expected)
+
+
+@pytest.mark.parametrize("size", [80001, 200003])
+def test_very_wide_images(size):
+    # Opposite quad sides on pixel-centre columns: the bounding boxes must keep them.
+    gen = torch.Generator().manual_seed(8)
+    first = torch.randint(0, size - 8, (3000,), generator=gen)
+    last = first + torch.randint(1, 4, (3000,), generator=gen)
+    along = torch.stack([first, last, last, first], -1).flatten()
+    across = torch.tensor([-2, -2, 4, 4]).repeat(3000)
+    pos = lattice(along, across, (2, size))
+    quad = torch.tensor([[0, 1, 2], [0, 2, 3]])
+    tri = (quad[None] + torch.arange(3000)[:, None, None] * 4).view(-1, 3).int()
+    edges = torch.zeros(size + 1)
+    edges.index_add_(0, first, torch.ones(3000)).index_add_(0, last, -torch.ones(3000))
+    expected = (edges.cumsum(0)[:size] > 0).expand(2, size)
+    (rast, _), = gpu_layers(pos, tri, (2, size), 1)
+    assert torch.equal(rast[0, ..., 3] > 0, expected)
+
+
+def test_range_mode_matches_per_item_oracle():
+    gen = torch.Generator().manual_seed(11)
+    pos, tri = random_mesh(120, gen, batch=1)
+    pos = pos[0]
+    ranges = torch.tensor([[0, 40], [30, 50], [100, 20], [0, 0], [60, 60]], dtype=torch.int32)
+    rast, db, _ = hip.rasterize_ranges(pos.cuda(), tri.cuda(), (40, 48), True, ranges)
+    ref, ref_db = R.rasterize_ranges(pos, tri, (40, 48), ranges)
+    assert torch.equal(rast.cpu()[..., 3], ref[..., 3])
+    assert rel_error(rast.cpu()[..., :3], ref[..., :3]) < VALUE_TOL
+    assert rel_error(db.cpu(), ref_db) < VALUE_TOL
+
+
+def test_range_mode_depth_peeling_matches_oracle():
+    gen = torch.Generator().manual_seed(12)
+    pos, tri = random_mesh(90, gen, batch=1, xy_range=0.7)
+    pos = pos[0]
+    ranges = torch.tensor([[0, 45], [45, 45], [20, 60]], dtype=torch.int32)
+    state = None
+    ref_states = [None] * 3
+    for layer in range(3):
+        rast, _, state = hip.rasterize_ranges(pos.cuda(), tri.cuda(), (32, 32), True, ranges, state)
+        for item, (start, count) in enumerate(ranges.tolist()):
+            r, _, ref_states[item] = R.rasterize_layer(pos[None], tri[start:start + count],
+                                                       (32, 32), True, ref_states[item])
+            ids = torch.where(r[..., 3] > 0, r[..., 3] + start, r[..., 3])
+            assert torch.equal(rast.cpu()[item, ..., 3], ids[0]), (layer, item)
+
+
+@pytest.mark.parametrize("grad_db", [True, False])
+@pytest.mark.parametrize("use", ["rast", "db", "both"])
+def test_gradients_match_oracle(grad_db, use):
+    pos, tri = random_mesh(80, torch.Generator().manual_seed(1), batch=2, w_range=(-1.0, 2.0))
+    gen = torch.Generator().manual_seed(0)
+    w_rast = torch.randn(2, 40, 56, 4, generator=gen)
+    w_db = torch.randn(2, 40, 56, 4, generator=gen)
+
+    def run(fn, p, device):
+        p = p.clone().to(device).requires_grad_(True)
+        rast, db = fn(p, tri.to(device), (40, 56), grad_db)
+        loss = 0
+        if use in ("rast", "both"):
+            loss = loss + (rast[..., :3] * w_rast[..., :3].to(device)).sum()
+        if use in ("db", "both") and db.requires_grad:
+            loss = loss + (db * w_db.to(device)).sum()
+        if not torch.is_tensor(loss) or not loss.requires_grad:
+            return None
+        loss.backward()
+        return p.grad.cpu()
+
+    ours = run(hip.rasterize, pos, "cuda")
+    ref = run(R.rasterize, pos, "cpu")
+    if ref is None:
+        assert ours is None
+        return
+    scale = ref.abs().max().item()
+    torch.testing.assert_close(ours, ref, atol=GRAD_TOL * scale, rtol=GRAD_TOL)
+
+
+def test_gradients_of_large_triangles_sharing_vertices():
+    pos, tri = random_mesh(6, torch.Generator().manual_seed(2), xy_range=0.9)
+    gen = torch.Generator().manual_seed(3)
+    w_rast = torch.randn(1, 256, 256, 4, generator=gen)
+    grads = []
+    for fn, device in ((hip.rasterize, "cuda"), (R.rasterize, "cpu")):
+        p = pos.clone().to(device).requires_grad_(True)
+        rast, db = fn(p, tri.to(device), (256, 256), True)
+        ((rast[..., :3] * w_rast[..., :3].to(device)).sum() + (db * w_rast.to(device)).sum()
+         ).backward()
+        grads.append(p.grad.cpu())
+    scale = grads[1].abs().max().item()
+    torch.testing.assert_close(grads[0], grads[1], atol=GRAD_TOL * scale, rtol=GRAD_TOL)
+
+
+def test_public_api_and_double_backward_guard():
+    ctx = dr.RasterizeContext("cuda")
+    pos, tri = random_mesh(20, torch.Generator().manual_seed(5))
+    pos = pos.cuda().requires_grad_(True)
+    rast, db = dr.rasterize(ctx, pos, tri.cuda(), (16, 16))
+    assert rast.shape == db.shape == (1, 16, 16, 4)
+    with pytest.raises(RuntimeError, match="no second-order gradients"):
+        torch.autograd.grad(rast[..., :3].square().sum(), pos, create_graph=True)
+
+
+def test_depth_peeler_range_mode_through_public_api():
+    ctx = dr.RasterizeContext("cuda")
+    gen = torch.Generator().manual_seed(13)
+    pos, tri = random_mesh(60, gen, batch=1, xy_range=0.6)
+    pos, tri = pos[0].cuda(), tri.cuda()
+    ranges = torch.tensor([[0, 30], [30, 30]], dtype=torch.int32)
+    with dr.DepthPeeler(ctx, pos, tri, (24, 24), ranges=ranges) as peeler:
+        first, _ = peeler.rasterize_next_layer()
+        second, _ = peeler.rasterize_next_layer()
+    both = (first[..., 3] > 0) & (second[..., 3] > 0)
+    assert both.any()
+    assert (second[..., 2][both] >= first[..., 2][both]).all()
+    with pytest.raises(RuntimeError, match="closed"):
+        peeler.rasterize_next_layer()
