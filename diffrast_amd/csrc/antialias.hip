@@ -71,14 +71,14 @@ __device__ __forceinline__ uint64_t edge_key(const int32_t* tri, int64_t e) {
   return ((uint64_t)lo << 32) | hi;
 }
 
-__global__ void hash_clear(HashTable h) {
+__global__ void edge_hash_clear(HashTable h) {
   const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i > h.mask) return;
   h.keys[i] = kEmptySlot;
   h.counts[i] = 0u;
 }
 
-__global__ __launch_bounds__(256) void hash_insert(const int32_t* tri, int64_t num_edges,
+__global__ __launch_bounds__(256) void edge_hash_insert(const int32_t* tri, int64_t num_edges,
                                                    HashTable h) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= num_edges) return;
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void hash_insert(const int32_t* tri, int64_t n
   }
 }
 
-__global__ __launch_bounds__(256) void hash_partner(const int32_t* tri, int64_t num_edges,
+__global__ __launch_bounds__(256) void edge_hash_partner(const int32_t* tri, int64_t num_edges,
                                                     HashTable h, int32_t* neighbours) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= num_edges) return;
@@ -137,7 +137,7 @@ __device__ __forceinline__ float side(const float (&line)[3], const XYW& p) {
   return v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f);
 }
 
-__global__ __launch_bounds__(256) void silhouette_kernel(const float* pos, int64_t stride,
+__global__ __launch_bounds__(256) void aa_silhouette_kernel(const float* pos, int64_t stride,
                                                          int pos_batch, const int32_t* tri,
                                                          int num_tri, const int32_t* nbr,
                                                          uint8_t* mask) {
@@ -346,7 +346,7 @@ struct Neighbour {
 };
 __constant__ Neighbour kPairs[4] = {{0, 1, true}, {1, 0, true}, {0, -1, false}, {-1, 0, false}};
 
-__global__ __launch_bounds__(256) void forward_kernel(DrAntialiasArgs a, float* out) {
+__global__ __launch_bounds__(256) void aa_fwd_kernel(DrAntialiasArgs a, float* out) {
   const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (pixel >= (int64_t)a.batch * a.height * a.width) return;
   const int C = a.channels;
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(256) void forward_kernel(DrAntialiasArgs a, float* 
   }
 }
 
-__global__ __launch_bounds__(256) void backward_kernel(DrAntialiasArgs a, const float* grad_out,
+__global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const float* grad_out,
                                                        float* grad_color, float* grad_pos) {
   const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (pixel >= (int64_t)a.batch * a.height * a.width) return;
@@ -480,9 +480,9 @@ extern "C" int dr_edge_neighbours(const int32_t* tri, int32_t num_tri, void* wor
   if (!workspace || workspace_bytes < h.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
   const int64_t edges = 3 * (int64_t)num_tri;
-  hash_clear<<<blocks_for((int64_t)h.mask + 1, 256), 256, 0, s>>>(h);
-  hash_insert<<<blocks_for(edges, 256), 256, 0, s>>>(tri, edges, h);
-  hash_partner<<<blocks_for(edges, 256), 256, 0, s>>>(tri, edges, h, neighbours);
+  edge_hash_clear<<<blocks_for((int64_t)h.mask + 1, 256), 256, 0, s>>>(h);
+  edge_hash_insert<<<blocks_for(edges, 256), 256, 0, s>>>(tri, edges, h);
+  edge_hash_partner<<<blocks_for(edges, 256), 256, 0, s>>>(tri, edges, h, neighbours);
   return launch_status();
 }
 
@@ -493,7 +493,7 @@ extern "C" int dr_silhouette_mask(const float* pos, int64_t pos_batch_stride, in
   const int64_t n = (int64_t)pos_batch * num_tri;
   if (n == 0) return DR_OK;
   if (!pos || !tri || !neighbours || !mask) return DR_ERR_ARGUMENT;
-  silhouette_kernel<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>(
+  aa_silhouette_kernel<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>(
       pos, pos_batch_stride, pos_batch, tri, num_tri, neighbours, mask);
   return launch_status();
 }
@@ -502,7 +502,7 @@ extern "C" int dr_antialias_forward(const DrAntialiasArgs* a, float* out, void* 
   if (!valid_args(a) || !out) return DR_ERR_ARGUMENT;
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0 || a->channels == 0) return DR_OK;
-  forward_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(*a, out);
+  aa_fwd_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(*a, out);
   return launch_status();
 }
 
@@ -511,7 +511,7 @@ extern "C" int dr_antialias_backward(const DrAntialiasArgs* a, const float* grad
   if (!valid_args(a) || !grad_out) return DR_ERR_ARGUMENT;
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0) return DR_OK;
-  backward_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
+  aa_bwd_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
       *a, grad_out, grad_color, grad_pos);
   return launch_status();
 }

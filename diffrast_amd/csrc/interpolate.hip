@@ -43,7 +43,7 @@ __device__ __forceinline__ Pixel load_pixel(const DrInterpolateArgs& a, int64_t 
 }
 
 template <int NC>
-__global__ __launch_bounds__(256) void forward_kernel(DrInterpolateArgs a, float* out,
+__global__ __launch_bounds__(256) void interp_fwd_kernel(DrInterpolateArgs a, float* out,
                                                       float* out_da) {
   const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (pixel >= (int64_t)a.batch * a.height * a.width) return;
@@ -77,24 +77,27 @@ __global__ __launch_bounds__(256) void forward_kernel(DrInterpolateArgs a, float
 }
 
 template <int NC>
-__global__ __launch_bounds__(256) void backward_kernel(DrInterpolateArgs a, const float* grad_out,
-                                                       const float* grad_da, float* grad_attr,
-                                                       float* grad_rast, float* grad_db) {
-  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const bool in_range = pixel < (int64_t)a.batch * a.height * a.width;
+__global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
+                                                         const float* grad_out,
+                                                         const float* grad_da, float* grad_attr,
+                                                         float* grad_rast, float* grad_db) {
+  __shared__ ScatterTable<1024, 8> table;
+  const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
+  const int64_t pixel = tp.pixel;
   const int C = NC > 0 ? NC : a.channels;
   Pixel p;
   p.valid = false;
+  p.u = p.v = 0.0f;
   float4 db = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (in_range) {
+  if (tp.inside) {
     float4 r;
     p = load_pixel(a, pixel, r);
     if (p.valid && a.num_diff > 0) db = load4(a.rast_db + 4 * pixel);
   }
-  const float* g = grad_out + (in_range ? pixel * C : 0);
-  const float* gd = (grad_da && in_range) ? grad_da + pixel * 2 * a.num_diff : nullptr;
+  const float* g = grad_out + (tp.inside ? pixel * C : 0);
+  const float* gd = (grad_da && tp.inside) ? grad_da + pixel * 2 * a.num_diff : nullptr;
 
-  if (in_range && (grad_rast || grad_db)) {
+  if (tp.inside && (grad_rast || grad_db)) {
     float gu = 0.f, gv = 0.f, g_dudx = 0.f, g_dudy = 0.f, g_dvdx = 0.f, g_dvdy = 0.f;
     if (p.valid) {
       const float* a0 = a.attr + p.rows[0];
@@ -119,54 +122,46 @@ __global__ __launch_bounds__(256) void backward_kernel(DrInterpolateArgs a, cons
     if (grad_rast) store4(grad_rast + 4 * pixel, make_float4(gu, gv, 0.f, 0.f));
     if (grad_db) store4(grad_db + 4 * pixel, make_float4(g_dudx, g_dudy, g_dvdx, g_dvdy));
   }
-  if (!grad_attr) return;
+  if (!grad_attr || C == 0) return;  // uniform over the workgroup
 
-  // Gradient of the three attribute rows, merged within the wave by (image batch, triangle).
-  const int64_t image = in_range ? pixel / ((int64_t)a.height * a.width) : 0;
-  const int64_t attr_image = a.attr_batch_stride != 0 ? image : 0;
-  const int64_t key = p.valid ? attr_image * a.num_tri + p.t : -1;
+  // Rows of the attribute table are the keys (p.rows holds their float offsets), C floats per
+  // row, 8 per pass.
+  uint32_t keys[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+    keys[k] = p.valid ? (uint32_t)(p.rows[k] / C) : ScatterTable<1024, 8>::kEmpty;
   const float w = 1.0f - p.u - p.v;
-  auto channel_grads = [&](int c, float& g0, float& g1, float& g2) {
-    const float gc = g[c];
-    g0 = gc * p.u;
-    g1 = gc * p.v;
-    g2 = gc * w;
-    if (gd) {
-      for (int k = 0; k < a.num_diff; ++k) {
-        if (a.diff[k] != c) continue;
-        const float t0 = gd[2 * k] * db.x + gd[2 * k + 1] * db.y;
-        const float t1 = gd[2 * k] * db.z + gd[2 * k + 1] * db.w;
-        g0 += t0;
-        g1 += t1;
-        g2 -= t0 + t1;
+  for (int c0 = 0; c0 < C; c0 += 8) {
+    const int n = min(8, C - c0);
+    float v0[8], v1[8], v2[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      v0[c] = v1[c] = v2[c] = 0.0f;
+      if (c >= n || !p.valid) continue;
+      const float gc = g[c0 + c];
+      v0[c] = gc * p.u;
+      v1[c] = gc * p.v;
+      v2[c] = gc * w;
+      if (gd) {
+        for (int k = 0; k < a.num_diff; ++k) {
+          if (a.diff[k] != c0 + c) continue;
+          const float t0 = gd[2 * k] * db.x + gd[2 * k + 1] * db.y;
+          const float t1 = gd[2 * k] * db.z + gd[2 * k + 1] * db.w;
+          v0[c] += t0;
+          v1[c] += t1;
+          v2[c] -= t0 + t1;
+        }
       }
     }
-  };
-  wave_grouped(
-      key, 4,
-      [&](uint64_t same, int leader) {
-        for (int c = 0; c < C; ++c) {
-          float g0 = 0.f, g1 = 0.f, g2 = 0.f;
-          if ((same >> lane_id()) & 1ull) channel_grads(c, g0, g1, g2);
-          g0 = wave_masked_sum(g0, same);
-          g1 = wave_masked_sum(g1, same);
-          g2 = wave_masked_sum(g2, same);
-          if (lane_id() == leader) {
-            if (g0 != 0.f) atomic_add(grad_attr + p.rows[0] + c, g0);
-            if (g1 != 0.f) atomic_add(grad_attr + p.rows[1] + c, g1);
-            if (g2 != 0.f) atomic_add(grad_attr + p.rows[2] + c, g2);
-          }
-        }
-      },
-      [&]() {
-        for (int c = 0; c < C; ++c) {
-          float g0, g1, g2;
-          channel_grads(c, g0, g1, g2);
-          if (g0 != 0.f) atomic_add(grad_attr + p.rows[0] + c, g0);
-          if (g1 != 0.f) atomic_add(grad_attr + p.rows[1] + c, g1);
-          if (g2 != 0.f) atomic_add(grad_attr + p.rows[2] + c, g2);
-        }
-      });
+    table.clear();
+    __syncthreads();
+    table.add_wave(keys[0], v0, n, grad_attr + c0, C);
+    table.add_wave(keys[1], v1, n, grad_attr + c0, C);
+    table.add_wave(keys[2], v2, n, grad_attr + c0, C);
+    __syncthreads();
+    table.flush(grad_attr + c0, C, n);
+    __syncthreads();
+  }
 }
 
 template <typename F>
@@ -200,7 +195,7 @@ extern "C" int dr_interpolate_forward(const DrInterpolateArgs* a, float* out, fl
   if (pixels == 0 || (a->channels == 0 && a->num_diff == 0)) return DR_OK;
   const DrInterpolateArgs args = *a;
   return dispatch_channels(args.channels, [&](auto nc) {
-    forward_kernel<decltype(nc)::value><<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
+    interp_fwd_kernel<decltype(nc)::value><<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
         args, out, args.num_diff > 0 ? out_da : nullptr);
     return launch_status();
   });
@@ -212,10 +207,13 @@ extern "C" int dr_interpolate_backward(const DrInterpolateArgs* a, const float* 
   if (!valid_args(a) || !grad_out) return DR_ERR_ARGUMENT;
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0) return DR_OK;
+  // Rows of the attribute table are 32-bit keys of the workgroup scatter table.
+  const int64_t rows = (a->attr_batch_stride != 0 ? (int64_t)a->batch : 1) * a->num_vertices;
+  if (grad_attr && rows >= 0xffffffffLL) return DR_ERR_ARGUMENT;
   const float* gda = a->num_diff > 0 ? grad_out_da : nullptr;
   return dispatch_channels(a->channels, [&](auto nc) {
-    backward_kernel<decltype(nc)::value>
-        <<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
+    interp_bwd_kernel<decltype(nc)::value>
+        <<<tile_blocks(a->batch, a->height, a->width), 256, 0, (hipStream_t)stream>>>(
             *a, grad_out, gda, grad_attr, grad_rast, a->num_diff > 0 ? grad_rast_db : nullptr);
     return launch_status();
   });

@@ -184,17 +184,17 @@ __device__ __forceinline__ void merge_key(uint64_t* keys, const uint64_t* prev, 
 
 // ---- kernels ----------------------------------------------------------------------------
 
-__global__ void fill_keys(uint64_t* keys, int64_t n) {
+__global__ void raster_fill_keys(uint64_t* keys, int64_t n) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   for (; i < n; i += (int64_t)gridDim.x * blockDim.x) keys[i] = kEmptyKey;
 }
 
-__global__ void fill_u32(uint32_t* p, int64_t n, uint32_t value) {
+__global__ void raster_fill_u32(uint32_t* p, int64_t n, uint32_t value) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   for (; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = value;
 }
 
-__global__ __launch_bounds__(256) void setup_kernel(DrRasterGeometry g, const uint64_t* prev,
+__global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g, const uint64_t* prev,
                                                     uint64_t* keys, Workspace ws) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   bool binned = false;
@@ -282,7 +282,7 @@ __device__ __forceinline__ uint2 scan_item(const uint32_t* counts, int64_t i, in
 }
 
 // Phase 1: per-block totals.
-__global__ __launch_bounds__(256) void scan_reduce(const uint32_t* counts, int64_t n,
+__global__ __launch_bounds__(256) void raster_scan_reduce(const uint32_t* counts, int64_t n,
                                                    uint2* block_sums) {
   __shared__ uint2 lds[4];
   const int64_t base = (int64_t)blockIdx.x * kScanBlock + threadIdx.x * 4;
@@ -297,7 +297,7 @@ __global__ __launch_bounds__(256) void scan_reduce(const uint32_t* counts, int64
 }
 
 // Phase 2: exclusive scan of the block totals in one block; totals go to the counters.
-__global__ __launch_bounds__(256) void scan_blocks(uint2* block_sums, int blocks,
+__global__ __launch_bounds__(256) void raster_scan_blocks(uint2* block_sums, int blocks,
                                                    uint32_t* counters) {
   __shared__ uint2 lds[4];
   __shared__ uint2 step_total;
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(256) void scan_blocks(uint2* block_sums, int blocks
 }
 
 // Phase 3: exclusive offsets per tile (and the totals at index n).
-__global__ __launch_bounds__(256) void scan_apply(const uint32_t* counts, int64_t n,
+__global__ __launch_bounds__(256) void raster_scan_apply(const uint32_t* counts, int64_t n,
                                                   const uint2* block_sums, uint32_t* offsets,
                                                   uint32_t* cursor, uint32_t* chunk_offsets) {
   __shared__ uint2 lds[4];
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(256) void scan_apply(const uint32_t* counts, int64_
   }
 }
 
-__global__ __launch_bounds__(256) void scatter_kernel(Workspace ws, uint32_t num_records,
+__global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint32_t num_records,
                                                       uint32_t* entries) {
   const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= num_records) return;
@@ -360,15 +360,39 @@ __global__ __launch_bounds__(256) void scatter_kernel(Workspace ws, uint32_t num
     for (int tx = tx0; tx <= tx1; ++tx) entries[atomicAdd(cursor + ty * ws.tiles_x + tx, 1u)] = r;
 }
 
-__global__ __launch_bounds__(256) void tile_kernel(DrRasterGeometry g, const uint64_t* prev,
-                                                   uint64_t* keys, Workspace ws,
-                                                   const uint32_t* entries) {
+// Bounding box of a triangle's candidate pixels, as in setup_kernel: [x_lo, x_hi] x [y_lo, y_hi],
+// empty (lo > hi) for a culled triangle.
+__device__ __forceinline__ void candidate_box(const DrRasterGeometry& g, const Tri& T, int& x_lo,
+                                              int& x_hi, int& y_lo, int& y_hi) {
+  x_lo = y_lo = 0;
+  x_hi = y_hi = -1;
+  const bool any_front = T.w[0] > 0.0f || T.w[1] > 0.0f || T.w[2] > 0.0f;
+  if (!finite_tri(T) || !any_front) return;
+  if (T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
+    axis_range(T.x[0] / T.w[0], T.x[1] / T.w[1], T.x[2] / T.w[2], g.width, x_lo, x_hi);
+    axis_range(T.y[0] / T.w[0], T.y[1] / T.w[1], T.y[2] / T.w[2], g.height, y_lo, y_hi);
+  } else {
+    x_hi = g.width - 1;
+    y_hi = g.height - 1;
+  }
+}
+
+// One workgroup per (tile, chunk of up to kChunk binned triangles). The tile's best keys live
+// in LDS; each wave takes one triangle at a time and sweeps only the pixels of its bounding
+// box inside the tile, lanes packed by the box width, merging hits with an LDS 64-bit min.
+// The tile's keys then go to global memory with one atomic min per pixel.
+__global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
+                                                          const uint64_t* prev, uint64_t* keys,
+                                                          Workspace ws,
+                                                          const uint32_t* entries) {
   __shared__ float sx[3][kChunk], sy[3][kChunk], sz[3][kChunk], sw[3][kChunk];
   __shared__ float s_reach_x[kChunk], s_reach_y[kChunk];
   __shared__ uint32_t s_tri[kChunk];
+  __shared__ uint32_t s_box[kChunk];  // tile-local x0 | x1 << 8 | y0 << 16 | y1 << 24
+  __shared__ unsigned long long s_key[kTile * kTile];
+  __shared__ unsigned long long s_prev[kTile * kTile];
   __shared__ int64_t s_tile;
 
-  // Tile of this work item: the last tile whose first chunk is at or before blockIdx.x.
   if (threadIdx.x == 0) {
     int64_t lo = 0, hi = ws.tiles;
     while (hi - lo > 1) {
@@ -387,9 +411,17 @@ __global__ __launch_bounds__(256) void tile_kernel(DrRasterGeometry g, const uin
   const int per_image = ws.tiles_x * ws.tiles_y;
   const int b = (int)(tile / per_image);
   const int in_image = (int)(tile - (int64_t)b * per_image);
-  const int x = (in_image % ws.tiles_x) * kTile + (threadIdx.x % kTile);
-  const int y = (in_image / ws.tiles_x) * kTile + (threadIdx.x / kTile);
+  const int tile_x0 = (in_image % ws.tiles_x) * kTile;
+  const int tile_y0 = (in_image / ws.tiles_x) * kTile;
 
+  {  // this thread's pixel of the tile: clear its key, stage the previous layer's key
+    const int x = tile_x0 + (threadIdx.x % kTile), y = tile_y0 + (threadIdx.x / kTile);
+    s_key[threadIdx.x] = kEmptyKey;
+    uint64_t floor_key = 0ull;
+    if (prev != nullptr && x < g.width && y < g.height)
+      floor_key = prev[((int64_t)b * g.height + y) * g.width + x];
+    s_prev[threadIdx.x] = floor_key;
+  }
   if ((int)threadIdx.x < n) {
     const int4 rec = ws.records[entries[first + threadIdx.x]];
     Tri T;
@@ -405,26 +437,53 @@ __global__ __launch_bounds__(256) void tile_kernel(DrRasterGeometry g, const uin
     s_reach_x[threadIdx.x] = T.reach_x;
     s_reach_y[threadIdx.x] = T.reach_y;
     s_tri[threadIdx.x] = (uint32_t)rec.y;
+    int x_lo, x_hi, y_lo, y_hi;
+    candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
+    const int bx0 = max(x_lo - tile_x0, 0), bx1 = min(x_hi - tile_x0, kTile - 1);
+    const int by0 = max(y_lo - tile_y0, 0), by1 = min(y_hi - tile_y0, kTile - 1);
+    s_box[threadIdx.x] = (bx0 > bx1 || by0 > by1)
+                             ? 0xffffffffu
+                             : (uint32_t)bx0 | ((uint32_t)bx1 << 8) | ((uint32_t)by0 << 16) |
+                                   ((uint32_t)by1 << 24);
   }
   __syncthreads();
-  if (x >= g.width || y >= g.height) return;
 
-  const int64_t pixel = ((int64_t)b * g.height + y) * g.width + x;
-  const uint64_t floor_key = prev != nullptr ? prev[pixel] : 0ull;
-  const float px = pixel_centre(x, g.width), py = pixel_centre(y, g.height);
-  uint64_t best = kEmptyKey;
-  for (int j = 0; j < n; ++j) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x / DR_WAVE;
+  for (int j = wave; j < n; j += 256 / DR_WAVE) {
+    const uint32_t box = s_box[j];
+    if (box == 0xffffffffu) continue;
+    const int bx0 = box & 0xff, bx1 = (box >> 8) & 0xff, by0 = (box >> 16) & 0xff,
+              by1 = box >> 24;
+    const int bw = bx1 - bx0 + 1;
+    // Lanes per row: the box width rounded up to a power of two (at most 16).
+    const int shift = bw <= 1 ? 0 : (bw <= 2 ? 1 : (bw <= 4 ? 2 : (bw <= 8 ? 3 : 4)));
+    const int lx = bx0 + (lane & ((1 << shift) - 1));
+    const int rows_per_step = DR_WAVE >> shift;
     const float X[3] = {sx[0][j], sx[1][j], sx[2][j]};
     const float Y[3] = {sy[0][j], sy[1][j], sy[2][j]};
     const float Z[3] = {sz[0][j], sz[1][j], sz[2][j]};
     const float Wv[3] = {sw[0][j], sw[1][j], sw[2][j]};
-    float depth;
-    if (covers(X, Y, Z, Wv, s_reach_x[j], s_reach_y[j], px, py, depth)) {
-      const uint64_t key = depth_key(depth, s_tri[j]);
-      if (key < best && (prev == nullptr || key > floor_key)) best = key;
+    const float rx = s_reach_x[j], ry = s_reach_y[j];
+    const uint32_t t = s_tri[j];
+    for (int ly = by0 + (lane >> shift); ly <= by1; ly += rows_per_step) {
+      if (lx > bx1) continue;
+      const int x = tile_x0 + lx, y = tile_y0 + ly;
+      float depth;
+      if (covers(X, Y, Z, Wv, rx, ry, pixel_centre(x, g.width), pixel_centre(y, g.height),
+                 depth)) {
+        const uint64_t key = depth_key(depth, t);
+        const int p = ly * kTile + lx;
+        if (prev == nullptr || key > s_prev[p]) atomicMin(s_key + p, (unsigned long long)key);
+      }
     }
   }
-  if (best != kEmptyKey && best < keys[pixel])
+  __syncthreads();
+  const int x = tile_x0 + (threadIdx.x % kTile), y = tile_y0 + (threadIdx.x / kTile);
+  const uint64_t best = s_key[threadIdx.x];
+  if (best == kEmptyKey || x >= g.width || y >= g.height) return;
+  const int64_t pixel = ((int64_t)b * g.height + y) * g.width + x;
+  if (best < keys[pixel])
     atomicMin((unsigned long long*)(keys + pixel), (unsigned long long)best);
 }
 
@@ -468,7 +527,7 @@ __device__ __forceinline__ void resolve_pixel(const Tri& T, float px, float py, 
   }
 }
 
-__global__ __launch_bounds__(256) void resolve_forward_kernel(DrRasterGeometry g,
+__global__ __launch_bounds__(256) void resolve_fwd_kernel(DrRasterGeometry g,
                                                               const uint64_t* keys, float* rast,
                                                               float* rast_db, float scale_x,
                                                               float scale_y) {
@@ -504,107 +563,101 @@ __device__ __forceinline__ void cross3(const float* u, const float* v, float* ou
 }
 
 // Reverse mode of resolve_pixel for the gradient of (b0, b1, depth) and, optionally, rast_db.
-// For u x v with upstream G: grad u = v x G, grad v = G x u.
-__global__ __launch_bounds__(256) void resolve_backward_kernel(
+// For u x v with upstream G: grad u = v x G, grad v = G x u. Vertex gradients (x, y, z, w)
+// gather in the workgroup's scatter table, keyed by vertex row of pos, before the atomics.
+__global__ __launch_bounds__(256) void resolve_bwd_kernel(
     DrRasterGeometry g, const uint64_t* keys, const float* grad_rast, const float* grad_db,
     float* grad_pos, float scale_x, float scale_y) {
-  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)g.batch * g.height * g.width;
-  int64_t merge_key_id = -1;
-  float vals[12];
+  using Table = ScatterTable<1024, 4>;
+  __shared__ Table table;
+  const TilePixel tp = tile_pixel(g.batch, g.height, g.width);
+  const int64_t pixel = tp.pixel;
+  float vals[3][4];
+  uint32_t rows[3] = {Table::kEmpty, Table::kEmpty, Table::kEmpty};
 #pragma unroll
-  for (int i = 0; i < 12; ++i) vals[i] = 0.0f;
-  int v[3] = {0, 0, 0};
-  int pos_b = 0;
-  if (pixel < total) {
-    const uint64_t key = keys[pixel];
-    if (key != kEmptyKey) {
-      const int t = (int)(uint32_t)key;
-      const int x = (int)(pixel % g.width);
-      const int64_t rest = pixel / g.width;
-      const int y = (int)(rest % g.height);
-      const int b = (int)(rest / g.height);
-      pos_b = g.pos_batch_stride != 0 ? b : 0;
-      Tri T;
-      load_tri(g, b, t, T, v);
-      const float px = pixel_centre(x, g.width), py = pixel_centre(y, g.height);
-      Resolved R;
-      resolve_pixel(T, px, py, R);
-      const float4 gr = load4(grad_rast + 4 * pixel);
-      float gb[3] = {gr.x, gr.y, 0.0f};
-      float gw[3] = {0.f, 0.f, 0.f}, gz[3];
-      // depth = num / den
-      const float g_num = gr.z / R.den;
-      const float g_den = -gr.z * R.depth / R.den;
+  for (int k = 0; k < 3; ++k)
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        gb[k] += g_num * T.z[k] + g_den * T.w[k];
-        gz[k] = g_num * R.b[k];
-        gw[k] = g_den * R.b[k];
-      }
-      float g_area = 0.0f;
-      float g_dex[3] = {0.f, 0.f, 0.f}, g_dey[3] = {0.f, 0.f, 0.f};
-      if (grad_db != nullptr) {
-        const float4 gd = load4(grad_db + 4 * pixel);
-        const float gx[3] = {gd.x * scale_x, gd.z * scale_x, 0.0f};
-        const float gy[3] = {gd.y * scale_y, gd.w * scale_y, 0.0f};
-        // db_dx_k = (dex_k - b_k Sx) / area, Sx = sum dex.
-        float dot_x = 0.f, dot_y = 0.f;
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-          dot_x += gx[k] * R.b[k];
-          dot_y += gy[k] * R.b[k];
-          gb[k] -= (gx[k] * R.sum_dx + gy[k] * R.sum_dy) / R.area;
-          g_area -= (gx[k] * R.db_dx[k] + gy[k] * R.db_dy[k]) / R.area;
-        }
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-          g_dex[k] = (gx[k] - dot_x) / R.area;
-          g_dey[k] = (gy[k] - dot_y) / R.area;
-        }
-      }
-      // b_k = e_k / area
-      float dot_b = 0.f;
-#pragma unroll
-      for (int k = 0; k < 3; ++k) dot_b += gb[k] * R.b[k];
-      g_area -= dot_b / R.area;
-      float ge[3];
-#pragma unroll
-      for (int k = 0; k < 3; ++k) ge[k] = gb[k] / R.area + g_area;
-      // e = a x c; dex = c x w; dey = w x a.
-      float ga[3], gc[3], tmp[3];
-      cross3(R.c, ge, ga);
-      cross3(ge, R.a, gc);
-      cross3(T.w, g_dex, tmp);  // grad c from dex = c x w
-      for (int k = 0; k < 3; ++k) gc[k] += tmp[k];
-      cross3(g_dex, R.c, tmp);  // grad w from dex
-      for (int k = 0; k < 3; ++k) gw[k] += tmp[k];
-      cross3(R.a, g_dey, tmp);  // grad w from dey = w x a
-      for (int k = 0; k < 3; ++k) gw[k] += tmp[k];
-      cross3(g_dey, T.w, tmp);  // grad a from dey
-      for (int k = 0; k < 3; ++k) ga[k] += tmp[k];
-      // a = x - px w, c = y - py w
-#pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        vals[4 * k + 0] = ga[k];
-        vals[4 * k + 1] = gc[k];
-        vals[4 * k + 2] = gz[k];
-        vals[4 * k + 3] = gw[k] - px * ga[k] - py * gc[k];
-      }
-      merge_key_id = (int64_t)pos_b * g.num_tri + t;
-    }
-  }
-  const int64_t stride = g.pos_batch_stride;
-  float* base = grad_pos + (int64_t)pos_b * stride;
-  wave_merged_scatter<12>(merge_key_id, vals, 4, [&](const float (&s)[12]) {
+    for (int c = 0; c < 4; ++c) vals[k][c] = 0.0f;
+  const uint64_t key = tp.inside ? keys[pixel] : kEmptyKey;
+  if (key != kEmptyKey) {
+    const int t = (int)(uint32_t)key;
+    const int b = tp.b;
+    Tri T;
+    int v[3];
+    load_tri(g, b, t, T, v);
+    const float px = pixel_centre(tp.x, g.width), py = pixel_centre(tp.y, g.height);
+    Resolved R;
+    resolve_pixel(T, px, py, R);
+    const float4 gr = load4(grad_rast + 4 * pixel);
+    float gb[3] = {gr.x, gr.y, 0.0f};
+    float gw[3] = {0.f, 0.f, 0.f}, gz[3];
+    // depth = num / den
+    const float g_num = gr.z / R.den;
+    const float g_den = -gr.z * R.depth / R.den;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-      float* p = base + 4 * (int64_t)v[k];
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (s[4 * k + c] != 0.0f) atomic_add(p + c, s[4 * k + c]);
+      gb[k] += g_num * T.z[k] + g_den * T.w[k];
+      gz[k] = g_num * R.b[k];
+      gw[k] = g_den * R.b[k];
     }
-  });
+    float g_area = 0.0f;
+    float g_dex[3] = {0.f, 0.f, 0.f}, g_dey[3] = {0.f, 0.f, 0.f};
+    if (grad_db != nullptr) {
+      const float4 gd = load4(grad_db + 4 * pixel);
+      const float gx[3] = {gd.x * scale_x, gd.z * scale_x, 0.0f};
+      const float gy[3] = {gd.y * scale_y, gd.w * scale_y, 0.0f};
+      // db_dx_k = (dex_k - b_k Sx) / area, Sx = sum dex.
+      float dot_x = 0.f, dot_y = 0.f;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        dot_x += gx[k] * R.b[k];
+        dot_y += gy[k] * R.b[k];
+        gb[k] -= (gx[k] * R.sum_dx + gy[k] * R.sum_dy) / R.area;
+        g_area -= (gx[k] * R.db_dx[k] + gy[k] * R.db_dy[k]) / R.area;
+      }
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        g_dex[k] = (gx[k] - dot_x) / R.area;
+        g_dey[k] = (gy[k] - dot_y) / R.area;
+      }
+    }
+    // b_k = e_k / area
+    float dot_b = 0.f;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) dot_b += gb[k] * R.b[k];
+    g_area -= dot_b / R.area;
+    float ge[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) ge[k] = gb[k] / R.area + g_area;
+    // e = a x c; dex = c x w; dey = w x a.
+    float ga[3], gc[3], tmp[3];
+    cross3(R.c, ge, ga);
+    cross3(ge, R.a, gc);
+    cross3(T.w, g_dex, tmp);  // grad c from dex = c x w
+    for (int k = 0; k < 3; ++k) gc[k] += tmp[k];
+    cross3(g_dex, R.c, tmp);  // grad w from dex
+    for (int k = 0; k < 3; ++k) gw[k] += tmp[k];
+    cross3(R.a, g_dey, tmp);  // grad w from dey = w x a
+    for (int k = 0; k < 3; ++k) gw[k] += tmp[k];
+    cross3(g_dey, T.w, tmp);  // grad a from dey
+    for (int k = 0; k < 3; ++k) ga[k] += tmp[k];
+    // a = x - px w, c = y - py w
+    const int64_t row0 = g.pos_batch_stride != 0 ? (int64_t)b * (g.pos_batch_stride / 4) : 0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      vals[k][0] = ga[k];
+      vals[k][1] = gc[k];
+      vals[k][2] = gz[k];
+      vals[k][3] = gw[k] - px * ga[k] - py * gc[k];
+      rows[k] = (uint32_t)(row0 + v[k]);
+    }
+  }
+  table.clear();
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 3; ++k) table.add_wave(rows[k], vals[k], 4, grad_pos, 4);
+  __syncthreads();
+  table.flush(grad_pos, 4, 4);
 }
 
 }  // namespace
@@ -641,15 +694,15 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   if (g->num_instances >= (int64_t)1 << 32) return DR_ERR_ARGUMENT;
   const int fill_blocks = (int)std::min<int64_t>(blocks_for(pixels, 256), 65536);
-  fill_keys<<<fill_blocks, 256, 0, s>>>(keys, pixels);
-  fill_u32<<<(int)std::min<int64_t>(blocks_for(ws.tiles + 1, 256), 65536), 256, 0, s>>>(
+  raster_fill_keys<<<fill_blocks, 256, 0, s>>>(keys, pixels);
+  raster_fill_u32<<<(int)std::min<int64_t>(blocks_for(ws.tiles + 1, 256), 65536), 256, 0, s>>>(
       ws.tile_counts, ws.tiles + 1, 0u);
-  fill_u32<<<1, 64, 0, s>>>(ws.counters, 4, 0u);
+  raster_fill_u32<<<1, 64, 0, s>>>(ws.counters, 4, 0u);
   if (g->num_instances > 0) {
-    setup_kernel<<<blocks_for(g->num_instances, 256), 256, 0, s>>>(*g, prev_keys, keys, ws);
-    scan_reduce<<<ws.scan_blocks, 256, 0, s>>>(ws.tile_counts, ws.tiles, ws.block_sums);
-    scan_blocks<<<1, 256, 0, s>>>(ws.block_sums, ws.scan_blocks, ws.counters);
-    scan_apply<<<ws.scan_blocks, 256, 0, s>>>(ws.tile_counts, ws.tiles, ws.block_sums,
+    raster_setup_kernel<<<blocks_for(g->num_instances, 256), 256, 0, s>>>(*g, prev_keys, keys, ws);
+    raster_scan_reduce<<<ws.scan_blocks, 256, 0, s>>>(ws.tile_counts, ws.tiles, ws.block_sums);
+    raster_scan_blocks<<<1, 256, 0, s>>>(ws.block_sums, ws.scan_blocks, ws.counters);
+    raster_scan_apply<<<ws.scan_blocks, 256, 0, s>>>(ws.tile_counts, ws.tiles, ws.block_sums,
                                               ws.tile_offsets, ws.tile_cursor,
                                               ws.chunk_offsets);
   }
@@ -675,8 +728,8 @@ extern "C" int dr_raster_visibility_finish(const DrRasterGeometry* g, const uint
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
-  scatter_kernel<<<blocks_for(counts[0], 256), 256, 0, s>>>(ws, counts[0], entries);
-  tile_kernel<<<counts[2], 256, 0, s>>>(*g, prev_keys, keys, ws, entries);
+  raster_bin_kernel<<<blocks_for(counts[0], 256), 256, 0, s>>>(ws, counts[0], entries);
+  raster_tile_kernel<<<counts[2], 256, 0, s>>>(*g, prev_keys, keys, ws, entries);
   return launch_status();
 }
 
@@ -693,7 +746,7 @@ extern "C" int dr_resolve_forward(const DrRasterGeometry* g, const uint64_t* key
   if (pixels == 0) return DR_OK;
   float sx, sy;
   resolve_scales(g, sx, sy);
-  resolve_forward_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
+  resolve_fwd_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
       *g, keys, rast, rast_db, sx, sy);
   return launch_status();
 }
@@ -706,7 +759,9 @@ extern "C" int dr_resolve_backward(const DrRasterGeometry* g, const uint64_t* ke
   if (pixels == 0) return DR_OK;
   float sx, sy;
   resolve_scales(g, sx, sy);
-  resolve_backward_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
+  if ((int64_t)g->batch * (g->pos_batch_stride / 4) >= 0xffffffffLL) return DR_ERR_ARGUMENT;
+  resolve_bwd_kernel<<<tile_blocks(g->batch, g->height, g->width), 256, 0,
+                       (hipStream_t)stream>>>(
       *g, keys, grad_rast, grad_rast_db, grad_pos, sx, sy);
   return launch_status();
 }

@@ -433,7 +433,7 @@ __device__ __forceinline__ bool nearest_setup(const DrTextureArgs& a, const Look
   return X.bad || Y.bad;
 }
 
-__global__ __launch_bounds__(256) void forward_kernel(DrTextureArgs a, float* out) {
+__global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* out) {
   const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (pixel >= (int64_t)a.batch * a.height * a.width) return;
   const int C = a.channels;
@@ -475,96 +475,138 @@ __global__ __launch_bounds__(256) void forward_kernel(DrTextureArgs a, float* ou
   }
 }
 
-__device__ __forceinline__ void add_texel(float* grad, int64_t index, int C, int c, float v) {
-  if (v != 0.0f) atomic_add(grad + index * C + c, v);
+// Coordinate-gradient contributions of one level: d/dfx, d/dfy summed over channels with the
+// level weight, and the level's value per channel for the blend-factor gradient.
+__device__ __forceinline__ void level_coordinate_grads(const Bilinear& L, const float* texels,
+                                                       const float* g, int C, float level_weight,
+                                                       float& g_fx, float& g_fy, float* g_value) {
+  for (int c = 0; c < C; ++c) {
+    float t[4], wgt[4], dfx, dfy;
+    fetch4(texels, L, C, c, t);
+    bilinear_grad(L, t, wgt, dfx, dfy);
+    const float gl = g[c] * level_weight;
+    g_fx += gl * dfx;
+    g_fy += gl * dfy;
+    if (g_value) *g_value += g[c] * bilinear_value(L, t);
+  }
 }
 
-__global__ __launch_bounds__(256) void backward_kernel(DrTextureArgs a, const float* grad_out,
-                                                       float* grad_texels, float* grad_uv,
-                                                       float* grad_uv_da, float* grad_bias) {
-  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (pixel >= (int64_t)a.batch * a.height * a.width) return;
+__device__ __forceinline__ void level_taps(const Bilinear& L, float level_weight,
+                                           int64_t tex_off, int64_t* index, float* weight) {
+  float t0[4] = {0.f, 0.f, 0.f, 0.f}, wgt[4], dfx, dfy;
+  bilinear_grad(L, t0, wgt, dfx, dfy);  // the weights do not depend on texel values
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    index[k] = L.valid[k] ? tex_off + L.index[k] : -1;
+    weight[k] = level_weight * wgt[k];
+  }
+}
+
+__global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const float* grad_out,
+                                                      float* grad_texels, float* grad_uv,
+                                                      float* grad_uv_da, float* grad_bias) {
+  __shared__ ScatterTable<2048, 4> table;
+  const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
+  const int64_t pixel = tp.pixel;
   const int C = a.channels;
   const bool cube = a.boundary == DR_BOUNDARY_CUBE;
-  const int uv_n = cube ? 3 : 2, da_n = cube ? 6 : 4;
-  const float* g = grad_out + pixel * C;
-  Lookup K;
-  lookup_setup(a, pixel, K);
-  const int64_t image = pixel / ((int64_t)a.height * a.width);
-  const int64_t tex_off = a.tex_batch > 1 ? image * a.num_texels * C : 0;
-  const float* texels = a.texels + tex_off;
-  float* gtex = grad_texels ? grad_texels + tex_off : nullptr;
+  const float* g = grad_out + (tp.inside ? pixel * C : 0);
+  const int64_t tex_off = a.tex_batch > 1 ? (int64_t)tp.b * a.num_texels : 0;
+  const float* texels = a.texels + tex_off * C;
 
+  Lookup K;
+  // Texel gradient targets: taps 0-3 of the first level, 4-7 of the second (-1: none).
+  int64_t tap_index[8];
+  float tap_weight[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    tap_index[k] = -1;
+    tap_weight[k] = 0.0f;
+  }
   float g_s = 0.0f, g_t = 0.0f, g_lod = 0.0f;
-  bool live = !K.dir_invalid;
+  bool live = false;
+  if (tp.inside) {
+    lookup_setup(a, pixel, K);
+    live = !K.dir_invalid;
+  }
   if (live && K.levels == 0) {
     int64_t index;
     bool valid;
     const bool bad = nearest_setup(a, K, index, valid);
-    if (!bad && valid && gtex)
-      for (int c = 0; c < C; ++c) add_texel(gtex, index, C, c, g[c]);
+    if (!bad && valid) {
+      tap_index[0] = tex_off + index;
+      tap_weight[0] = 1.0f;
+    }
     live = false;  // no coordinate gradient
   } else if (live) {
-    Bilinear L[2];
-    L[0] = level_setup(a, K, 0);
-    bool bad = K.bad || L[0].bad;
-    if (K.levels == 2) {
-      L[1] = level_setup(a, K, 1);
-      bad = bad || L[1].bad;
-    }
-    if (bad) {
+    const Bilinear L0 = level_setup(a, K, 0);
+    Bilinear L1 = L0;
+    const bool two = K.levels == 2;
+    if (two) L1 = level_setup(a, K, 1);
+    if (K.bad || L0.bad || (two && L1.bad)) {
       live = false;
     } else {
-      float g_fx[2] = {0.f, 0.f}, g_fy[2] = {0.f, 0.f};
-      for (int c = 0; c < C; ++c) {
-        const float gc = g[c];
-        float value[2] = {0.f, 0.f};
-        for (int l = 0; l < K.levels; ++l) {
-          float t[4], wgt[4], dfx, dfy;
-          fetch4(texels, L[l], C, c, t);
-          if (K.levels == 2) value[l] = bilinear_value(L[l], t);
-          bilinear_grad(L[l], t, wgt, dfx, dfy);
-          const float gl = gc * K.level_weight[l];
-          g_fx[l] += gl * dfx;
-          g_fy[l] += gl * dfy;
-          if (gtex)
-            for (int k = 0; k < 4; ++k)
-              if (L[l].valid[k]) add_texel(gtex, L[l].index[k], C, c, gl * wgt[k]);
-        }
-        if (K.levels == 2) g_lod += gc * (value[1] - value[0]);
+      float fx0 = 0.f, fy0 = 0.f, fx1 = 0.f, fy1 = 0.f, v0 = 0.f, v1 = 0.f;
+      level_coordinate_grads(L0, texels, g, C, K.level_weight[0], fx0, fy0, two ? &v0 : nullptr);
+      level_taps(L0, K.level_weight[0], tex_off, tap_index, tap_weight);
+      if (L0.pass_x) g_s += fx0 * L0.size_x;
+      if (L0.pass_y) g_t += fy0 * L0.size_y;
+      if (two) {
+        level_coordinate_grads(L1, texels, g, C, K.level_weight[1], fx1, fy1, &v1);
+        level_taps(L1, K.level_weight[1], tex_off, tap_index + 4, tap_weight + 4);
+        if (L1.pass_x) g_s += fx1 * L1.size_x;
+        if (L1.pass_y) g_t += fy1 * L1.size_y;
+        g_lod = K.lod_grad ? v1 - v0 : 0.0f;
       }
-      for (int l = 0; l < K.levels; ++l) {
-        if (L[l].pass_x) g_s += g_fx[l] * L[l].size_x;
-        if (L[l].pass_y) g_t += g_fy[l] * L[l].size_y;
-      }
-      if (!K.lod_grad) g_lod = 0.0f;
     }
   }
-  // Coordinate, derivative and bias gradients (zero where nothing passes).
-  float g_da[4] = {0.f, 0.f, 0.f, 0.f};
-  const bool has_da = K.mip && a.uv_da != nullptr;
-  if (live && has_da && g_lod != 0.0f) {
-    const float* da = cube ? K.P.st_da : a.uv_da + 4 * pixel;
-    footprint_lod_grad(da, a.level_height[0], a.level_width[0], g_lod, g_da);
-  }
-  if (grad_bias) grad_bias[pixel] = live ? g_lod : 0.0f;
-  if (cube) {
-    float gdir[3] = {0.f, 0.f, 0.f}, gdir_da[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (live) cube_project_backward(K.P, g_s, g_t, has_da ? g_da : nullptr, gdir, gdir_da);
-    if (grad_uv)
-      for (int k = 0; k < 3; ++k) grad_uv[3 * pixel + k] = gdir[k];
-    if (grad_uv_da)
-      for (int k = 0; k < 6; ++k) grad_uv_da[6 * pixel + k] = gdir_da[k];
-  } else {
-    if (grad_uv) {
-      grad_uv[2 * pixel] = live ? g_s : 0.0f;
-      grad_uv[2 * pixel + 1] = live ? g_t : 0.0f;
+
+  if (tp.inside) {
+    float g_da[4] = {0.f, 0.f, 0.f, 0.f};
+    const bool has_da = K.mip && a.uv_da != nullptr;
+    if (live && has_da && g_lod != 0.0f) {
+      const float* da = cube ? K.P.st_da : a.uv_da + 4 * pixel;
+      footprint_lod_grad(da, a.level_height[0], a.level_width[0], g_lod, g_da);
     }
-    if (grad_uv_da)
-      for (int k = 0; k < 4; ++k) grad_uv_da[4 * pixel + k] = live ? g_da[k] : 0.0f;
+    if (grad_bias) grad_bias[pixel] = live ? g_lod : 0.0f;
+    if (cube) {
+      float gdir[3] = {0.f, 0.f, 0.f}, gdir_da[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (live) cube_project_backward(K.P, g_s, g_t, has_da ? g_da : nullptr, gdir, gdir_da);
+      if (grad_uv)
+        for (int k = 0; k < 3; ++k) grad_uv[3 * pixel + k] = gdir[k];
+      if (grad_uv_da)
+        for (int k = 0; k < 6; ++k) grad_uv_da[6 * pixel + k] = gdir_da[k];
+    } else {
+      if (grad_uv) {
+        grad_uv[2 * pixel] = live ? g_s : 0.0f;
+        grad_uv[2 * pixel + 1] = live ? g_t : 0.0f;
+      }
+      if (grad_uv_da)
+        for (int k = 0; k < 4; ++k) grad_uv_da[4 * pixel + k] = live ? g_da[k] : 0.0f;
+    }
   }
-  (void)uv_n;
-  (void)da_n;
+  if (grad_texels == nullptr) return;  // uniform over the workgroup
+
+  // Texel gradients, four channels per pass through the workgroup's table.
+  using Table = ScatterTable<2048, 4>;
+  for (int c0 = 0; c0 < C; c0 += 4) {
+    const int n = min(4, C - c0);
+    table.clear();
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      uint32_t key = Table::kEmpty;
+      if (tap_index[k] >= 0) {
+        key = (uint32_t)tap_index[k];
+        for (int c = 0; c < n; ++c) v[c] = g[c0 + c] * tap_weight[k];
+      }
+      table.add_wave(key, v, n, grad_texels + c0, C);
+    }
+    __syncthreads();
+    table.flush(grad_texels + c0, C, n);
+    __syncthreads();
+  }
 }
 
 // ---- mip chain --------------------------------------------------------------------------
@@ -594,8 +636,8 @@ struct MipLevels {
   int64_t off[DR_MAX_LEVELS];
 };
 
-// Level k + 1 from level k, one thread per destination texel and channel group.
-__global__ __launch_bounds__(256) void mip_down_kernel(float* texels, int C, int64_t num_texels,
+// Level k + 1 from level k, one thread per destination texel and channel.
+__global__ __launch_bounds__(256) void mip_down(float* texels, int C, int64_t num_texels,
                                                        int faces, MipLevels L, int k,
                                                        int64_t count) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -625,9 +667,9 @@ __global__ __launch_bounds__(256) void mip_down_kernel(float* texels, int C, int
   dst[((int64_t)row * w2 + col) * C + c] = sum;
 }
 
-// Adjoint of mip_down_kernel: source texel (i, j) of level k gathers the gradient of the
+// Adjoint of mip_down: source texel (i, j) of level k gathers the gradient of the
 // destination texels of level k + 1 whose bins overlap it.
-__global__ __launch_bounds__(256) void mip_up_kernel(float* grad, int C, int64_t num_texels,
+__global__ __launch_bounds__(256) void mip_up(float* grad, int C, int64_t num_texels,
                                                      int faces, MipLevels L, int k,
                                                      int64_t count) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -700,7 +742,7 @@ extern "C" int dr_texture_forward(const DrTextureArgs* a, float* out, void* stre
   if (!valid_args(a) || !out) return DR_ERR_ARGUMENT;
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0) return DR_OK;
-  forward_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(*a, out);
+  tex_fwd_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(*a, out);
   return launch_status();
 }
 
@@ -710,7 +752,8 @@ extern "C" int dr_texture_backward(const DrTextureArgs* a, const float* grad_out
   if (!valid_args(a) || !grad_out) return DR_ERR_ARGUMENT;
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0) return DR_OK;
-  backward_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
+  if ((int64_t)a->tex_batch * a->num_texels >= 0xffffffffLL) return DR_ERR_ARGUMENT;
+  tex_bwd_kernel<<<tile_blocks(a->batch, a->height, a->width), 256, 0, (hipStream_t)stream>>>(
       *a, grad_out, grad_texels, grad_uv, a->uv_da ? grad_uv_da : nullptr,
       a->bias ? grad_bias : nullptr);
   return launch_status();
@@ -726,7 +769,7 @@ extern "C" int dr_mip_build(float* texels, int32_t tex_batch, int32_t channels,
   const MipLevels L = copy_levels(num_levels, level_height, level_width, level_offset);
   for (int k = 0; k + 1 < num_levels; ++k) {
     const int64_t count = (int64_t)tex_batch * faces * L.h[k + 1] * L.w[k + 1] * channels;
-    mip_down_kernel<<<blocks_for(count, 256), 256, 0, (hipStream_t)stream>>>(
+    mip_down<<<blocks_for(count, 256), 256, 0, (hipStream_t)stream>>>(
         texels, channels, num_texels, faces, L, k, count);
   }
   return launch_status();
@@ -742,7 +785,7 @@ extern "C" int dr_mip_build_backward(float* grad_texels, int32_t tex_batch, int3
   const MipLevels L = copy_levels(num_levels, level_height, level_width, level_offset);
   for (int k = num_levels - 2; k >= 0; --k) {
     const int64_t count = (int64_t)tex_batch * faces * L.h[k] * L.w[k] * channels;
-    mip_up_kernel<<<blocks_for(count, 256), 256, 0, (hipStream_t)stream>>>(
+    mip_up<<<blocks_for(count, 256), 256, 0, (hipStream_t)stream>>>(
         grad_texels, channels, num_texels, faces, L, k, count);
   }
   return launch_status();
