@@ -467,30 +467,37 @@ def _aa_args(color, rast, pos, tri, mask, boost):
 
 
 class _Antialias(torch.autograd.Function):
-    """(reference: _triton_antialias.py:271-320, reference.py:202-265)"""
+    """(reference: _triton_antialias.py:271-320, reference.py:202-265)
+
+    The forward pass keeps the per-pixel pair records (crossing and owner bits) for the
+    backward pass, which then needs no crossing search of its own."""
 
     @staticmethod
     def forward(ctx, color, rast, pos, tri, mask, boost):
         color, rast, pos, tri = (t.contiguous() for t in (color, rast, pos, tri))
         out = torch.empty_like(color)
         args = _aa_args(color, rast, pos, tri, mask, boost)
-        call("dr_antialias_forward", ref(args), ptr(out), _stream(color))
+        size = ctypes.c_size_t()
+        call("dr_antialias_workspace_size", ref(args), ctypes.byref(size))
+        pairs = torch.empty(max(size.value, 1), dtype=torch.uint8, device=color.device)
+        call("dr_antialias_forward", ref(args), ptr(pairs), size.value, ptr(out),
+             _stream(color))
         ctx.boost = boost
-        ctx.save_for_backward(_saveable(color), _saveable(rast), _saveable(pos), tri, mask)
+        ctx.save_for_backward(_saveable(color), _saveable(rast), _saveable(pos), tri, mask, pairs)
         return out
 
     @staticmethod
     @first_order("antialias")
     def backward(ctx, grad_out):
-        color, rast, pos, tri, mask = ctx.saved_tensors
+        color, rast, pos, tri, mask, pairs = ctx.saved_tensors
         need_color, _, need_pos = ctx.needs_input_grad[:3]
         grad_color = torch.empty_like(color) if need_color else None
         grad_pos = torch.zeros_like(pos) if need_pos else None
         if grad_color is None and grad_pos is None:
             return None, None, None, None, None, None
         args = _aa_args(color, rast, pos, tri, mask, ctx.boost)
-        call("dr_antialias_backward", ref(args), ptr(grad_out.contiguous()), ptr(grad_color),
-             ptr(grad_pos), _stream(color))
+        call("dr_antialias_backward", ref(args), ptr(pairs), pairs.numel(),
+             ptr(grad_out.contiguous()), ptr(grad_color), ptr(grad_pos), _stream(color))
         return grad_color, None, grad_pos, None, None, None
 
 

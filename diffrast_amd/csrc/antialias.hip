@@ -12,10 +12,12 @@
 // adjacent pixels showing different triangles, each pixel's triangle is tested at the other
 // centre; the crossing t of its exit edge is found by linear interpolation of the edge
 // functions, the nearer triangle owns the edge, and the pixel on t's side takes |t - 0.5| of
-// the other's colour. The forward kernel is a gather: every pixel evaluates the (at most four)
-// pairs it belongs to and writes its own output, so no atomics are needed. The backward kernel
-// gathers the colour gradient the same way and scatters the position gradient of each active
-// pair (two vertices, x, y and w) with atomics from the pair's first pixel.
+// the other's colour. aa_pairs_kernel evaluates every pair once (each pixel its right and
+// lower pair) into a compact record -- t and (active, owner, edge) bits -- that the rest
+// reuses: aa_blend_kernel gathers a pixel's four pairs into its output, and aa_bwd_kernel
+// gathers the colour gradient the same way and sends the position gradient of each active
+// pair (two vertices; x, y and w) through the workgroup's scatter table. No pass needs a
+// colour atomic.
 #include "common.h"
 
 namespace dr {
@@ -138,28 +140,29 @@ __device__ __forceinline__ float side(const float (&line)[3], const XYW& p) {
 }
 
 __global__ __launch_bounds__(256) void aa_silhouette_kernel(const float* pos, int64_t stride,
-                                                         int pos_batch, const int32_t* tri,
-                                                         int num_tri, const int32_t* nbr,
-                                                         uint8_t* mask) {
+                                                            int pos_batch, const int32_t* tri,
+                                                            int num_tri, const int32_t* nbr,
+                                                            uint8_t* mask) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (int64_t)pos_batch * num_tri) return;
   const int b = (int)(i / num_tri);
   const int t = (int)(i - (int64_t)b * num_tri);
   const float* P = pos + (int64_t)b * stride;
   const int v[3] = {tri[3 * t], tri[3 * t + 1], tri[3 * t + 2]};
+  const int partner[3] = {nbr[3 * t], nbr[3 * t + 1], nbr[3 * t + 2]};
+  const XYW p[3] = {load_xyw(P, v[0]), load_xyw(P, v[1]), load_xyw(P, v[2])};
   uint8_t bits = 0;
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
-    const int partner = nbr[3 * t + k];
-    if (partner < 0) {
+    if (partner[k] < 0) {
       bits |= (uint8_t)(1u << k);
       continue;
     }
-    const XYW s = load_xyw(P, v[(k + 1) % 3]), e = load_xyw(P, v[(k + 2) % 3]);
+    const XYW& s = p[(k + 1) % 3];
+    const XYW& e = p[(k + 2) % 3];
     const float line[3] = {s.y * e.w - s.w * e.y, s.w * e.x - s.x * e.w, s.x * e.y - s.y * e.x};
-    const XYW mine = load_xyw(P, v[k]);
-    const XYW theirs = load_xyw(P, tri[partner]);  // vertex opposite the partner edge
-    if (side(line, mine) * side(line, theirs) > 0.0f) bits |= (uint8_t)(1u << k);
+    const XYW theirs = load_xyw(P, tri[partner[k]]);  // vertex opposite the partner edge
+    if (side(line, p[k]) * side(line, theirs) > 0.0f) bits |= (uint8_t)(1u << k);
   }
   mask[i] = bits;
 }
@@ -264,10 +267,6 @@ __device__ __forceinline__ void crossing_grad(const Triangle& T, int edge, float
   for (int k = 0; k < 6; ++k) g[k] = dt_des * ds[k] + dt_ded * dd[k];
 }
 
-struct AAContext {
-  const DrAntialiasArgs* a;
-};
-
 __device__ __forceinline__ int pixel_tri(const DrAntialiasArgs& a, int64_t pixel, float& depth) {
   const float4 r = load4(a.rast + 4 * pixel);
   depth = r.z;
@@ -289,168 +288,225 @@ __device__ __forceinline__ void load_triangle(const DrAntialiasArgs& a, int b, i
   }
 }
 
-struct Pair {
-  bool active;
-  bool use_p;      // the first pixel's triangle owns the edge (else the second's)
-  float t;         // crossing from the first pixel, in [0, 1]
-  int edge;
-  Triangle T;      // owner triangle
-  float sx, sy, dx, dy;  // owner's source and destination centres
-};
+// Pair record bits: the pair is active, the first pixel's triangle owns the edge, edge index.
+constexpr uint8_t kActive = 0x8, kOwnerFirst = 0x4;
 
-// Evaluate the pair (p, q), q = p + (d_row, d_col); ids and depths already loaded.
-__device__ __forceinline__ Pair eval_pair(const DrAntialiasArgs& a, int b, int row, int col,
-                                          int d_row, int d_col, int id_p, int id_q,
-                                          float depth_p, float depth_q) {
-  Pair pr;
-  pr.active = false;
-  if (id_p == id_q) return pr;
+// The pair (p, q), q = p + (d_row, d_col), as in reference.py:238-258: crossing t from p and
+// the record bits. ids and depths are already loaded.
+__device__ __forceinline__ uint8_t eval_pair(const DrAntialiasArgs& a, int b, int row, int col,
+                                             int d_row, int d_col, int id_p, int id_q,
+                                             float depth_p, float depth_q, float& t) {
+  t = 0.0f;
+  if (id_p == id_q) return 0;
+  const uint8_t* sil = a.silhouette + (int64_t)b * a.silhouette_batch_stride;
+  const uint8_t sil_p = id_p >= 0 ? sil[id_p] : 0, sil_q = id_q >= 0 ? sil[id_q] : 0;
+  if (sil_p == 0 && sil_q == 0) return 0;
   const bool horizontal = d_col == 1;
   const float px = pixel_centre(col, a.width), py = pixel_centre(row, a.height);
   const float qx = pixel_centre(col + d_col, a.width), qy = pixel_centre(row + d_row, a.height);
-  const uint8_t* sil = a.silhouette + (int64_t)b * a.silhouette_batch_stride;
   Crossing from_p{false, 0.f, 0}, from_q{false, 0.f, 0};
-  Triangle Tp, Tq;
-  if (id_p >= 0 && sil[id_p] != 0) {
-    load_triangle(a, b, id_p, Tp);
-    from_p = crossing(Tp, sil[id_p], horizontal, a.width, a.height, px, py, qx, qy);
+  if (sil_p != 0) {
+    Triangle T;
+    load_triangle(a, b, id_p, T);
+    from_p = crossing(T, sil_p, horizontal, a.width, a.height, px, py, qx, qy);
   }
-  if (id_q >= 0 && sil[id_q] != 0) {
-    load_triangle(a, b, id_q, Tq);
-    from_q = crossing(Tq, sil[id_q], horizontal, a.width, a.height, qx, qy, px, py);
+  if (sil_q != 0) {
+    Triangle T;
+    load_triangle(a, b, id_q, T);
+    from_q = crossing(T, sil_q, horizontal, a.width, a.height, qx, qy, px, py);
   }
   const bool use_p = from_p.found && (!from_q.found || depth_p <= depth_q);
   const bool use_q = from_q.found && !use_p;
-  if (!use_p && !use_q) return pr;
-  pr.active = true;
-  pr.use_p = use_p;
-  if (use_p) {
-    pr.t = from_p.t;
-    pr.edge = from_p.edge;
-    pr.T = Tp;
-    pr.sx = px; pr.sy = py; pr.dx = qx; pr.dy = qy;
-  } else {
-    pr.t = 1.0f - from_q.t;
-    pr.edge = from_q.edge;
-    pr.T = Tq;
-    pr.sx = qx; pr.sy = qy; pr.dx = px; pr.dy = py;
-  }
-  return pr;
+  if (!use_p && !use_q) return 0;
+  t = use_p ? from_p.t : 1.0f - from_q.t;
+  return (uint8_t)(kActive | (use_p ? kOwnerFirst : 0) | (use_p ? from_p.edge : from_q.edge));
 }
 
-// The four pairs of a pixel: as first pixel with its right and lower neighbours, and as
-// second pixel with its left and upper neighbours.
-struct Neighbour {
-  int d_row, d_col;
-  bool first;
+// Every pixel evaluates the pairs it forms with its right and lower neighbours, once.
+__global__ __launch_bounds__(256) void aa_pairs_kernel(DrAntialiasArgs a, float2* pair_t,
+                                                       uchar2* pair_bits) {
+  const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
+  if (!tp.inside) return;
+  float depth;
+  const int id = pixel_tri(a, tp.pixel, depth);
+  float t_right = 0.f, t_down = 0.f;
+  uint8_t right = 0, down = 0;
+  if (tp.x + 1 < a.width) {
+    float d2;
+    const int id2 = pixel_tri(a, tp.pixel + 1, d2);
+    right = eval_pair(a, tp.b, tp.y, tp.x, 0, 1, id, id2, depth, d2, t_right);
+  }
+  if (tp.y + 1 < a.height) {
+    float d2;
+    const int id2 = pixel_tri(a, tp.pixel + a.width, d2);
+    down = eval_pair(a, tp.b, tp.y, tp.x, 1, 0, id, id2, depth, d2, t_down);
+  }
+  pair_t[tp.pixel] = make_float2(t_right, t_down);
+  pair_bits[tp.pixel] = make_uchar2(right, down);
+}
+
+// The four pairs of a pixel as (active, t, other pixel, this pixel is the first).
+struct PixelPairs {
+  bool active[4];
+  float t[4];
+  int64_t other[4];
+  bool first[4];
 };
-__constant__ Neighbour kPairs[4] = {{0, 1, true}, {1, 0, true}, {0, -1, false}, {-1, 0, false}};
 
-__global__ __launch_bounds__(256) void aa_fwd_kernel(DrAntialiasArgs a, float* out) {
-  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (pixel >= (int64_t)a.batch * a.height * a.width) return;
+__device__ __forceinline__ PixelPairs pixel_pairs(const DrAntialiasArgs& a, const TilePixel& tp,
+                                                  const float2* pair_t,
+                                                  const uchar2* pair_bits) {
+  PixelPairs P;
+  const float2 own_t = pair_t[tp.pixel];
+  const uchar2 own_b = pair_bits[tp.pixel];
+  P.active[0] = own_b.x & kActive;
+  P.t[0] = own_t.x;
+  P.other[0] = tp.pixel + 1;
+  P.first[0] = true;
+  P.active[1] = own_b.y & kActive;
+  P.t[1] = own_t.y;
+  P.other[1] = tp.pixel + a.width;
+  P.first[1] = true;
+  P.active[2] = false;
+  P.active[3] = false;
+  if (tp.x > 0) {
+    P.active[2] = pair_bits[tp.pixel - 1].x & kActive;
+    P.t[2] = pair_t[tp.pixel - 1].x;
+  }
+  P.other[2] = tp.pixel - 1;
+  P.first[2] = false;
+  if (tp.y > 0) {
+    P.active[3] = pair_bits[tp.pixel - a.width].y & kActive;
+    P.t[3] = pair_t[tp.pixel - a.width].y;
+  }
+  P.other[3] = tp.pixel - a.width;
+  P.first[3] = false;
+  return P;
+}
+
+// out = colour + |t - 0.5| of the neighbour's colour on the side of each crossing
+// (reference.py:253-264). A pixel takes (0.5 - t) of its pair partner when it is the first
+// pixel and t < 0.5, and (t - 0.5) when it is the second and t >= 0.5.
+__global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const float2* pair_t,
+                                                       const uchar2* pair_bits, float* out) {
+  const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
+  if (!tp.inside) return;
   const int C = a.channels;
-  const int col = (int)(pixel % a.width);
-  const int64_t rest = pixel / a.width;
-  const int row = (int)(rest % a.height);
-  const int b = (int)(rest / a.height);
-  const float* color = a.color + pixel * C;
-  float* o = out + pixel * C;
-  for (int c = 0; c < C; ++c) o[c] = color[c];
-  float depth;
-  const int id = pixel_tri(a, pixel, depth);
+  const PixelPairs P = pixel_pairs(a, tp, pair_t, pair_bits);
+  float weight[4];
+  bool any = false;
+#pragma unroll
   for (int n = 0; n < 4; ++n) {
-    const Neighbour nb = kPairs[n];
-    const int r2 = row + nb.d_row, c2 = col + nb.d_col;
-    if (r2 < 0 || r2 >= a.height || c2 < 0 || c2 >= a.width) continue;
-    const int64_t other = pixel + (int64_t)nb.d_row * a.width + nb.d_col;
-    float depth2;
-    const int id2 = pixel_tri(a, other, depth2);
-    if (id2 == id) continue;
-    Pair pr;
-    if (nb.first)
-      pr = eval_pair(a, b, row, col, nb.d_row, nb.d_col, id, id2, depth, depth2);
-    else
-      pr = eval_pair(a, b, r2, c2, -nb.d_row, -nb.d_col, id2, id, depth2, depth);
-    if (!pr.active) continue;
-    const float* color2 = a.color + other * C;
-    if (nb.first && pr.t < 0.5f) {
-      for (int c = 0; c < C; ++c) o[c] += (0.5f - pr.t) * (color2[c] - color[c]);
-    } else if (!nb.first && pr.t >= 0.5f) {
-      for (int c = 0; c < C; ++c) o[c] += (pr.t - 0.5f) * (color2[c] - color[c]);
+    const float t = P.t[n];
+    const bool takes = P.active[n] && (P.first[n] ? t < 0.5f : t >= 0.5f);
+    weight[n] = takes ? (P.first[n] ? 0.5f - t : t - 0.5f) : 0.0f;
+    any = any || takes;
+  }
+  const float* color = a.color + tp.pixel * C;
+  float* o = out + tp.pixel * C;
+  for (int c = 0; c < C; ++c) {
+    const float own = color[c];
+    float v = own;
+    if (any) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+        if (weight[n] != 0.0f) v += weight[n] * (a.color[P.other[n] * C + c] - own);
     }
+    o[c] = v;
   }
 }
 
-__global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const float* grad_out,
-                                                       float* grad_color, float* grad_pos) {
-  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (pixel >= (int64_t)a.batch * a.height * a.width) return;
+// Colour gradient (a gather over the same pairs) and position gradient of each active pair,
+// written by its first pixel through the workgroup's scatter table (rows of pos: x, y, z, w).
+__global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const float2* pair_t,
+                                                     const uchar2* pair_bits,
+                                                     const float* grad_out, float* grad_color,
+                                                     float* grad_pos) {
+  using Table = ScatterTable<1024, 4>;
+  __shared__ Table table;
+  const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   const int C = a.channels;
-  const int col = (int)(pixel % a.width);
-  const int64_t rest = pixel / a.width;
-  const int row = (int)(rest % a.height);
-  const int b = (int)(rest / a.height);
-  const float* g = grad_out + pixel * C;
-  float* gc = grad_color ? grad_color + pixel * C : nullptr;
-  if (gc)
-    for (int c = 0; c < C; ++c) gc[c] = g[c];
-  float depth;
-  const int id = pixel_tri(a, pixel, depth);
-  const int pos_b = a.pos_batch_stride != 0 ? b : 0;
-  for (int n = 0; n < 4; ++n) {
-    const Neighbour nb = kPairs[n];
-    const int r2 = row + nb.d_row, c2 = col + nb.d_col;
-    if (r2 < 0 || r2 >= a.height || c2 < 0 || c2 >= a.width) continue;
-    const int64_t other = pixel + (int64_t)nb.d_row * a.width + nb.d_col;
-    float depth2;
-    const int id2 = pixel_tri(a, other, depth2);
-    if (id2 == id) continue;
-    Pair pr;
-    if (nb.first)
-      pr = eval_pair(a, b, row, col, nb.d_row, nb.d_col, id, id2, depth, depth2);
-    else
-      pr = eval_pair(a, b, r2, c2, -nb.d_row, -nb.d_col, id2, id, depth2, depth);
-    if (!pr.active) continue;
-    const float* g2 = grad_out + other * C;
-    // Pair (P, Q) with P the first pixel. delta_P = (0.5 - t)(c_Q - c_P) when t < 0.5,
-    // delta_Q = (t - 0.5)(c_P - c_Q) otherwise.
-    const bool low = pr.t < 0.5f;
-    if (gc) {
-      if (nb.first) {
-        if (low) for (int c = 0; c < C; ++c) gc[c] -= (0.5f - pr.t) * g[c];
-        else for (int c = 0; c < C; ++c) gc[c] += (pr.t - 0.5f) * g2[c];
-      } else {
-        if (low) for (int c = 0; c < C; ++c) gc[c] += (0.5f - pr.t) * g2[c];
-        else for (int c = 0; c < C; ++c) gc[c] -= (pr.t - 0.5f) * g[c];
+  uint32_t rows[4] = {Table::kEmpty, Table::kEmpty, Table::kEmpty, Table::kEmpty};
+  float vals[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) vals[k][c] = 0.0f;
+  if (tp.inside) {
+    const PixelPairs P = pixel_pairs(a, tp, pair_t, pair_bits);
+    const float* g = grad_out + tp.pixel * C;
+    if (grad_color) {
+      float* gc = grad_color + tp.pixel * C;
+      for (int c = 0; c < C; ++c) {
+        float v = g[c];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          if (!P.active[n]) continue;
+          const float t = P.t[n];
+          const float* g2 = grad_out + P.other[n] * C;
+          if (P.first[n]) {
+            v += t < 0.5f ? -(0.5f - t) * g[c] : (t - 0.5f) * g2[c];
+          } else {
+            v += t < 0.5f ? (0.5f - t) * g2[c] : -(t - 0.5f) * g[c];
+          }
+        }
+        gc[c] = v;
       }
     }
-    if (!nb.first || grad_pos == nullptr) continue;
-    // Position gradient, once per pair from its first pixel.
-    const float* cP = a.color + pixel * C;
-    const float* cQ = a.color + other * C;
-    float g_t = 0.0f;
-    if (low) {
-      for (int c = 0; c < C; ++c) g_t -= g[c] * (cQ[c] - cP[c]);
-    } else {
-      for (int c = 0; c < C; ++c) g_t += g2[c] * (cP[c] - cQ[c]);
+    if (grad_pos) {
+      const uchar2 bits = pair_bits[tp.pixel];
+      const int pos_b = a.pos_batch_stride != 0 ? tp.b : 0;
+      const int64_t row0 = (int64_t)pos_b * (a.pos_batch_stride / 4);
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        const uint8_t info = n == 0 ? bits.x : bits.y;
+        if (!(info & kActive)) continue;
+        const float t = P.t[n];
+        const int64_t q = P.other[n];
+        const float* cP = a.color + tp.pixel * C;
+        const float* cQ = a.color + q * C;
+        const float* g2 = grad_out + q * C;
+        float g_t = 0.0f;
+        if (t < 0.5f) {
+          for (int c = 0; c < C; ++c) g_t -= g[c] * (cQ[c] - cP[c]);
+        } else {
+          for (int c = 0; c < C; ++c) g_t += g2[c] * (cP[c] - cQ[c]);
+        }
+        const bool owner_first = info & kOwnerFirst;
+        g_t *= owner_first ? a.boost : -a.boost;  // t = 1 - t_q when the second pixel owns it
+        if (g_t == 0.0f) continue;
+        const int qx = tp.x + (n == 0 ? 1 : 0), qy = tp.y + (n == 0 ? 0 : 1);
+        const float px = pixel_centre(tp.x, a.width), py = pixel_centre(tp.y, a.height);
+        const float qcx = pixel_centre(qx, a.width), qcy = pixel_centre(qy, a.height);
+        float depth;
+        const int owner = pixel_tri(a, owner_first ? tp.pixel : q, depth);
+        Triangle T;
+        load_triangle(a, tp.b, owner, T);
+        const int edge = info & 3;
+        float d[6];
+        if (owner_first)
+          crossing_grad(T, edge, px, py, qcx, qcy, d);
+        else
+          crossing_grad(T, edge, qcx, qcy, px, py, d);
+        const int vi = T.v[(edge + 1) % 3], vj = T.v[(edge + 2) % 3];
+        rows[2 * n] = (uint32_t)(row0 + vi);
+        rows[2 * n + 1] = (uint32_t)(row0 + vj);
+        vals[2 * n][0] = g_t * d[0];
+        vals[2 * n][1] = g_t * d[1];
+        vals[2 * n][3] = g_t * d[2];
+        vals[2 * n + 1][0] = g_t * d[3];
+        vals[2 * n + 1][1] = g_t * d[4];
+        vals[2 * n + 1][3] = g_t * d[5];
+      }
     }
-    g_t *= a.boost;
-    if (!pr.use_p) g_t = -g_t;  // t = 1 - t_q
-    if (g_t == 0.0f) continue;
-    float d[6];
-    crossing_grad(pr.T, pr.edge, pr.sx, pr.sy, pr.dx, pr.dy, d);
-    float* base = grad_pos + (int64_t)pos_b * a.pos_batch_stride;
-    const int vi = pr.T.v[(pr.edge + 1) % 3], vj = pr.T.v[(pr.edge + 2) % 3];
-    float* pi = base + 4 * (int64_t)vi;
-    float* pj = base + 4 * (int64_t)vj;
-    atomic_add(pi + 0, g_t * d[0]);
-    atomic_add(pi + 1, g_t * d[1]);
-    atomic_add(pi + 3, g_t * d[2]);
-    atomic_add(pj + 0, g_t * d[3]);
-    atomic_add(pj + 1, g_t * d[4]);
-    atomic_add(pj + 3, g_t * d[5]);
   }
+  if (grad_pos == nullptr) return;  // uniform over the workgroup
+  table.clear();
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) table.add_wave(rows[k], vals[k], 4, grad_pos, 4);
+  __syncthreads();
+  table.flush(grad_pos, 4, 4);
 }
 
 bool valid_args(const DrAntialiasArgs* a) {
@@ -498,20 +554,52 @@ extern "C" int dr_silhouette_mask(const float* pos, int64_t pos_batch_stride, in
   return launch_status();
 }
 
-extern "C" int dr_antialias_forward(const DrAntialiasArgs* a, float* out, void* stream) {
+extern "C" int dr_antialias_workspace_size(const DrAntialiasArgs* a, size_t* bytes) {
+  if (!valid_args(a) || !bytes) return DR_ERR_ARGUMENT;
+  const int64_t pixels = (int64_t)a->batch * a->height * a->width;
+  *bytes = (size_t)pixels * (sizeof(float2) + sizeof(uchar2));
+  return DR_OK;
+}
+
+static void pair_buffers(const DrAntialiasArgs* a, void* pairs, float2*& t, uchar2*& bits) {
+  const int64_t pixels = (int64_t)a->batch * a->height * a->width;
+  t = (float2*)pairs;
+  bits = (uchar2*)((char*)pairs + pixels * sizeof(float2));
+}
+
+extern "C" int dr_antialias_forward(const DrAntialiasArgs* a, void* pairs, size_t pairs_bytes,
+                                    float* out, void* stream) {
   if (!valid_args(a) || !out) return DR_ERR_ARGUMENT;
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
-  if (pixels == 0 || a->channels == 0) return DR_OK;
-  aa_fwd_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(*a, out);
+  if (pixels == 0) return DR_OK;
+  size_t need = 0;
+  dr_antialias_workspace_size(a, &need);
+  if (!pairs || pairs_bytes < need) return DR_ERR_CAPACITY;
+  float2* t;
+  uchar2* bits;
+  pair_buffers(a, pairs, t, bits);
+  const int64_t blocks = tile_blocks(a->batch, a->height, a->width);
+  aa_pairs_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits);
+  if (a->channels > 0)
+    aa_blend_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, out);
   return launch_status();
 }
 
-extern "C" int dr_antialias_backward(const DrAntialiasArgs* a, const float* grad_out,
+extern "C" int dr_antialias_backward(const DrAntialiasArgs* a, const void* pairs,
+                                     size_t pairs_bytes, const float* grad_out,
                                      float* grad_color, float* grad_pos, void* stream) {
   if (!valid_args(a) || !grad_out) return DR_ERR_ARGUMENT;
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0) return DR_OK;
-  aa_bwd_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
-      *a, grad_out, grad_color, grad_pos);
+  size_t need = 0;
+  dr_antialias_workspace_size(a, &need);
+  if (!pairs || pairs_bytes < need) return DR_ERR_CAPACITY;
+  if (grad_pos && (int64_t)a->batch * (a->pos_batch_stride / 4) >= 0xffffffffLL)
+    return DR_ERR_ARGUMENT;
+  float2* t;
+  uchar2* bits;
+  pair_buffers(a, (void*)pairs, t, bits);
+  aa_bwd_kernel<<<tile_blocks(a->batch, a->height, a->width), 256, 0, (hipStream_t)stream>>>(
+      *a, t, bits, grad_out, grad_color, grad_pos);
   return launch_status();
 }

@@ -217,12 +217,20 @@ typedef struct DrAntialiasArgs {
   float boost;                 /* pos_gradient_boost */
 } DrAntialiasArgs;
 
-/* out [batch, h, w, channels] = color blended across silhouette edges. */
-int dr_antialias_forward(const DrAntialiasArgs* a, float* out, void* stream);
+/* Bytes of the pair records that dr_antialias_forward writes and dr_antialias_backward
+ * reads (10 per pixel). */
+int dr_antialias_workspace_size(const DrAntialiasArgs* a, size_t* bytes);
 
-/* grad_color (written, nullable) and grad_pos (accumulated, nullable; layout of pos). */
-int dr_antialias_backward(const DrAntialiasArgs* a, const float* grad_out, float* grad_color,
-                          float* grad_pos, void* stream);
+/* out [batch, h, w, channels] = color blended across silhouette edges; also fills the pair
+ * records (crossing t and owner/edge bits of each pixel's right and lower pair). */
+int dr_antialias_forward(const DrAntialiasArgs* a, void* pairs, size_t pairs_bytes, float* out,
+                         void* stream);
+
+/* grad_color (written, nullable) and grad_pos (accumulated, nullable; layout of pos) from the
+ * pair records of the forward pass. */
+int dr_antialias_backward(const DrAntialiasArgs* a, const void* pairs, size_t pairs_bytes,
+                          const float* grad_out, float* grad_color, float* grad_pos,
+                          void* stream);
 
 #ifdef __cplusplus
 }
