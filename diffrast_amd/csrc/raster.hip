@@ -2,14 +2,25 @@
 //
 // Visibility decides, per pixel, the nearest triangle that covers the pixel centre, with the
 // coverage test of the reference backend (src/diffrast/backends/reference.py:293-365) and its
-// tie-break (lower triangle row on equal depth, reference.py:368-397). Every triangle instance
-// (image, triangle) gets one thread in the setup kernel, which culls it (a non-finite
-// coordinate, or every w <= 0: the interpolated w is then never positive) and bounds its
-// pixels. Triangles whose bounding box holds at most kSmallPixels pixel centres -- nearly all
-// of a dense mesh -- are rasterized right there; the others are binned into 16x16 tiles
-// (counts, a three-phase scan, a scatter into per-tile lists) and rasterized by one 256-thread
-// workgroup per tile chunk, which stages up to 256 triangles in LDS and keeps the best key of
-// its pixel in a register. Both paths merge into the key buffer with 64-bit atomic min.
+// tie-break (lower triangle row on equal depth, reference.py:368-397). The result does not
+// depend on the order in which triangles are processed -- a key is (depth, row) and merging
+// takes the minimum -- which leaves the processing order free for the hardware's sake:
+//
+// 1. Order. For a large instanced mesh, triangles are bucket-sorted by the Morton code of their
+//    centroid in the first view's clip space (an affine image of world space, so neighbours in
+//    the order are neighbours on screen in every view). Meshes such as subdivided spheres list
+//    children of one face far apart; in this order a workgroup's triangles cover a compact
+//    patch of the screen, which makes the binning below aggregate well.
+// 2. Setup: one thread per triangle instance culls it (a non-finite coordinate, or every w <= 0:
+//    the interpolated w is then never positive) and bounds its pixels. Boxes of at most
+//    kSmallPixels pixel centres are rasterized right away (64-bit atomic min per covered
+//    pixel); the others are binned into 16x16 tiles. Per-tile counts gather in an LDS table of
+//    the workgroup before one global atomic per distinct tile.
+// 3. A three-phase scan turns tile counts into list offsets and work chunks; the bin pass
+//    reserves each workgroup's share of a tile's list with one global atomic and fills it.
+// 4. One 256-thread workgroup per (tile, chunk of <= 256 triangles) stages its triangles in LDS,
+//    keeps the tile's best keys in LDS, and lets each wave sweep one triangle's box inside the
+//    tile (LDS 64-bit min), then merges the tile into the key buffer, one atomic per pixel.
 //
 // The resolve kernels turn keys into rast / rast_db (reference.py:69-114) and carry gradients
 // back to the vertices.
@@ -22,16 +33,27 @@ constexpr int kTile = 16;            // tile edge in pixels; a tile is one 256-t
 constexpr int kChunk = 256;          // triangles per tile work item
 constexpr int kSmallPixels = 16;     // bounding boxes up to this many pixels skip binning
 constexpr int kScanBlock = 1024;     // elements per scan block (256 threads x 4)
+constexpr int kOrderBuckets = 4096;  // Morton buckets (12 bits of a 30-bit code)
+constexpr int kOrderMinTris = 8192;  // smaller meshes keep their own order
+constexpr int kTileSlots = 1024;     // LDS table of a workgroup's tiles
 constexpr float kAreaTolerance = 2.384185791015625e-07f;  // 2 * float32 epsilon
 
 struct Workspace {
   int4* records;             // binned triangles: (image, row, tx0 | tx1 << 16, ty0 | ty1 << 16)
-  uint32_t* tile_counts;     // [tiles]
+  uint32_t* tile_counts;     // [tiles + 1]
   uint32_t* tile_offsets;    // [tiles + 1] exclusive prefix of tile_counts
-  uint32_t* tile_cursor;     // [tiles] fill positions for the scatter
+  uint32_t* tile_cursor;     // [tiles + 1] fill positions of the bin pass
   uint32_t* chunk_offsets;   // [tiles + 1] exclusive prefix of ceil(count / kChunk)
   uint2* block_sums;         // [scan blocks] (entries, chunks)
   uint32_t* counters;        // [0] binned triangles, [1] entries, [2] chunks
+  float* px;                 // [width] pixel-centre x per column
+  float* py;                 // [height] pixel-centre y per row
+  uint32_t* order;           // [num_tri] processing order (instanced meshes only)
+  float4* centroids;         // [num_tri] clip-space centroids in the first view
+  uint32_t* bucket_counts;   // [kOrderBuckets]
+  uint32_t* bucket_cursor;   // [kOrderBuckets]
+  uint32_t* bounds;          // [6] order-preserving bits of min x, y, z and max x, y, z
+  bool ordered;
   int tiles_x, tiles_y;
   int64_t tiles;
   int scan_blocks;
@@ -40,12 +62,17 @@ struct Workspace {
 
 size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 
+bool use_order(const DrRasterGeometry& g) {
+  return g.ranges == nullptr && g.num_tri >= kOrderMinTris;
+}
+
 Workspace layout(const DrRasterGeometry& g, char* base) {
   Workspace w{};
   w.tiles_x = (g.width + kTile - 1) / kTile;
   w.tiles_y = (g.height + kTile - 1) / kTile;
   w.tiles = (int64_t)g.batch * w.tiles_x * w.tiles_y;
   w.scan_blocks = (int)((w.tiles + 1 + kScanBlock - 1) / kScanBlock);
+  w.ordered = use_order(g);
   size_t off = 0;
   auto take = [&](size_t bytes) {
     char* p = base ? base + off : nullptr;
@@ -58,6 +85,15 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
   w.tile_cursor = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
   w.chunk_offsets = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
   w.block_sums = (uint2*)take(sizeof(uint2) * (w.scan_blocks + 1));
+  w.px = (float*)take(sizeof(float) * g.width);
+  w.py = (float*)take(sizeof(float) * g.height);
+  if (w.ordered) {
+    w.order = (uint32_t*)take(sizeof(uint32_t) * g.num_tri);
+    w.centroids = (float4*)take(sizeof(float4) * g.num_tri);
+    w.bucket_counts = (uint32_t*)take(sizeof(uint32_t) * kOrderBuckets);
+    w.bucket_cursor = (uint32_t*)take(sizeof(uint32_t) * kOrderBuckets);
+    w.bounds = (uint32_t*)take(sizeof(uint32_t) * 8);
+  }
   w.records = (int4*)take(sizeof(int4) * (size_t)(g.num_instances > 0 ? g.num_instances : 1));
   w.bytes = off;
   return w;
@@ -66,10 +102,12 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
 // ---- geometry helpers -------------------------------------------------------------------
 
 // (image, triangle row) of triangle instance i.
-__device__ __forceinline__ void instance(const DrRasterGeometry& g, int64_t i, int& b, int& t) {
+__device__ __forceinline__ void instance(const DrRasterGeometry& g, const uint32_t* order,
+                                         int64_t i, int& b, int& t) {
   if (g.ranges == nullptr) {
     b = (int)(i / g.num_tri);
-    t = (int)(i - (int64_t)b * g.num_tri);
+    const int j = (int)(i - (int64_t)b * g.num_tri);
+    t = order != nullptr ? (int)order[j] : j;
     return;
   }
   int lo = 0, hi = g.batch;  // largest b with range_prefix[b] <= i
@@ -175,14 +213,76 @@ __device__ __forceinline__ void axis_range(float n0, float n1, float n2, int siz
   hi = min((int)floorf(c), size - 1);
 }
 
-// Whether a visibility key may enter this layer; merges it into the key buffer.
+// Box [x_lo, x_hi] x [y_lo, y_hi] of the pixel centres a triangle may cover; empty (lo > hi)
+// for a culled triangle. A triangle crossing the camera plane may cover any pixel.
+__device__ __forceinline__ void candidate_box(const DrRasterGeometry& g, const Tri& T, int& x_lo,
+                                              int& x_hi, int& y_lo, int& y_hi) {
+  x_lo = y_lo = 0;
+  x_hi = y_hi = -1;
+  const bool any_front = T.w[0] > 0.0f || T.w[1] > 0.0f || T.w[2] > 0.0f;
+  if (!finite_tri(T) || !any_front) return;
+  if (T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
+    axis_range(T.x[0] / T.w[0], T.x[1] / T.w[1], T.x[2] / T.w[2], g.width, x_lo, x_hi);
+    axis_range(T.y[0] / T.w[0], T.y[1] / T.w[1], T.y[2] / T.w[2], g.height, y_lo, y_hi);
+  } else {
+    x_hi = g.width - 1;
+    y_hi = g.height - 1;
+  }
+}
+
+// Merges a key into the key buffer, unless the previous layer rules it out.
 __device__ __forceinline__ void merge_key(uint64_t* keys, const uint64_t* prev, int64_t pixel,
                                           uint64_t key) {
   if (prev != nullptr && key <= prev[pixel]) return;
   if (key < keys[pixel]) atomicMin((unsigned long long*)(keys + pixel), (unsigned long long)key);
 }
 
-// ---- kernels ----------------------------------------------------------------------------
+// ---- workgroup table of tiles -------------------------------------------------------------
+
+// Counts (and, in the bin pass, list reservations) per distinct tile of a workgroup, in LDS.
+// A tile whose key finds no free slot within kProbe steps is handled with global atomics; the
+// same key always meets the same fate within one pass, so counts and reservations agree.
+struct TileTable {
+  static constexpr uint32_t kEmpty = 0xffffffffu;
+  static constexpr int kProbe = 32;
+  uint32_t key[kTileSlots];
+  uint32_t count[kTileSlots];
+  uint32_t base[kTileSlots];
+
+  __device__ __forceinline__ void clear() {
+    for (int i = threadIdx.x; i < kTileSlots; i += blockDim.x) {
+      key[i] = kEmpty;
+      count[i] = 0u;
+    }
+  }
+  __device__ __forceinline__ static uint32_t hash(uint32_t k) {
+    k ^= k >> 16;
+    k *= 0x7feb352du;
+    k ^= k >> 15;
+    return k & (kTileSlots - 1);
+  }
+  __device__ __forceinline__ int insert(uint32_t k) {
+    uint32_t slot = hash(k);
+    for (int probe = 0; probe < kProbe; ++probe) {
+      const uint32_t seen = atomicCAS(key + slot, kEmpty, k);
+      if (seen == kEmpty || seen == k) return (int)slot;
+      slot = (slot + 1) & (kTileSlots - 1);
+    }
+    return -1;
+  }
+  __device__ __forceinline__ int find(uint32_t k) const {
+    uint32_t slot = hash(k);
+    for (int probe = 0; probe < kProbe; ++probe) {
+      const uint32_t seen = key[slot];
+      if (seen == k) return (int)slot;
+      if (seen == kEmpty) return -1;
+      slot = (slot + 1) & (kTileSlots - 1);
+    }
+    return -1;
+  }
+};
+
+// ---- kernels: fills and pixel centres -----------------------------------------------------
 
 __global__ void raster_fill_keys(uint64_t* keys, int64_t n) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -194,63 +294,197 @@ __global__ void raster_fill_u32(uint32_t* p, int64_t n, uint32_t value) {
   for (; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = value;
 }
 
-__global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g, const uint64_t* prev,
-                                                    uint64_t* keys, Workspace ws) {
+__global__ void raster_centres(float* px, int width, float* py, int height) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < width) px[i] = pixel_centre(i, width);
+  if (i < height) py[i] = pixel_centre(i, height);
+}
+
+// ---- kernels: triangle order --------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t ordered_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_ordered_bits(uint32_t u) {
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+
+// Centroid of every triangle in the first view and the bounds of the finite ones.
+__global__ __launch_bounds__(256) void order_centroids(DrRasterGeometry g, Workspace ws) {
+  __shared__ uint32_t lo[3], hi[3];
+  if (threadIdx.x < 3) {
+    lo[threadIdx.x] = 0xffffffffu;
+    hi[threadIdx.x] = 0u;
+  }
+  __syncthreads();
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < g.num_tri) {
+    const int32_t* row = g.tri + 3 * (int64_t)t;
+    float c[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const float4 p = load4(g.pos + 4 * (int64_t)row[k]);
+      c[0] += p.x;
+      c[1] += p.y;
+      c[2] += p.z;
+    }
+    ws.centroids[t] = make_float4(c[0], c[1], c[2], 0.0f);
+    if (isfinite(c[0]) && isfinite(c[1]) && isfinite(c[2])) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        atomicMin(lo + k, ordered_bits(c[k]));
+        atomicMax(hi + k, ordered_bits(c[k]));
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 3) {
+    atomicMin(ws.bounds + threadIdx.x, lo[threadIdx.x]);
+    atomicMax(ws.bounds + 3 + threadIdx.x, hi[threadIdx.x]);
+  }
+}
+
+__device__ __forceinline__ uint32_t spread10(uint32_t v) {
+  v &= 1023u;
+  v = (v | (v << 16)) & 0x030000FFu;
+  v = (v | (v << 8)) & 0x0300F00Fu;
+  v = (v | (v << 4)) & 0x030C30C3u;
+  v = (v | (v << 2)) & 0x09249249u;
+  return v;
+}
+
+// Morton bucket (top 12 bits of a 30-bit code) of a triangle's centroid.
+__device__ __forceinline__ uint32_t order_bucket(const Workspace& ws, int t) {
+  const float4 c = ws.centroids[t];
+  const float cc[3] = {c.x, c.y, c.z};
+  uint32_t q[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const float lo = from_ordered_bits(ws.bounds[k]), hi = from_ordered_bits(ws.bounds[3 + k]);
+    const float range = hi - lo;
+    float u = range > 0.0f ? (cc[k] - lo) / range : 0.0f;
+    u = isfinite(u) ? fminf(fmaxf(u, 0.0f), 1.0f) : 0.0f;
+    q[k] = min((uint32_t)(u * 1024.0f), 1023u);
+  }
+  const uint32_t code = (spread10(q[0]) << 2) | (spread10(q[1]) << 1) | spread10(q[2]);
+  return code >> 18;
+}
+
+__global__ __launch_bounds__(256) void order_count(DrRasterGeometry g, Workspace ws) {
+  __shared__ uint32_t hist[kOrderBuckets];
+  for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x) hist[i] = 0u;
+  __syncthreads();
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < g.num_tri) atomicAdd(hist + order_bucket(ws, t), 1u);
+  __syncthreads();
+  for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x)
+    if (hist[i]) atomicAdd(ws.bucket_counts + i, hist[i]);
+}
+
+// Exclusive scan of the bucket counts into the bucket cursors (one workgroup).
+__global__ __launch_bounds__(256) void order_scan(Workspace ws) {
+  __shared__ uint32_t part[256];
+  constexpr int kPer = kOrderBuckets / 256;
+  uint32_t local[kPer], sum = 0;
+  for (int k = 0; k < kPer; ++k) {
+    local[k] = ws.bucket_counts[threadIdx.x * kPer + k];
+    sum += local[k];
+  }
+  part[threadIdx.x] = sum;
+  __syncthreads();
+  for (int d = 1; d < 256; d <<= 1) {
+    const uint32_t v = threadIdx.x >= (unsigned)d ? part[threadIdx.x - d] : 0u;
+    __syncthreads();
+    part[threadIdx.x] += v;
+    __syncthreads();
+  }
+  uint32_t run = part[threadIdx.x] - sum;
+  for (int k = 0; k < kPer; ++k) {
+    ws.bucket_cursor[threadIdx.x * kPer + k] = run;
+    run += local[k];
+  }
+}
+
+__global__ __launch_bounds__(256) void order_place(DrRasterGeometry g, Workspace ws) {
+  __shared__ uint32_t hist[kOrderBuckets];
+  __shared__ uint32_t base[kOrderBuckets];
+  for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x) hist[i] = 0u;
+  __syncthreads();
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t bucket = t < g.num_tri ? order_bucket(ws, t) : 0u;
+  if (t < g.num_tri) atomicAdd(hist + bucket, 1u);
+  __syncthreads();
+  for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x) {
+    if (hist[i]) base[i] = atomicAdd(ws.bucket_cursor + i, hist[i]);
+    hist[i] = 0u;
+  }
+  __syncthreads();
+  if (t < g.num_tri) ws.order[base[bucket] + atomicAdd(hist + bucket, 1u)] = (uint32_t)t;
+}
+
+// ---- kernels: setup, scan, bin, tiles -----------------------------------------------------
+
+__global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
+                                                           const uint64_t* prev, uint64_t* keys,
+                                                           Workspace ws) {
+  __shared__ TileTable table;
+  table.clear();
+  __syncthreads();
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   bool binned = false;
   int b = 0, t = 0, x_lo = 0, x_hi = -1, y_lo = 0, y_hi = -1;
   if (i < g.num_instances) {
-    instance(g, i, b, t);
+    instance(g, ws.ordered ? ws.order : nullptr, i, b, t);
     Tri T;
     int v[3];
     load_tri(g, b, t, T, v);
-    const bool any_front = T.w[0] > 0.0f || T.w[1] > 0.0f || T.w[2] > 0.0f;
-    if (finite_tri(T) && any_front) {
-      if (T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
-        axis_range(T.x[0] / T.w[0], T.x[1] / T.w[1], T.x[2] / T.w[2], g.width, x_lo, x_hi);
-        axis_range(T.y[0] / T.w[0], T.y[1] / T.w[1], T.y[2] / T.w[2], g.height, y_lo, y_hi);
-      } else {
-        // Crossing the camera plane: the projection is unbounded, so take the whole image.
-        x_lo = 0;
-        x_hi = g.width - 1;
-        y_lo = 0;
-        y_hi = g.height - 1;
-      }
-      if (x_lo <= x_hi && y_lo <= y_hi) {
-        const int64_t count = (int64_t)(x_hi - x_lo + 1) * (y_hi - y_lo + 1);
-        if (count <= kSmallPixels) {
-          const int64_t image = (int64_t)b * g.height;
-          for (int y = y_lo; y <= y_hi; ++y) {
-            const float py = pixel_centre(y, g.height);
-            for (int x = x_lo; x <= x_hi; ++x) {
-              float depth;
-              if (covers(T.x, T.y, T.z, T.w, T.reach_x, T.reach_y, pixel_centre(x, g.width), py,
-                         depth))
-                merge_key(keys, prev, (image + y) * g.width + x, depth_key(depth, (uint32_t)t));
-            }
+    candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
+    if (x_lo <= x_hi && y_lo <= y_hi) {
+      const int64_t count = (int64_t)(x_hi - x_lo + 1) * (y_hi - y_lo + 1);
+      if (count <= kSmallPixels) {
+        const int64_t image = (int64_t)b * g.height;
+        for (int y = y_lo; y <= y_hi; ++y) {
+          const float py = ws.py[y];
+          for (int x = x_lo; x <= x_hi; ++x) {
+            float depth;
+            if (covers(T.x, T.y, T.z, T.w, T.reach_x, T.reach_y, ws.px[x], py, depth))
+              merge_key(keys, prev, (image + y) * g.width + x, depth_key(depth, (uint32_t)t));
           }
-        } else {
-          binned = true;
         }
+      } else {
+        binned = true;
       }
     }
   }
   // Append binned triangles with one counter atomic per wave.
   const uint64_t mask = __ballot(binned);
-  if (mask == 0) return;
-  const int lane = lane_id();
-  const int leader = __ffsll((unsigned long long)mask) - 1;
-  uint32_t base = 0;
-  if (lane == leader) base = atomicAdd(ws.counters, (uint32_t)__popcll(mask));
-  base = __shfl(base, leader);
-  if (!binned) return;
-  const uint32_t rec = base + (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
-  const int tx0 = x_lo / kTile, tx1 = x_hi / kTile, ty0 = y_lo / kTile, ty1 = y_hi / kTile;
-  ws.records[rec] = make_int4(b, t, (int)((uint32_t)tx0 | ((uint32_t)tx1 << 16)),
-                             (int)((uint32_t)ty0 | ((uint32_t)ty1 << 16)));
-  uint32_t* counts = ws.tile_counts + (int64_t)b * ws.tiles_x * ws.tiles_y;
-  for (int ty = ty0; ty <= ty1; ++ty)
-    for (int tx = tx0; tx <= tx1; ++tx) atomicAdd(counts + ty * ws.tiles_x + tx, 1u);
+  if (mask != 0) {
+    const int lane = lane_id();
+    const int leader = __ffsll((unsigned long long)mask) - 1;
+    uint32_t first = 0;
+    if (lane == leader) first = atomicAdd(ws.counters, (uint32_t)__popcll(mask));
+    first = __shfl(first, leader);
+    if (binned) {
+      const uint32_t rec = first + (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
+      const int tx0 = x_lo / kTile, tx1 = x_hi / kTile, ty0 = y_lo / kTile, ty1 = y_hi / kTile;
+      ws.records[rec] = make_int4(b, t, (int)((uint32_t)tx0 | ((uint32_t)tx1 << 16)),
+                                  (int)((uint32_t)ty0 | ((uint32_t)ty1 << 16)));
+      const uint32_t image_tiles = (uint32_t)b * ws.tiles_x * ws.tiles_y;
+      for (int ty = ty0; ty <= ty1; ++ty)
+        for (int tx = tx0; tx <= tx1; ++tx) {
+          const uint32_t tile = image_tiles + ty * ws.tiles_x + tx;
+          const int slot = table.insert(tile);
+          if (slot >= 0)
+            atomicAdd(table.count + slot, 1u);
+          else
+            atomicAdd(ws.tile_counts + tile, 1u);
+        }
+    }
+  }
+  __syncthreads();
+  for (int s = threadIdx.x; s < kTileSlots; s += blockDim.x)
+    if (table.key[s] != TileTable::kEmpty) atomicAdd(ws.tile_counts + table.key[s], table.count[s]);
 }
 
 // Inclusive scan of (entries, chunks) pairs over the 256 threads of a block.
@@ -283,7 +517,7 @@ __device__ __forceinline__ uint2 scan_item(const uint32_t* counts, int64_t i, in
 
 // Phase 1: per-block totals.
 __global__ __launch_bounds__(256) void raster_scan_reduce(const uint32_t* counts, int64_t n,
-                                                   uint2* block_sums) {
+                                                          uint2* block_sums) {
   __shared__ uint2 lds[4];
   const int64_t base = (int64_t)blockIdx.x * kScanBlock + threadIdx.x * 4;
   uint2 s = make_uint2(0, 0);
@@ -298,7 +532,7 @@ __global__ __launch_bounds__(256) void raster_scan_reduce(const uint32_t* counts
 
 // Phase 2: exclusive scan of the block totals in one block; totals go to the counters.
 __global__ __launch_bounds__(256) void raster_scan_blocks(uint2* block_sums, int blocks,
-                                                   uint32_t* counters) {
+                                                          uint32_t* counters) {
   __shared__ uint2 lds[4];
   __shared__ uint2 step_total;
   uint2 carry = make_uint2(0, 0);
@@ -321,8 +555,9 @@ __global__ __launch_bounds__(256) void raster_scan_blocks(uint2* block_sums, int
 
 // Phase 3: exclusive offsets per tile (and the totals at index n).
 __global__ __launch_bounds__(256) void raster_scan_apply(const uint32_t* counts, int64_t n,
-                                                  const uint2* block_sums, uint32_t* offsets,
-                                                  uint32_t* cursor, uint32_t* chunk_offsets) {
+                                                         const uint2* block_sums,
+                                                         uint32_t* offsets, uint32_t* cursor,
+                                                         uint32_t* chunk_offsets) {
   __shared__ uint2 lds[4];
   const int64_t base = (int64_t)blockIdx.x * kScanBlock + threadIdx.x * 4;
   uint2 items[4];
@@ -347,34 +582,45 @@ __global__ __launch_bounds__(256) void raster_scan_apply(const uint32_t* counts,
   }
 }
 
+// Fills the per-tile lists: the workgroup counts its records per tile in LDS, reserves its
+// share of each tile's list with one global atomic, then writes the entries.
 __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint32_t num_records,
-                                                      uint32_t* entries) {
+                                                         uint32_t* entries) {
+  __shared__ TileTable table;
+  table.clear();
+  __syncthreads();
   const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= num_records) return;
-  const int4 rec = ws.records[r];
-  const uint32_t rx = (uint32_t)rec.z, ry = (uint32_t)rec.w;
-  const int tx0 = (int)(rx & 0xffffu), tx1 = (int)(rx >> 16);
-  const int ty0 = (int)(ry & 0xffffu), ty1 = (int)(ry >> 16);
-  uint32_t* cursor = ws.tile_cursor + (int64_t)rec.x * ws.tiles_x * ws.tiles_y;
-  for (int ty = ty0; ty <= ty1; ++ty)
-    for (int tx = tx0; tx <= tx1; ++tx) entries[atomicAdd(cursor + ty * ws.tiles_x + tx, 1u)] = r;
-}
-
-// Bounding box of a triangle's candidate pixels, as in setup_kernel: [x_lo, x_hi] x [y_lo, y_hi],
-// empty (lo > hi) for a culled triangle.
-__device__ __forceinline__ void candidate_box(const DrRasterGeometry& g, const Tri& T, int& x_lo,
-                                              int& x_hi, int& y_lo, int& y_hi) {
-  x_lo = y_lo = 0;
-  x_hi = y_hi = -1;
-  const bool any_front = T.w[0] > 0.0f || T.w[1] > 0.0f || T.w[2] > 0.0f;
-  if (!finite_tri(T) || !any_front) return;
-  if (T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
-    axis_range(T.x[0] / T.w[0], T.x[1] / T.w[1], T.x[2] / T.w[2], g.width, x_lo, x_hi);
-    axis_range(T.y[0] / T.w[0], T.y[1] / T.w[1], T.y[2] / T.w[2], g.height, y_lo, y_hi);
-  } else {
-    x_hi = g.width - 1;
-    y_hi = g.height - 1;
+  int tx0 = 0, tx1 = -1, ty0 = 0, ty1 = -1;
+  uint32_t image_tiles = 0;
+  if (r < num_records) {
+    const int4 rec = ws.records[r];
+    const uint32_t rx = (uint32_t)rec.z, ry = (uint32_t)rec.w;
+    tx0 = (int)(rx & 0xffffu);
+    tx1 = (int)(rx >> 16);
+    ty0 = (int)(ry & 0xffffu);
+    ty1 = (int)(ry >> 16);
+    image_tiles = (uint32_t)rec.x * ws.tiles_x * ws.tiles_y;
   }
+  for (int ty = ty0; ty <= ty1; ++ty)
+    for (int tx = tx0; tx <= tx1; ++tx) {
+      const int slot = table.insert(image_tiles + ty * ws.tiles_x + tx);
+      if (slot >= 0) atomicAdd(table.count + slot, 1u);
+    }
+  __syncthreads();
+  for (int s = threadIdx.x; s < kTileSlots; s += blockDim.x) {
+    if (table.key[s] != TileTable::kEmpty)
+      table.base[s] = atomicAdd(ws.tile_cursor + table.key[s], table.count[s]);
+    table.count[s] = 0u;
+  }
+  __syncthreads();
+  for (int ty = ty0; ty <= ty1; ++ty)
+    for (int tx = tx0; tx <= tx1; ++tx) {
+      const uint32_t tile = image_tiles + ty * ws.tiles_x + tx;
+      const int slot = table.find(tile);
+      const uint32_t at = slot >= 0 ? table.base[slot] + atomicAdd(table.count + slot, 1u)
+                                    : atomicAdd(ws.tile_cursor + tile, 1u);
+      entries[at] = r;
+    }
 }
 
 // One workgroup per (tile, chunk of up to kChunk binned triangles). The tile's best keys live
@@ -391,6 +637,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   __shared__ uint32_t s_box[kChunk];  // tile-local x0 | x1 << 8 | y0 << 16 | y1 << 24
   __shared__ unsigned long long s_key[kTile * kTile];
   __shared__ unsigned long long s_prev[kTile * kTile];
+  __shared__ float s_px[kTile], s_py[kTile];
   __shared__ int64_t s_tile;
 
   if (threadIdx.x == 0) {
@@ -421,6 +668,11 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     if (prev != nullptr && x < g.width && y < g.height)
       floor_key = prev[((int64_t)b * g.height + y) * g.width + x];
     s_prev[threadIdx.x] = floor_key;
+    if (threadIdx.x < kTile && tile_x0 + (int)threadIdx.x < g.width)
+      s_px[threadIdx.x] = ws.px[tile_x0 + threadIdx.x];
+    if (threadIdx.x >= 32 && threadIdx.x < 32 + kTile &&
+        tile_y0 + (int)threadIdx.x - 32 < g.height)
+      s_py[threadIdx.x - 32] = ws.py[tile_y0 + threadIdx.x - 32];
   }
   if ((int)threadIdx.x < n) {
     const int4 rec = ws.records[entries[first + threadIdx.x]];
@@ -468,10 +720,8 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     const uint32_t t = s_tri[j];
     for (int ly = by0 + (lane >> shift); ly <= by1; ly += rows_per_step) {
       if (lx > bx1) continue;
-      const int x = tile_x0 + lx, y = tile_y0 + ly;
       float depth;
-      if (covers(X, Y, Z, Wv, rx, ry, pixel_centre(x, g.width), pixel_centre(y, g.height),
-                 depth)) {
+      if (covers(X, Y, Z, Wv, rx, ry, s_px[lx], s_py[ly], depth)) {
         const uint64_t key = depth_key(depth, t);
         const int p = ly * kTile + lx;
         if (prev == nullptr || key > s_prev[p]) atomicMin(s_key + p, (unsigned long long)key);
@@ -692,19 +942,33 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
   if (pixels == 0) return DR_OK;
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
-  if (g->num_instances >= (int64_t)1 << 32) return DR_ERR_ARGUMENT;
+  if (g->num_instances >= (int64_t)1 << 32 || ws.tiles >= (int64_t)1 << 32) return DR_ERR_ARGUMENT;
   const int fill_blocks = (int)std::min<int64_t>(blocks_for(pixels, 256), 65536);
   raster_fill_keys<<<fill_blocks, 256, 0, s>>>(keys, pixels);
   raster_fill_u32<<<(int)std::min<int64_t>(blocks_for(ws.tiles + 1, 256), 65536), 256, 0, s>>>(
       ws.tile_counts, ws.tiles + 1, 0u);
   raster_fill_u32<<<1, 64, 0, s>>>(ws.counters, 4, 0u);
+  raster_centres<<<blocks_for(std::max(g->width, g->height), 256), 256, 0, s>>>(
+      ws.px, g->width, ws.py, g->height);
   if (g->num_instances > 0) {
-    raster_setup_kernel<<<blocks_for(g->num_instances, 256), 256, 0, s>>>(*g, prev_keys, keys, ws);
+    if (ws.ordered) {
+      const int tri_blocks = blocks_for(g->num_tri, 256);
+      raster_fill_u32<<<blocks_for(kOrderBuckets, 256), 256, 0, s>>>(ws.bucket_counts,
+                                                                     kOrderBuckets, 0u);
+      raster_fill_u32<<<1, 64, 0, s>>>(ws.bounds, 3, 0xffffffffu);
+      raster_fill_u32<<<1, 64, 0, s>>>(ws.bounds + 3, 3, 0u);
+      order_centroids<<<tri_blocks, 256, 0, s>>>(*g, ws);
+      order_count<<<tri_blocks, 256, 0, s>>>(*g, ws);
+      order_scan<<<1, 256, 0, s>>>(ws);
+      order_place<<<tri_blocks, 256, 0, s>>>(*g, ws);
+    }
+    raster_setup_kernel<<<blocks_for(g->num_instances, 256), 256, 0, s>>>(*g, prev_keys, keys,
+                                                                          ws);
     raster_scan_reduce<<<ws.scan_blocks, 256, 0, s>>>(ws.tile_counts, ws.tiles, ws.block_sums);
     raster_scan_blocks<<<1, 256, 0, s>>>(ws.block_sums, ws.scan_blocks, ws.counters);
     raster_scan_apply<<<ws.scan_blocks, 256, 0, s>>>(ws.tile_counts, ws.tiles, ws.block_sums,
-                                              ws.tile_offsets, ws.tile_cursor,
-                                              ws.chunk_offsets);
+                                                     ws.tile_offsets, ws.tile_cursor,
+                                                     ws.chunk_offsets);
   }
   int status = launch_status();
   if (status != DR_OK) return status;

@@ -102,6 +102,34 @@ def test_mixed_triangle_sizes():
     assert_layers_match(pos, tri, (96, 80), count=2)
 
 
+def test_large_mesh_in_spatial_order_keeps_index_tie_break():
+    # Meshes of 8192 triangles or more are processed in a spatially sorted order. Copies of
+    # earlier triangles appended at the end tie in depth with their originals, which must win;
+    # non-finite and camera-crossing triangles must not disturb the sort's bounds.
+    gen = torch.Generator().manual_seed(21)
+    small, small_tri = tiny_mesh(9000, gen, 0.05, batch=2)
+    large, large_tri = random_mesh(60, gen, batch=2, w_range=(-1.0, 2.0))
+    pos = torch.cat([small, large], 1)
+    tri = torch.cat([small_tri, large_tri + small.shape[1]])
+    tri = torch.cat([tri, tri[:700].flip(0)])
+    pos[:, 5, :] = float("nan")
+    pos[1, 40, 0] = float("inf")
+    assert tri.shape[0] >= 8192
+    ref = assert_layers_match(pos, tri, (64, 72), count=3)
+    ids = ref[0][0][..., 3]
+    assert (ids > 0).any() and not (ids > tri.shape[0] - 700).any()
+
+
+def test_subdivided_sphere_in_spatial_order():
+    from diffrast_amd import workloads as W
+    gen = torch.Generator().manual_seed(22)
+    verts, tri = W.icosphere(5)
+    verts = verts * (1 + 0.02 * torch.randn(verts.shape[0], 1, generator=gen))
+    pos = W.clip_positions(verts, W.random_eyes(2, 3.0, gen), 1.0)
+    assert tri.shape[0] >= 8192
+    assert_layers_match(pos, tri, (96, 96), count=2)
+
+
 @pytest.mark.parametrize("w_range", [(1.0, 2.0), (-1.0, 2.0)])
 def test_every_pixel_of_every_layer(w_range):
     gen = torch.Generator().manual_seed(9)
