@@ -12,9 +12,13 @@ GPU before timing starts. ``--steps`` steps are timed between synchronisations, 
 ``--warmup`` untimed ones; the line printed is JSON.
 
 Per-kernel time: every C-ABI entry point called in the timed steps is bracketed by HIP events
-on the stream it launches on; ``roofline`` reports the entry point with the largest total time
-(one kernel for all but visibility), its algorithmic bytes per launch (inputs read once,
-outputs written once) over its mean duration, against 8 TB/s.
+on the stream it launches on. ``roofline`` reports the longest-running entry point that
+launches a single kernel (so that its event time is that kernel's duration): its algorithmic
+bytes per launch -- the unique bytes its algorithm must move, stated per entry point in
+``algorithmic_bytes`` -- over its mean duration, against 8 TB/s. ``traffic`` is the HBM bytes
+per launch measured for that kernel with rocprofv3 counters (FETCH_SIZE, WRITE_SIZE, each
+scaled by the counter's reading for a copy of known size), read from the summary under
+profiles/ when one exists for it.
 
 CPU baseline: the oracle (a pure-PyTorch restatement of the reference backend) on the host
 cores, on a bounded sample of the same workload -- one view, the visibility pass over a subset
@@ -45,12 +49,28 @@ HBM_PEAK = 8.0e12  # bytes/s, MI355X
 METRIC = "ms per fwd+bwd render (4-op pipeline) at 8×1024², 1.3M tris; % HBM roofline"
 
 
-class KernelTimer:
-    """HIP events around the backend's C-ABI calls, on the current stream."""
+# Entry points that launch exactly one kernel, and that kernel.
+SINGLE_KERNEL = {
+    "dr_raster_visibility_tiles": "raster_tile_kernel",
+    "dr_resolve_forward": "resolve_fwd_kernel",
+    "dr_resolve_backward": "resolve_bwd_kernel",
+    "dr_interpolate_forward": "interp_fwd_kernel",
+    "dr_interpolate_backward": "interp_bwd_kernel",
+    "dr_texture_forward": "tex_fwd_kernel",
+    "dr_texture_backward": "tex_bwd_kernel",
+    "dr_silhouette_mask": "aa_silhouette_kernel",
+    "dr_antialias_backward": "aa_bwd_kernel",
+}
 
-    def __init__(self):
+
+class KernelTimer:
+    """HIP events around the backend's C-ABI calls, on the current stream, and the algorithmic
+    bytes of each call."""
+
+    def __init__(self, bytes_of):
         self.events = defaultdict(list)
-        self.shapes = {}
+        self.bytes = defaultdict(float)
+        self.bytes_of = bytes_of
         self.active = False
         self._call = hip.call
 
@@ -64,6 +84,9 @@ class KernelTimer:
             self._call(name, *args)
             end.record()
             self.events[name].append((start, end))
+            amount = self.bytes_of(name, args)
+            if amount is not None:
+                self.bytes[name] += amount
 
         hip.call = timed
 
@@ -79,8 +102,16 @@ class KernelTimer:
         return out
 
 
+# Tile rasterization, per tile list entry: the entry (4 B), the binned triangle's record
+# (16 B), its index row (12 B) and its three vertices (48 B); per work chunk: the 256 keys of
+# its tile read and merged (16 B each).
+TILE_ENTRY_BYTES = 4 + 16 + 12 + 48
+TILE_CHUNK_BYTES = 256 * 16
+
+
 def algorithmic_bytes(w):
-    """Unique bytes each entry point must move per launch for this workload (fp32 = 4 B)."""
+    """Unique bytes each entry point must move per launch for this workload (fp32 = 4 B); a
+    callable where they depend on the call (the tile pass, on its list sizes)."""
     t = w.tensors
     B, (H, W) = w.batch, w.resolution
     P = B * H * W
@@ -97,19 +128,28 @@ def algorithmic_bytes(w):
     N0 = tex_h * tex_w
     pos = B * V * 16
     tri = T * 12
-    feat_c = t["feat"].shape[-1]
+
+    def interpolate_forward(args):
+        a = args[0]._obj  # rast (and rast_db) in, attributes once, outputs out
+        ch, nd = a.channels, a.num_diff
+        return (P * 16 + (P * 16 if nd else 0) + tri + a.num_vertices * ch * 4
+                + P * ch * 4 + P * 2 * nd * 4)
+
+    def interpolate_backward(args):
+        a = args[0]._obj  # output grads and rast in, attribute and rast grads out
+        ch, nd = a.channels, a.num_diff
+        return (P * ch * 4 + P * 2 * nd * 4 + P * 16 + (P * 16 if nd else 0) + tri
+                + 2 * a.num_vertices * ch * 4 + P * 16 + (P * 16 if nd else 0))
+
     return {
-        # visibility: pos and tri in, one key per pixel out
+        # visibility set-up: pos and tri in, one key per pixel out
         "dr_raster_visibility_begin": pos + tri + P * 8,
+        "dr_raster_visibility_tiles": lambda args: (
+            args[6][1] * TILE_ENTRY_BYTES + args[6][2] * TILE_CHUNK_BYTES),
         "dr_resolve_forward": P * 8 + pos + tri + 2 * P * 16,
         "dr_resolve_backward": P * 8 + 2 * P * 16 + pos + tri + pos,
-        # two calls per step: features (C=8, no derivatives), uv (C=2, D=2)
-        "dr_interpolate_forward": (
-            (P * 16 + tri + V * feat_c * 4 + P * feat_c * 4)
-            + (2 * P * 16 + tri + V * 2 * 4 + P * 2 * 4 + P * 4 * 4)) / 2,
-        "dr_interpolate_backward": (
-            (P * feat_c * 4 + P * 16 + tri + V * feat_c * 4 + P * 16 + V * feat_c * 4)
-            + (P * 2 * 4 + P * 4 * 4 + 2 * P * 16 + tri + V * 2 * 4 + 2 * P * 16)) / 2,
+        "dr_interpolate_forward": interpolate_forward,
+        "dr_interpolate_backward": interpolate_backward,
         "dr_mip_build": N0 * C * 4 + (L - N0) * C * 4,
         "dr_texture_forward": L * C * 4 + P * 8 + P * 16 + P * C * 4,
         "dr_texture_backward": P * C * 4 + P * 8 + P * 16 + 2 * L * C * 4 + P * 16,
@@ -191,14 +231,41 @@ def cpu_baseline(w, sample_tris: int) -> dict:
     }
 
 
+def profiled_traffic(kernel: str, workload: str) -> dict | None:
+    """HBM bytes per launch of ``kernel`` from its committed rocprofv3 counter summary."""
+    path = ROOT / "profiles" / f"{kernel}.{workload}.pmc.txt"
+    if not path.exists():
+        return None
+    fields = {}
+    for line in path.read_text().splitlines():
+        key, sep, value = line.partition(":")
+        if sep and key.strip() in ("fetch_bytes", "write_bytes", "copy_factor_fetch",
+                                   "copy_factor_write"):
+            fields[key.strip()] = float(value)
+    if len(fields) != 4:
+        return None
+    return {"bytes": fields["fetch_bytes"] + fields["write_bytes"], "source": str(
+        path.relative_to(ROOT))}
+
+
+def copy_probe(mib: int, device) -> None:
+    """One device-to-device copy of ``mib`` MiB, the calibration of the HBM byte counters."""
+    src = torch.ones(mib << 18, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--workload", default="large")
-    parser.add_argument("--cpu-sample-tris", type=int, default=256)
+    parser.add_argument("--cpu-sample-tris", type=int, default=2048)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--copy-probe-mib", type=int, default=0,
+                        help="run one copy of this size first (counter calibration)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported (the views would "
@@ -209,13 +276,21 @@ def main():
         raise SystemExit("only the headline workload 'large' is benchmarked here")
 
     device = torch.device("cuda", 0)
+    if args.copy_probe_mib:
+        copy_probe(args.copy_probe_mib, device)
     w = workloads.build(args.workload)
     step = make_step(w, device)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
 
-    timer = KernelTimer()
+    bytes_model = algorithmic_bytes(w)
+
+    def bytes_of(name, call_args):
+        model = bytes_model.get(name)
+        return model(call_args) if callable(model) else model
+
+    timer = KernelTimer(bytes_of)
     timer.install()
     timer.active = True
     torch.cuda.synchronize()
@@ -229,21 +304,23 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
 
     per_kernel = timer.summary()
-    bytes_model = algorithmic_bytes(w)
     kernels = {}
     for name, (total_ms, count) in per_kernel.items():
         mean_ms = total_ms / count
         entry = {"ms_per_step": round(total_ms / args.steps, 4), "launches_per_step":
                  count // args.steps, "mean_launch_ms": round(mean_ms, 4)}
-        if name in bytes_model:
-            gbs = bytes_model[name] / (mean_ms * 1e-3) / 1e9
+        if name in timer.bytes:
+            gbs = timer.bytes[name] / count / (mean_ms * 1e-3) / 1e9
             entry["GB/s"] = round(gbs, 1)
             entry["frac"] = round(gbs * 1e9 / HBM_PEAK, 4)
         kernels[name] = entry
-    dominant = max((n for n in per_kernel if n in bytes_model),
+    dominant = max((n for n in per_kernel if n in SINGLE_KERNEL and n in timer.bytes),
                    key=lambda n: per_kernel[n][0])
-    dom_ms = per_kernel[dominant][0] / per_kernel[dominant][1]
-    achieved = bytes_model[dominant] / (dom_ms * 1e-3) / 1e9
+    dom_total, dom_count = per_kernel[dominant]
+    dom_ms = dom_total / dom_count
+    dom_bytes = timer.bytes[dominant] / dom_count
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    traffic = profiled_traffic(SINGLE_KERNEL[dominant], args.workload)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -279,13 +356,15 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": dominant,
+            "kernel": SINGLE_KERNEL[dominant],
+            "entry_point": dominant,
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": round(achieved * 1e9 / HBM_PEAK, 4),
-            "traffic": None,
-            "algorithmic_bytes": int(bytes_model[dominant]),
+            "traffic": None if traffic is None else int(traffic["bytes"]),
+            "traffic_source": None if traffic is None else traffic["source"],
+            "algorithmic_bytes": int(dom_bytes),
             "mean_launch_ms": round(dom_ms, 4),
         },
         "cpu_baseline": cpu,

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent.parent / "libdiffrast_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 MAX_LEVELS = 32
 
 c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -105,7 +105,9 @@ _SIGNATURES = {
     "dr_raster_workspace_size": ([_P, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "dr_raster_visibility_begin": (
         [_P, _P, _P, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_uint32), _P], ctypes.c_int),
-    "dr_raster_visibility_finish": (
+    "dr_raster_visibility_bin": (
+        [_P, _P, ctypes.c_size_t, _P, ctypes.POINTER(ctypes.c_uint32), _P], ctypes.c_int),
+    "dr_raster_visibility_tiles": (
         [_P, _P, _P, _P, ctypes.c_size_t, _P, ctypes.POINTER(ctypes.c_uint32), _P], ctypes.c_int),
     "dr_resolve_forward": ([_P, _P, _P, _P, _P], ctypes.c_int),
     "dr_resolve_backward": ([_P, _P, _P, _P, _P, _P], ctypes.c_int),

@@ -93,8 +93,11 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
     call("dr_raster_visibility_begin", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),
          size.value, counts, stream)
     if counts[1]:
-        entries = torch.empty(counts[1], dtype=torch.int32, device=device)
-        call("dr_raster_visibility_finish", ref(geo.struct), ptr(prev), ptr(keys),
+        # the tile lists, then the tile of each work chunk
+        entries = torch.empty(counts[1] + counts[2], dtype=torch.int32, device=device)
+        call("dr_raster_visibility_bin", ref(geo.struct), ptr(workspace), size.value,
+             ptr(entries), counts, stream)
+        call("dr_raster_visibility_tiles", ref(geo.struct), ptr(prev), ptr(keys),
              ptr(workspace), size.value, ptr(entries), counts, stream)
     return keys
 

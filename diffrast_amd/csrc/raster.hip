@@ -36,16 +36,20 @@ constexpr int kScanBlock = 1024;     // elements per scan block (256 threads x 4
 constexpr int kOrderBuckets = 4096;  // Morton buckets (12 bits of a 30-bit code)
 constexpr int kOrderMinTris = 8192;  // smaller meshes keep their own order
 constexpr int kTileSlots = 1024;     // LDS table of a workgroup's tiles
+constexpr int kRecord = 4;           // float4 per binned triangle record (one 64-byte line)
 constexpr float kAreaTolerance = 2.384185791015625e-07f;  // 2 * float32 epsilon
 
 struct Workspace {
-  int4* records;             // binned triangles: (image, row, tx0 | tx1 << 16, ty0 | ty1 << 16)
+  float4* records;           // binned triangles, kRecord float4 each: the three clip-space
+                             // vertices, then the bits of (image, row, tx0 | tx1 << 16,
+                             // ty0 | ty1 << 16)
   uint32_t* tile_counts;     // [tiles + 1]
   uint32_t* tile_offsets;    // [tiles + 1] exclusive prefix of tile_counts
   uint32_t* tile_cursor;     // [tiles + 1] fill positions of the bin pass
   uint32_t* chunk_offsets;   // [tiles + 1] exclusive prefix of ceil(count / kChunk)
   uint2* block_sums;         // [scan blocks] (entries, chunks)
-  uint32_t* counters;        // [0] binned triangles, [1] entries, [2] chunks
+  uint32_t* counters;        // [1] entries, [2] chunks
+  uint32_t* block_records;   // [record_blocks] binned triangles of each setup workgroup
   float* px;                 // [width] pixel-centre x per column
   float* py;                 // [height] pixel-centre y per row
   uint32_t* order;           // [num_tri] processing order (instanced meshes only)
@@ -57,6 +61,7 @@ struct Workspace {
   int tiles_x, tiles_y;
   int64_t tiles;
   int scan_blocks;
+  int record_blocks;          // setup workgroups; each owns 256 record slots
   size_t bytes;
 };
 
@@ -73,6 +78,7 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
   w.tiles = (int64_t)g.batch * w.tiles_x * w.tiles_y;
   w.scan_blocks = (int)((w.tiles + 1 + kScanBlock - 1) / kScanBlock);
   w.ordered = use_order(g);
+  w.record_blocks = std::max(blocks_for(g.num_instances, 256), 1);
   size_t off = 0;
   auto take = [&](size_t bytes) {
     char* p = base ? base + off : nullptr;
@@ -85,6 +91,7 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
   w.tile_cursor = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
   w.chunk_offsets = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
   w.block_sums = (uint2*)take(sizeof(uint2) * (w.scan_blocks + 1));
+  w.block_records = (uint32_t*)take(sizeof(uint32_t) * w.record_blocks);
   w.px = (float*)take(sizeof(float) * g.width);
   w.py = (float*)take(sizeof(float) * g.height);
   if (w.ordered) {
@@ -94,7 +101,7 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
     w.bucket_cursor = (uint32_t*)take(sizeof(uint32_t) * kOrderBuckets);
     w.bounds = (uint32_t*)take(sizeof(uint32_t) * 8);
   }
-  w.records = (int4*)take(sizeof(int4) * (size_t)(g.num_instances > 0 ? g.num_instances : 1));
+  w.records = (float4*)take(sizeof(float4) * kRecord * 256 * (size_t)w.record_blocks);
   w.bytes = off;
   return w;
 }
@@ -124,6 +131,12 @@ struct Tri {
   float reach_x, reach_y;  // max_k |x_k| + |w_k| and likewise for y (reference.py:321-326)
 };
 
+// max_k |a_k| + |w_k|
+__device__ __forceinline__ float reach(const float* a, const float* w) {
+  return fmaxf(fmaxf(fabsf(a[0]) + fabsf(w[0]), fabsf(a[1]) + fabsf(w[1])),
+               fabsf(a[2]) + fabsf(w[2]));
+}
+
 __device__ __forceinline__ void load_tri(const DrRasterGeometry& g, int b, int t, Tri& T,
                                          int (&v)[3]) {
   const int32_t* row = g.tri + 3 * (int64_t)t;
@@ -139,10 +152,8 @@ __device__ __forceinline__ void load_tri(const DrRasterGeometry& g, int b, int t
     T.z[k] = p.z;
     T.w[k] = p.w;
   }
-  T.reach_x = fmaxf(fmaxf(fabsf(T.x[0]) + fabsf(T.w[0]), fabsf(T.x[1]) + fabsf(T.w[1])),
-                    fabsf(T.x[2]) + fabsf(T.w[2]));
-  T.reach_y = fmaxf(fmaxf(fabsf(T.y[0]) + fabsf(T.w[0]), fabsf(T.y[1]) + fabsf(T.w[1])),
-                    fabsf(T.y[2]) + fabsf(T.w[2]));
+  T.reach_x = reach(T.x, T.w);
+  T.reach_y = reach(T.y, T.w);
 }
 
 // Fill-rule test of one edge (reference.py:338-365).
@@ -230,11 +241,12 @@ __device__ __forceinline__ void candidate_box(const DrRasterGeometry& g, const T
   }
 }
 
-// Merges a key into the key buffer, unless the previous layer rules it out.
+// Merges a key into the key buffer, unless the previous layer rules it out. The atomic
+// returns nothing, so a thread never waits on it.
 __device__ __forceinline__ void merge_key(uint64_t* keys, const uint64_t* prev, int64_t pixel,
                                           uint64_t key) {
   if (prev != nullptr && key <= prev[pixel]) return;
-  if (key < keys[pixel]) atomicMin((unsigned long long*)(keys + pixel), (unsigned long long)key);
+  atomicMin((unsigned long long*)(keys + pixel), (unsigned long long)key);
 }
 
 // ---- workgroup table of tiles -------------------------------------------------------------
@@ -425,51 +437,126 @@ __global__ __launch_bounds__(256) void order_place(DrRasterGeometry g, Workspace
 
 // ---- kernels: setup, scan, bin, tiles -----------------------------------------------------
 
+// Splits work item p of a box bw pixels wide (bw <= 16, p < 256) into (dx, dy). The float
+// quotient (p + 1/2) / bw lies at least 1/32 away from an integer, far more than the error of
+// the approximate reciprocal, so the truncation is exact.
+__device__ __forceinline__ void box_cell(int p, int bw, int& dx, int& dy) {
+  dy = (int)(((float)p + 0.5f) * __builtin_amdgcn_rcpf((float)bw));
+  dx = p - dy * bw;
+}
+
+// Packs a box of at most 16 x 16 pixels: x0 | (w - 1) << 8 | y0 << 16 | (h - 1) << 24.
+__device__ __forceinline__ uint32_t pack_box(int x0, int w, int y0, int h) {
+  return (uint32_t)x0 | ((uint32_t)(w - 1) << 8) | ((uint32_t)y0 << 16) |
+         ((uint32_t)(h - 1) << 24);
+}
+
+// Small triangles of a workgroup staged for the wave that rasterizes them.
+struct SmallStage {
+  float4 tri[256][4];  // the three vertices, then (reach_x, reach_y, row bits, image bits)
+  uint2 box[256];      // (x0 | (w - 1) << 20, y0 | (h - 1) << 20), w * h <= kSmallPixels
+  int start[256];      // first work item of each lane's triangle within its wave
+};
+
+// One thread per triangle instance. A small triangle's pixels become work items of its wave
+// (lane j owns items start[j] .. start[j + 1] - 1), which the wave's lanes take in steps of 64;
+// the others are binned, their per-tile counts gathered in the workgroup's tile table.
 __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
                                                            const uint64_t* prev, uint64_t* keys,
                                                            Workspace ws) {
-  __shared__ TileTable table;
-  table.clear();
-  __syncthreads();
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  __shared__ union {
+    SmallStage small;
+    TileTable table;
+  } lds;
+  __shared__ int s_wave_binned[256 / DR_WAVE];
+  const int64_t block = xcd_order(blockIdx.x, gridDim.x);
+  const int64_t i = block * blockDim.x + threadIdx.x;
   bool binned = false;
+  int area = 0;
   int b = 0, t = 0, x_lo = 0, x_hi = -1, y_lo = 0, y_hi = -1;
+  Tri T;
   if (i < g.num_instances) {
     instance(g, ws.ordered ? ws.order : nullptr, i, b, t);
-    Tri T;
     int v[3];
     load_tri(g, b, t, T, v);
     candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
     if (x_lo <= x_hi && y_lo <= y_hi) {
       const int64_t count = (int64_t)(x_hi - x_lo + 1) * (y_hi - y_lo + 1);
       if (count <= kSmallPixels) {
-        const int64_t image = (int64_t)b * g.height;
-        for (int y = y_lo; y <= y_hi; ++y) {
-          const float py = ws.py[y];
-          for (int x = x_lo; x <= x_hi; ++x) {
-            float depth;
-            if (covers(T.x, T.y, T.z, T.w, T.reach_x, T.reach_y, ws.px[x], py, depth))
-              merge_key(keys, prev, (image + y) * g.width + x, depth_key(depth, (uint32_t)t));
-          }
-        }
+        area = (int)count;
+        SmallStage& st = lds.small;
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+          st.tri[threadIdx.x][k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
+        st.tri[threadIdx.x][3] = make_float4(T.reach_x, T.reach_y, __int_as_float(t),
+                                             __int_as_float(b));
+        st.box[threadIdx.x] = make_uint2((uint32_t)x_lo | ((uint32_t)(x_hi - x_lo) << 20),
+                                         (uint32_t)y_lo | ((uint32_t)(y_hi - y_lo) << 20));
       } else {
         binned = true;
       }
     }
   }
-  // Append binned triangles with one counter atomic per wave.
+  // Small triangles: exclusive prefix of the areas over the wave, then the wave's items.
+  const int lane = lane_id();
+  const int wave_base = threadIdx.x - lane;
+  int incl = area;
+#pragma unroll
+  for (int d = 1; d < DR_WAVE; d <<= 1) {
+    const int up = __shfl_up(incl, d);
+    if (lane >= d) incl += up;
+  }
+  const int total = __shfl(incl, DR_WAVE - 1);
+  lds.small.start[threadIdx.x] = incl - area;
+  __syncthreads();
+  for (int item = lane; item < total; item += DR_WAVE) {
+    const int* start = lds.small.start + wave_base;
+    int j = 0;  // the last lane whose first item is at or before this one (start[0] = 0)
+#pragma unroll
+    for (int step = DR_WAVE / 2; step >= 1; step >>= 1)
+      if (start[j + step] <= item) j += step;
+    const int owner = wave_base + j;
+    const float4 v0 = lds.small.tri[owner][0], v1 = lds.small.tri[owner][1];
+    const float4 v2 = lds.small.tri[owner][2], extra = lds.small.tri[owner][3];
+    const uint2 box = lds.small.box[owner];
+    int dx, dy;
+    box_cell(item - start[j], (int)(box.x >> 20) + 1, dx, dy);
+    const int x = (int)(box.x & 0xfffffu) + dx, y = (int)(box.y & 0xfffffu) + dy;
+    const float X[3] = {v0.x, v1.x, v2.x}, Y[3] = {v0.y, v1.y, v2.y};
+    const float Z[3] = {v0.z, v1.z, v2.z}, Wv[3] = {v0.w, v1.w, v2.w};
+    float depth;
+    if (covers(X, Y, Z, Wv, extra.x, extra.y, ws.px[x], ws.py[y], depth)) {
+      const int64_t pixel = ((int64_t)__float_as_int(extra.w) * g.height + y) * g.width + x;
+      merge_key(keys, prev, pixel, depth_key(depth, (uint32_t)__float_as_int(extra.z)));
+    }
+  }
+  // Binned triangles go to this workgroup's record slots, compacted in thread order.
+  const int wave = threadIdx.x / DR_WAVE;
   const uint64_t mask = __ballot(binned);
-  if (mask != 0) {
-    const int lane = lane_id();
-    const int leader = __ffsll((unsigned long long)mask) - 1;
-    uint32_t first = 0;
-    if (lane == leader) first = atomicAdd(ws.counters, (uint32_t)__popcll(mask));
-    first = __shfl(first, leader);
+  if (lane == 0) s_wave_binned[wave] = __popcll(mask);
+  __syncthreads();  // the stage's memory becomes the tile table
+  lds.table.clear();
+  int before = 0, block_binned = 0;
+#pragma unroll
+  for (int w = 0; w < 256 / DR_WAVE; ++w) {
+    before += w < wave ? s_wave_binned[w] : 0;
+    block_binned += s_wave_binned[w];
+  }
+  if (threadIdx.x == 0) ws.block_records[block] = (uint32_t)block_binned;
+  __syncthreads();
+  TileTable& table = lds.table;
+
+  {
     if (binned) {
-      const uint32_t rec = first + (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
+      const uint32_t rec = (uint32_t)(block * 256 + before) +
+                           (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
       const int tx0 = x_lo / kTile, tx1 = x_hi / kTile, ty0 = y_lo / kTile, ty1 = y_hi / kTile;
-      ws.records[rec] = make_int4(b, t, (int)((uint32_t)tx0 | ((uint32_t)tx1 << 16)),
-                                  (int)((uint32_t)ty0 | ((uint32_t)ty1 << 16)));
+      float4* out = ws.records + (size_t)rec * kRecord;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) out[k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
+      out[3] = make_float4(__int_as_float(b), __int_as_float(t),
+                           __uint_as_float((uint32_t)tx0 | ((uint32_t)tx1 << 16)),
+                           __uint_as_float((uint32_t)ty0 | ((uint32_t)ty1 << 16)));
       const uint32_t image_tiles = (uint32_t)b * ws.tiles_x * ws.tiles_y;
       for (int ty = ty0; ty <= ty1; ++ty)
         for (int tx = tx0; tx <= tx1; ++tx) {
@@ -584,22 +671,23 @@ __global__ __launch_bounds__(256) void raster_scan_apply(const uint32_t* counts,
 
 // Fills the per-tile lists: the workgroup counts its records per tile in LDS, reserves its
 // share of each tile's list with one global atomic, then writes the entries.
-__global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint32_t num_records,
+__global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
                                                          uint32_t* entries) {
   __shared__ TileTable table;
   table.clear();
   __syncthreads();
+  // The records of setup workgroup blockIdx.x.
   const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
   int tx0 = 0, tx1 = -1, ty0 = 0, ty1 = -1;
   uint32_t image_tiles = 0;
-  if (r < num_records) {
-    const int4 rec = ws.records[r];
-    const uint32_t rx = (uint32_t)rec.z, ry = (uint32_t)rec.w;
+  if (threadIdx.x < ws.block_records[blockIdx.x]) {
+    const float4 rec = ws.records[(size_t)r * kRecord + 3];
+    const uint32_t rx = __float_as_uint(rec.z), ry = __float_as_uint(rec.w);
     tx0 = (int)(rx & 0xffffu);
     tx1 = (int)(rx >> 16);
     ty0 = (int)(ry & 0xffffu);
     ty1 = (int)(ry >> 16);
-    image_tiles = (uint32_t)rec.x * ws.tiles_x * ws.tiles_y;
+    image_tiles = (uint32_t)__float_as_int(rec.x) * ws.tiles_x * ws.tiles_y;
   }
   for (int ty = ty0; ty <= ty1; ++ty)
     for (int tx = tx0; tx <= tx1; ++tx) {
@@ -623,34 +711,38 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint32_t 
     }
 }
 
-// One workgroup per (tile, chunk of up to kChunk binned triangles). The tile's best keys live
-// in LDS; each wave takes one triangle at a time and sweeps only the pixels of its bounding
-// box inside the tile, lanes packed by the box width, merging hits with an LDS 64-bit min.
-// The tile's keys then go to global memory with one atomic min per pixel.
+// The tile of every work chunk: chunk_tile[c] = t for the chunks of tile t.
+__global__ __launch_bounds__(256) void raster_chunk_tiles(Workspace ws, uint32_t* chunk_tile) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= ws.tiles) return;
+  for (uint32_t c = ws.chunk_offsets[t]; c < ws.chunk_offsets[t + 1]; ++c)
+    chunk_tile[c] = (uint32_t)t;
+}
+
+// One workgroup per (tile, chunk of up to kChunk binned triangles). The chunk's triangles and
+// the parts of their bounding boxes inside the tile are staged in LDS; the pixels of all those
+// boxes form one list of work items (triangle j owns items s_start[j] .. s_start[j + 1] - 1),
+// which the 256 threads walk in steps of 256, so every lane has a pixel to test whatever the
+// sizes of the boxes. Hits merge into the tile's keys in LDS (64-bit min); the tile then goes
+// to the key buffer with one atomic min per pixel.
 __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
                                                           const uint64_t* prev, uint64_t* keys,
                                                           Workspace ws,
-                                                          const uint32_t* entries) {
-  __shared__ float sx[3][kChunk], sy[3][kChunk], sz[3][kChunk], sw[3][kChunk];
-  __shared__ float s_reach_x[kChunk], s_reach_y[kChunk];
-  __shared__ uint32_t s_tri[kChunk];
-  __shared__ uint32_t s_box[kChunk];  // tile-local x0 | x1 << 8 | y0 << 16 | y1 << 24
+                                                          const uint32_t* entries,
+                                                          const uint32_t* chunk_tile) {
+  // Per staged triangle: the three vertices, then (reach_x, reach_y, row bits, box bits).
+  __shared__ float4 s_tri[kChunk][4];
+  __shared__ int s_start[kChunk];
+  __shared__ int s_wave_sum[256 / DR_WAVE];
   __shared__ unsigned long long s_key[kTile * kTile];
   __shared__ unsigned long long s_prev[kTile * kTile];
   __shared__ float s_px[kTile], s_py[kTile];
-  __shared__ int64_t s_tile;
 
-  if (threadIdx.x == 0) {
-    int64_t lo = 0, hi = ws.tiles;
-    while (hi - lo > 1) {
-      int64_t mid = (lo + hi) >> 1;
-      if (ws.chunk_offsets[mid] <= blockIdx.x) lo = mid; else hi = mid;
-    }
-    s_tile = lo;
-  }
-  __syncthreads();
-  const int64_t tile = s_tile;
-  const uint32_t chunk = blockIdx.x - ws.chunk_offsets[tile];
+  // Neighbouring chunks (the chunks of one tile, then nearby tiles) run on one XCD and share
+  // its L2.
+  const uint32_t work = (uint32_t)xcd_order(blockIdx.x, gridDim.x);
+  const int64_t tile = chunk_tile[work];
+  const uint32_t chunk = work - ws.chunk_offsets[tile];
   const uint32_t first = ws.tile_offsets[tile] + chunk * kChunk;
   const uint32_t end = min(ws.tile_offsets[tile + 1], first + kChunk);
   const int n = (int)(end - first);
@@ -674,58 +766,72 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
         tile_y0 + (int)threadIdx.x - 32 < g.height)
       s_py[threadIdx.x - 32] = ws.py[tile_y0 + threadIdx.x - 32];
   }
+  int area = 0;
   if ((int)threadIdx.x < n) {
-    const int4 rec = ws.records[entries[first + threadIdx.x]];
+    const float4* rec = ws.records + (size_t)entries[first + threadIdx.x] * kRecord;
     Tri T;
-    int v[3];
-    load_tri(g, rec.x, rec.y, T, v);
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-      sx[k][threadIdx.x] = T.x[k];
-      sy[k][threadIdx.x] = T.y[k];
-      sz[k][threadIdx.x] = T.z[k];
-      sw[k][threadIdx.x] = T.w[k];
+      const float4 p = rec[k];
+      s_tri[threadIdx.x][k] = p;
+      T.x[k] = p.x;
+      T.y[k] = p.y;
+      T.z[k] = p.z;
+      T.w[k] = p.w;
     }
-    s_reach_x[threadIdx.x] = T.reach_x;
-    s_reach_y[threadIdx.x] = T.reach_y;
-    s_tri[threadIdx.x] = (uint32_t)rec.y;
     int x_lo, x_hi, y_lo, y_hi;
     candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
     const int bx0 = max(x_lo - tile_x0, 0), bx1 = min(x_hi - tile_x0, kTile - 1);
     const int by0 = max(y_lo - tile_y0, 0), by1 = min(y_hi - tile_y0, kTile - 1);
-    s_box[threadIdx.x] = (bx0 > bx1 || by0 > by1)
-                             ? 0xffffffffu
-                             : (uint32_t)bx0 | ((uint32_t)bx1 << 8) | ((uint32_t)by0 << 16) |
-                                   ((uint32_t)by1 << 24);
+    uint32_t box = 0u;
+    if (bx0 <= bx1 && by0 <= by1) {
+      area = (bx1 - bx0 + 1) * (by1 - by0 + 1);
+      box = pack_box(bx0, bx1 - bx0 + 1, by0, by1 - by0 + 1);
+    }
+    s_tri[threadIdx.x][3] = make_float4(reach(T.x, T.w), reach(T.y, T.w),
+                                        __int_as_float(__float_as_int(rec[3].y)),
+                                        __uint_as_float(box));
   }
-  __syncthreads();
-
+  // Exclusive prefix of the areas over the workgroup.
   const int lane = lane_id();
   const int wave = threadIdx.x / DR_WAVE;
-  for (int j = wave; j < n; j += 256 / DR_WAVE) {
-    const uint32_t box = s_box[j];
-    if (box == 0xffffffffu) continue;
-    const int bx0 = box & 0xff, bx1 = (box >> 8) & 0xff, by0 = (box >> 16) & 0xff,
-              by1 = box >> 24;
-    const int bw = bx1 - bx0 + 1;
-    // Lanes per row: the box width rounded up to a power of two (at most 16).
-    const int shift = bw <= 1 ? 0 : (bw <= 2 ? 1 : (bw <= 4 ? 2 : (bw <= 8 ? 3 : 4)));
-    const int lx = bx0 + (lane & ((1 << shift) - 1));
-    const int rows_per_step = DR_WAVE >> shift;
-    const float X[3] = {sx[0][j], sx[1][j], sx[2][j]};
-    const float Y[3] = {sy[0][j], sy[1][j], sy[2][j]};
-    const float Z[3] = {sz[0][j], sz[1][j], sz[2][j]};
-    const float Wv[3] = {sw[0][j], sw[1][j], sw[2][j]};
-    const float rx = s_reach_x[j], ry = s_reach_y[j];
-    const uint32_t t = s_tri[j];
-    for (int ly = by0 + (lane >> shift); ly <= by1; ly += rows_per_step) {
-      if (lx > bx1) continue;
-      float depth;
-      if (covers(X, Y, Z, Wv, rx, ry, s_px[lx], s_py[ly], depth)) {
-        const uint64_t key = depth_key(depth, t);
-        const int p = ly * kTile + lx;
-        if (prev == nullptr || key > s_prev[p]) atomicMin(s_key + p, (unsigned long long)key);
-      }
+  int incl = area;
+#pragma unroll
+  for (int d = 1; d < DR_WAVE; d <<= 1) {
+    const int up = __shfl_up(incl, d);
+    if (lane >= d) incl += up;
+  }
+  if (lane == DR_WAVE - 1) s_wave_sum[wave] = incl;
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < 256 / DR_WAVE; ++w) {
+    const int v = s_wave_sum[w];
+    before += w < wave ? v : 0;
+    total += v;
+  }
+  s_start[threadIdx.x] = before + incl - area;
+  __syncthreads();
+
+  for (int item = threadIdx.x; item < total; item += 256) {
+    // The last triangle whose first item is at or before this one (s_start[0] = 0).
+    int j = 0;
+#pragma unroll
+    for (int step = kChunk / 2; step >= 1; step >>= 1)
+      if (s_start[j + step] <= item) j += step;
+    const float4 v0 = s_tri[j][0], v1 = s_tri[j][1], v2 = s_tri[j][2], extra = s_tri[j][3];
+    const uint32_t box = __float_as_uint(extra.w);
+    const int bw = (int)((box >> 8) & 0xff) + 1;
+    int dx, dy;
+    box_cell(item - s_start[j], bw, dx, dy);
+    const int lx = (int)(box & 0xff) + dx, ly = (int)((box >> 16) & 0xff) + dy;
+    const float X[3] = {v0.x, v1.x, v2.x}, Y[3] = {v0.y, v1.y, v2.y};
+    const float Z[3] = {v0.z, v1.z, v2.z}, Wv[3] = {v0.w, v1.w, v2.w};
+    float depth;
+    if (covers(X, Y, Z, Wv, extra.x, extra.y, s_px[lx], s_py[ly], depth)) {
+      const uint64_t key = depth_key(depth, (uint32_t)__float_as_int(extra.z));
+      const int p = ly * kTile + lx;
+      if (prev == nullptr || key > s_prev[p]) atomicMin(s_key + p, (unsigned long long)key);
     }
   }
   __syncthreads();
@@ -733,8 +839,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   const uint64_t best = s_key[threadIdx.x];
   if (best == kEmptyKey || x >= g.width || y >= g.height) return;
   const int64_t pixel = ((int64_t)b * g.height + y) * g.width + x;
-  if (best < keys[pixel])
-    atomicMin((unsigned long long*)(keys + pixel), (unsigned long long)best);
+  atomicMin((unsigned long long*)(keys + pixel), (unsigned long long)best);
 }
 
 // ---- resolve ----------------------------------------------------------------------------
@@ -942,7 +1047,9 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
   if (pixels == 0) return DR_OK;
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
-  if (g->num_instances >= (int64_t)1 << 32 || ws.tiles >= (int64_t)1 << 32) return DR_ERR_ARGUMENT;
+  // Record slots (256 per setup workgroup) and tiles are indexed with 32 bits.
+  if (g->num_instances > ((int64_t)1 << 32) - 512 || ws.tiles >= (int64_t)1 << 32)
+    return DR_ERR_ARGUMENT;
   const int fill_blocks = (int)std::min<int64_t>(blocks_for(pixels, 256), 65536);
   raster_fill_keys<<<fill_blocks, 256, 0, s>>>(keys, pixels);
   raster_fill_u32<<<(int)std::min<int64_t>(blocks_for(ws.tiles + 1, 256), 65536), 256, 0, s>>>(
@@ -976,24 +1083,38 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
   if (hipMemcpyAsync(host, ws.counters, sizeof(host), hipMemcpyDeviceToHost, s) != hipSuccess ||
       hipStreamSynchronize(s) != hipSuccess)
     return DR_ERR_HIP;
-  counts[0] = host[0];
+  counts[0] = (uint32_t)ws.record_blocks;
   counts[1] = host[1];
   counts[2] = host[2];
   return DR_OK;
 }
 
-extern "C" int dr_raster_visibility_finish(const DrRasterGeometry* g, const uint64_t* prev_keys,
-                                           uint64_t* keys, void* workspace,
-                                           size_t workspace_bytes, uint32_t* entries,
-                                           const uint32_t counts[3], void* stream) {
+extern "C" int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspace,
+                                        size_t workspace_bytes, uint32_t* entries,
+                                        const uint32_t counts[3], void* stream) {
   if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
   if (counts[1] == 0) return DR_OK;
-  if (!entries) return DR_ERR_ARGUMENT;
+  if (!entries || counts[2] == 0) return DR_ERR_ARGUMENT;
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
-  raster_bin_kernel<<<blocks_for(counts[0], 256), 256, 0, s>>>(ws, counts[0], entries);
-  raster_tile_kernel<<<counts[2], 256, 0, s>>>(*g, prev_keys, keys, ws, entries);
+  raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, entries);
+  raster_chunk_tiles<<<blocks_for(ws.tiles, 256), 256, 0, s>>>(ws, entries + counts[1]);
+  return launch_status();
+}
+
+extern "C" int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                                          uint64_t* keys, void* workspace,
+                                          size_t workspace_bytes, const uint32_t* entries,
+                                          const uint32_t counts[3], void* stream) {
+  if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
+  if (counts[1] == 0) return DR_OK;
+  if (!entries || !keys || counts[2] == 0) return DR_ERR_ARGUMENT;
+  Workspace ws = layout(*g, (char*)workspace);
+  if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
+  hipStream_t s = (hipStream_t)stream;
+  raster_tile_kernel<<<counts[2], 256, 0, s>>>(*g, prev_keys, keys, ws, entries,
+                                               entries + counts[1]);
   return launch_status();
 }
 

@@ -34,7 +34,7 @@ enum {
 
 /* Message for a code returned by any entry point (static storage). */
 const char* dr_error_string(int code);
-/* ABI version; bumped whenever a struct below changes. */
+/* ABI version; bumped whenever a struct or an entry point below changes. */
 int dr_abi_version(void);
 /* sizeof of the argument structs, in the order DrRasterGeometry, DrInterpolateArgs,
  * DrTextureArgs, DrAntialiasArgs (which = 0..3); -1 otherwise. Lets bindings check layout. */
@@ -69,19 +69,27 @@ typedef struct DrRasterGeometry {
 /* Bytes of the visibility workspace for this geometry. */
 int dr_raster_workspace_size(const DrRasterGeometry* g, size_t* bytes);
 
-/* Visibility, first part: clears keys, rasterizes triangles with a small bounding box
- * directly, and bins the others into 16x16 tiles (counts and scan). Waits for the stream and
- * returns in counts[0..2] the number of binned triangles, tile entries and tile work chunks.
+/* Visibility, first part: clears keys, orders the triangles of a large mesh spatially,
+ * rasterizes triangles with a small bounding box directly, and bins the others into 16x16
+ * tiles (counts and scan). Waits for the stream and returns in counts[0..2] the number of
+ * setup workgroups (each with up to 256 binned triangles), tile entries and tile work chunks.
  * prev_keys (nullable) is the previous depth layer. */
 int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                uint64_t* keys, void* workspace, size_t workspace_bytes,
                                uint32_t counts[3], void* stream);
 
-/* Visibility, second part: fills the per-tile lists (entries holds counts[1] uint32) and
- * rasterizes the binned triangles tile by tile. Nothing to do when counts[1] == 0. */
-int dr_raster_visibility_finish(const DrRasterGeometry* g, const uint64_t* prev_keys,
-                                uint64_t* keys, void* workspace, size_t workspace_bytes,
-                                uint32_t* entries, const uint32_t counts[3], void* stream);
+/* Visibility, second part: fills the per-tile lists. entries holds counts[1] + counts[2]
+ * uint32: the lists of all tiles, then the tile of each work chunk. Nothing to do when
+ * counts[1] == 0. (The reference has no binning: its visibility tests every triangle at every
+ * pixel, reference.py:368-397; _triton_raster.py:241-306 keeps the nearest per pixel.) */
+int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspace, size_t workspace_bytes,
+                             uint32_t* entries, const uint32_t counts[3], void* stream);
+
+/* Visibility, third part: rasterizes the binned triangles tile by tile into keys, after
+ * dr_raster_visibility_bin with the same entries. Nothing to do when counts[1] == 0. */
+int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                               uint64_t* keys, void* workspace, size_t workspace_bytes,
+                               const uint32_t* entries, const uint32_t counts[3], void* stream);
 
 /* rast [batch, h, w, 4] = (u, v, z/w, id + 1) and rast_db [batch, h, w, 4] = (du/dx, du/dy,
  * dv/dx, dv/dy) from keys; zeros where a key is empty. rast_db may be NULL.
