@@ -422,8 +422,9 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
                                                      const uchar2* pair_bits,
                                                      const float* grad_out, float* grad_color,
                                                      float* grad_pos) {
-  using Table = ScatterTable<1024, 4>;
+  using Table = RowTable<512, 4>;
   __shared__ Table table;
+  table.init();
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   const int C = a.channels;
   uint32_t rows[4] = {Table::kEmpty, Table::kEmpty, Table::kEmpty, Table::kEmpty};
@@ -501,7 +502,6 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
     }
   }
   if (grad_pos == nullptr) return;  // uniform over the workgroup
-  table.clear();
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < 4; ++k) table.add_wave(rows[k], vals[k], 4, grad_pos, 4);

@@ -94,6 +94,53 @@ __device__ __forceinline__ void wave_merged_scatter(int64_t key, const float (&v
 }
 
 
+// ---- sums over runs of lanes ----------------------------------------------------------------
+
+// The value of lane - S of the same 16-lane row, 0 in the row's first S lanes (DPP row_shr).
+template <int S>
+__device__ __forceinline__ float row_shr(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + S, 0xf, 0xf, true));
+}
+template <int S>
+__device__ __forceinline__ uint32_t row_shr(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x110 + S, 0xf, 0xf, true);
+}
+// The value of lane + S of the same 16-lane row, 0 in the row's last S lanes (DPP row_shl).
+template <int S>
+__device__ __forceinline__ uint32_t row_shl(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x100 + S, 0xf, 0xf, true);
+}
+
+template <int S, int N>
+__device__ __forceinline__ void run_step(float (&v)[N], bool take) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float y = row_shr<S>(v[i]);
+    v[i] += take ? y : 0.0f;
+  }
+}
+
+// Segmented sums over runs of consecutive lanes of a 16-lane row that hold the same key (a
+// tile row of pixels showing one triangle): afterwards the last lane of each run holds in v
+// the sum over the run. Returns true in those lanes. Every lane of the wave must be active.
+template <int N>
+__device__ __forceinline__ bool row_run_sums(uint32_t key, float (&v)[N]) {
+  const int lane = lane_id();
+  const int pos = lane & 15;
+  // Both neighbours are read in every lane (a DPP read from an inactive lane yields 0).
+  const uint32_t left = row_shr<1>(key), right = row_shl<1>(key);
+  const bool head = (pos == 0) | (left != key);
+  const bool last = (pos == 15) | (right != key);
+  const uint64_t heads = __ballot(head);
+  const int start = 63 - __clzll(heads & ((2ull << lane) - 1ull));  // first lane of the run
+  run_step<1>(v, lane - 1 >= start);
+  run_step<2>(v, lane - 2 >= start);
+  run_step<4>(v, lane - 4 >= start);
+  run_step<8>(v, lane - 8 >= start);
+  return last;
+}
+
 // ---- workgroup tiling ---------------------------------------------------------------------
 
 // Workgroups are dispatched round-robin over the 8 XCDs of an MI355X, each with its own L2.
@@ -138,20 +185,29 @@ inline int64_t tile_blocks(int batch, int height, int width) {
 // ---- workgroup scatter table --------------------------------------------------------------
 
 // Accumulates gradient rows in LDS before they reach global memory. A row is CH floats at
-// dst + key * stride; a workgroup adds its rows here (open addressing on the key, LDS float
-// atomics), then flush() writes each distinct row once, CH consecutive lanes per row, so that
-// the global atomics are few and each row's are coalesced. Rows that find no free slot within
-// kProbe steps go straight to global memory. Keys must be < 0xffffffff.
+// dst + key * stride. Lanes add rows here: open addressing on the key, where a plain read finds
+// a key already present and a compare-and-swap claims a free slot, which then joins the list
+// of used slots. flush() adds each used row to global memory once, CH consecutive lanes per
+// row, and zeroes it, so clearing and flushing cost what the workgroup touched, not the table
+// size. A key that finds no slot within kProbe steps goes straight to global memory. Keys must
+// be < 0xffffffff.
 template <int SLOTS, int CH>
-struct ScatterTable {
+struct RowTable {
   static constexpr uint32_t kEmpty = 0xffffffffu;
-  static constexpr int kProbe = 32;
+  static constexpr int kProbe = 16;
+  static_assert((SLOTS & (SLOTS - 1)) == 0 && CH % 4 == 0, "power-of-two slots, CH % 4 == 0");
   uint32_t keys[SLOTS];
   float vals[SLOTS * CH];
+  uint32_t used[SLOTS];
+  uint32_t count;
 
-  __device__ __forceinline__ void clear() {
+  // Empties the table. Every thread of the workgroup calls it; a barrier must follow.
+  __device__ __forceinline__ void init() {
     for (int i = threadIdx.x; i < SLOTS; i += blockDim.x) keys[i] = kEmpty;
-    for (int i = threadIdx.x; i < SLOTS * CH; i += blockDim.x) vals[i] = 0.0f;
+    float4* v4 = reinterpret_cast<float4*>(vals);
+    for (int i = threadIdx.x; i < SLOTS * CH / 4; i += blockDim.x)
+      v4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (threadIdx.x == 0) count = 0u;
   }
 
   __device__ __forceinline__ static uint32_t hash(uint32_t k) {
@@ -161,24 +217,46 @@ struct ScatterTable {
     return k;
   }
 
-  // Adds n (<= CH) values of row `key`; returns false if the table had no room.
-  __device__ __forceinline__ bool add(uint32_t key, const float* v, int n) {
+  // Slot of `key`, claimed if new; -1 if none within kProbe steps.
+  __device__ __forceinline__ int slot_of(uint32_t key) {
     uint32_t slot = hash(key) & (SLOTS - 1);
     for (int probe = 0; probe < kProbe; ++probe) {
-      const uint32_t seen = atomicCAS(keys + slot, kEmpty, key);
-      if (seen == kEmpty || seen == key) {
-        for (int c = 0; c < n; ++c)
-          if (v[c] != 0.0f) atomicAdd(vals + slot * CH + c, v[c]);
-        return true;
+      uint32_t seen =
+          __hip_atomic_load(keys + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (seen == key) return (int)slot;
+      if (seen == kEmpty) {
+        seen = atomicCAS(keys + slot, kEmpty, key);
+        if (seen == kEmpty) {
+          used[atomicAdd(&count, 1u)] = slot;
+          return (int)slot;
+        }
+        if (seen == key) return (int)slot;
       }
       slot = (slot + 1) & (SLOTS - 1);
     }
-    return false;
+    return -1;
+  }
+
+  // Adds n (<= CH) values of row `key`; false if the table had no room.
+  __device__ __forceinline__ bool add(uint32_t key, const float* v, int n) {
+    const int slot = slot_of(key);
+    if (slot < 0) return false;
+    for (int c = 0; c < n; ++c)
+      if (v[c] != 0.0f) atomicAdd(vals + slot * CH + c, v[c]);
+    return true;
+  }
+
+  // Adds a row to the table, or to global memory if the table has no room.
+  __device__ __forceinline__ void add_or_global(uint32_t key, const float* v, int n, float* dst,
+                                                int64_t stride) {
+    if (!add(key, v, n))
+      for (int c = 0; c < n; ++c)
+        if (v[c] != 0.0f) atomic_add(dst + (int64_t)key * stride + c, v[c]);
   }
 
   // Adds a row from every lane that has one (key != kEmpty). When every such lane of the wave
   // has the same key, the wave sums first and one lane adds, which keeps a hot row from
-  // serialising 64 LDS atomics. Rows without room are added to global memory directly.
+  // serialising 64 LDS atomics.
   __device__ __forceinline__ void add_wave(uint32_t key, const float* v, int n, float* dst,
                                            int64_t stride) {
     const uint64_t live = __ballot(key != kEmpty);
@@ -188,25 +266,36 @@ struct ScatterTable {
     if (__ballot(key == lead) == live && __popcll(live) > 1) {
       float sums[CH];
       for (int c = 0; c < n; ++c) sums[c] = wave_masked_sum(v[c], live);
-      if (lane_id() == first && !add(lead, sums, n))
-        for (int c = 0; c < n; ++c)
-          if (sums[c] != 0.0f) atomic_add(dst + (int64_t)lead * stride + c, sums[c]);
+      if (lane_id() == first) add_or_global(lead, sums, n, dst, stride);
       return;
     }
-    if (key != kEmpty && !add(key, v, n))
-      for (int c = 0; c < n; ++c)
-        if (v[c] != 0.0f) atomic_add(dst + (int64_t)key * stride + c, v[c]);
+    if (key != kEmpty) add_or_global(key, v, n, dst, stride);
   }
 
-  // Writes the accumulated rows; call after a barrier that follows every add.
+  // Adds the used rows to global memory and zeroes them; call after a barrier that follows
+  // every add. Lanes take (row, channel) pairs, a power of two >= n lanes per row.
   __device__ __forceinline__ void flush(float* dst, int64_t stride, int n) {
-    for (int i = threadIdx.x; i < SLOTS * CH; i += blockDim.x) {
-      const int slot = i / CH, c = i - slot * CH;
-      const uint32_t key = keys[slot];
-      if (key == kEmpty || c >= n) continue;
-      const float v = vals[i];
-      if (v != 0.0f) atomic_add(dst + (int64_t)key * stride + c, v);
+    const int shift = n <= 1 ? 0 : (n <= 2 ? 1 : (n <= 4 ? 2 : 3));
+    const uint32_t rows = count;
+    for (uint32_t i = threadIdx.x; i < (rows << shift); i += blockDim.x) {
+      const int c = (int)(i & ((1u << shift) - 1u));
+      if (c >= n) continue;
+      const uint32_t slot = used[i >> shift];
+      float* p = vals + slot * CH + c;
+      const float v = *p;
+      if (v != 0.0f) atomic_add(dst + (int64_t)keys[slot] * stride + c, v);
+      *p = 0.0f;
     }
+  }
+
+  // Empties the table again after flush() for another pass; call after a barrier that follows
+  // the flush. Contains its own barriers.
+  __device__ __forceinline__ void reset() {
+    const uint32_t rows = count;
+    for (uint32_t i = threadIdx.x; i < rows; i += blockDim.x) keys[used[i]] = kEmpty;
+    __syncthreads();
+    if (threadIdx.x == 0) count = 0u;
+    __syncthreads();
   }
 };
 

@@ -81,7 +81,8 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
                                                          const float* grad_out,
                                                          const float* grad_da, float* grad_attr,
                                                          float* grad_rast, float* grad_db) {
-  __shared__ ScatterTable<1024, 8> table;
+  __shared__ RowTable<512, 8> table;
+  table.init();  // the first pass's barriers order it before any add
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   const int64_t pixel = tp.pixel;
   const int C = NC > 0 ? NC : a.channels;
@@ -125,42 +126,48 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
   if (!grad_attr || C == 0) return;  // uniform over the workgroup
 
   // Rows of the attribute table are the keys (p.rows holds their float offsets), C floats per
-  // row, 8 per pass.
+  // row, 8 per pass. Pixels of a tile row that show one triangle are summed first, so each
+  // run of them makes one table update per vertex.
   uint32_t keys[3];
 #pragma unroll
   for (int k = 0; k < 3; ++k)
-    keys[k] = p.valid ? (uint32_t)(p.rows[k] / C) : ScatterTable<1024, 8>::kEmpty;
+    keys[k] = p.valid ? (uint32_t)(p.rows[k] / C) : RowTable<512, 8>::kEmpty;
+  const uint32_t run_key = p.valid ? (uint32_t)p.t : 0xffffffffu;
   const float w = 1.0f - p.u - p.v;
   for (int c0 = 0; c0 < C; c0 += 8) {
     const int n = min(8, C - c0);
-    float v0[8], v1[8], v2[8];
+    float v[24];  // vertex k, channel c at v[8 k + c]
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      v0[c] = v1[c] = v2[c] = 0.0f;
+      v[c] = v[8 + c] = v[16 + c] = 0.0f;
       if (c >= n || !p.valid) continue;
       const float gc = g[c0 + c];
-      v0[c] = gc * p.u;
-      v1[c] = gc * p.v;
-      v2[c] = gc * w;
+      v[c] = gc * p.u;
+      v[8 + c] = gc * p.v;
+      v[16 + c] = gc * w;
       if (gd) {
         for (int k = 0; k < a.num_diff; ++k) {
           if (a.diff[k] != c0 + c) continue;
           const float t0 = gd[2 * k] * db.x + gd[2 * k + 1] * db.y;
           const float t1 = gd[2 * k] * db.z + gd[2 * k + 1] * db.w;
-          v0[c] += t0;
-          v1[c] += t1;
-          v2[c] -= t0 + t1;
+          v[c] += t0;
+          v[8 + c] += t1;
+          v[16 + c] -= t0 + t1;
         }
       }
     }
-    table.clear();
+    const bool last = row_run_sums(run_key, v);
     __syncthreads();
-    table.add_wave(keys[0], v0, n, grad_attr + c0, C);
-    table.add_wave(keys[1], v1, n, grad_attr + c0, C);
-    table.add_wave(keys[2], v2, n, grad_attr + c0, C);
+    if (last && p.valid) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) table.add_or_global(keys[k], v + 8 * k, n, grad_attr + c0, C);
+    }
     __syncthreads();
     table.flush(grad_attr + c0, C, n);
-    __syncthreads();
+    if (c0 + 8 < C) {
+      __syncthreads();
+      table.reset();
+    }
   }
 }
 

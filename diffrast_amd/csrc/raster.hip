@@ -923,8 +923,9 @@ __device__ __forceinline__ void cross3(const float* u, const float* v, float* ou
 __global__ __launch_bounds__(256) void resolve_bwd_kernel(
     DrRasterGeometry g, const uint64_t* keys, const float* grad_rast, const float* grad_db,
     float* grad_pos, float scale_x, float scale_y) {
-  using Table = ScatterTable<1024, 4>;
+  using Table = RowTable<512, 4>;
   __shared__ Table table;
+  table.init();
   const TilePixel tp = tile_pixel(g.batch, g.height, g.width);
   const int64_t pixel = tp.pixel;
   float vals[3][4];
@@ -1007,10 +1008,19 @@ __global__ __launch_bounds__(256) void resolve_bwd_kernel(
       rows[k] = (uint32_t)(row0 + v[k]);
     }
   }
-  table.clear();
-  __syncthreads();
+  // Pixels of a tile row that show one triangle are summed first; each run then makes one
+  // table update per vertex.
+  float run[12];
 #pragma unroll
-  for (int k = 0; k < 3; ++k) table.add_wave(rows[k], vals[k], 4, grad_pos, 4);
+  for (int k = 0; k < 3; ++k)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) run[4 * k + c] = vals[k][c];
+  const bool last = row_run_sums(key != kEmptyKey ? (uint32_t)key : 0xffffffffu, run);
+  __syncthreads();
+  if (last && key != kEmptyKey) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) table.add_or_global(rows[k], run + 4 * k, 4, grad_pos, 4);
+  }
   __syncthreads();
   table.flush(grad_pos, 4, 4);
 }

@@ -505,7 +505,9 @@ __device__ __forceinline__ void level_taps(const Bilinear& L, float level_weight
 __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const float* grad_out,
                                                       float* grad_texels, float* grad_uv,
                                                       float* grad_uv_da, float* grad_bias) {
-  __shared__ ScatterTable<2048, 4> table;
+  using Table = RowTable<1024, 4>;
+  __shared__ Table table;
+  table.init();
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   const int64_t pixel = tp.pixel;
   const int C = a.channels;
@@ -588,10 +590,8 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
   if (grad_texels == nullptr) return;  // uniform over the workgroup
 
   // Texel gradients, four channels per pass through the workgroup's table.
-  using Table = ScatterTable<2048, 4>;
   for (int c0 = 0; c0 < C; c0 += 4) {
     const int n = min(4, C - c0);
-    table.clear();
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -605,7 +605,10 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     }
     __syncthreads();
     table.flush(grad_texels + c0, C, n);
-    __syncthreads();
+    if (c0 + 4 < C) {
+      __syncthreads();
+      table.reset();
+    }
   }
 }
 
