@@ -18,156 +18,197 @@ namespace {
 struct Pixel {
   bool valid;
   int t;
-  int64_t rows[3];  // attribute row offsets (floats) of the three vertices
+  uint32_t row[3];  // attribute rows (image * rows per image + vertex) of the three vertices
   float u, v;
 };
 
-__device__ __forceinline__ Pixel load_pixel(const DrInterpolateArgs& a, int64_t pixel,
-                                            float4& r) {
+// Reads rast for `pixel` of `image` and, for a covered pixel, the triangle's index row.
+// rows_per_image is 0 for attributes shared by all images.
+__device__ __forceinline__ Pixel load_pixel(const DrInterpolateArgs& a, int64_t pixel, int image,
+                                            uint32_t rows_per_image) {
   Pixel p;
-  r = load4(a.rast + 4 * pixel);
+  const float4 r = load4(a.rast + 4 * pixel);
   // rast stores id + 1 as a float; ids past the end of tri are background (reference.py:128).
   const float id = rintf(r.w);
   p.valid = id >= 1.0f && id <= (float)a.num_tri;
   p.t = p.valid ? (int)id - 1 : 0;
   p.u = r.x;
   p.v = r.y;
+  p.row[0] = p.row[1] = p.row[2] = 0u;
   if (p.valid) {
-    const int64_t image = pixel / ((int64_t)a.height * a.width);
-    const int64_t base = image * a.attr_batch_stride;
-    const int32_t* row = a.tri + 3 * (int64_t)p.t;
+    const int32_t* tri = a.tri + 3 * (int64_t)p.t;
+    const uint32_t base = (uint32_t)image * rows_per_image;
 #pragma unroll
-    for (int k = 0; k < 3; ++k) p.rows[k] = base + (int64_t)row[k] * a.channels;
+    for (int k = 0; k < 3; ++k) p.row[k] = base + (uint32_t)tri[k];
   }
   return p;
 }
 
-template <int NC>
-__global__ __launch_bounds__(256) void interp_fwd_kernel(DrInterpolateArgs a, float* out,
-                                                      float* out_da) {
-  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (pixel >= (int64_t)a.batch * a.height * a.width) return;
-  const int C = NC > 0 ? NC : a.channels;
-  float4 r;
-  const Pixel p = load_pixel(a, pixel, r);
-  float* o = out + pixel * C;
-  float* od = out_da ? out_da + pixel * 2 * a.num_diff : nullptr;
-  if (!p.valid) {
-    for (int c = 0; c < C; ++c) o[c] = 0.0f;
-    if (od)
-      for (int k = 0; k < 2 * a.num_diff; ++k) od[k] = 0.0f;
-    return;
-  }
-  const float* a0 = a.attr + p.rows[0];
-  const float* a1 = a.attr + p.rows[1];
-  const float* a2 = a.attr + p.rows[2];
-  const float w = 1.0f - p.u - p.v;
+// The three attribute rows of a pixel, channels [c0, c0 + N), in registers (0 past C).
+template <int N>
+__device__ __forceinline__ void load_rows(const float* attr, const Pixel& p, int C, int c0,
+                                          float (&A)[3][N]) {
 #pragma unroll
-  for (int c = 0; c < C; ++c) o[c] = p.u * a0[c] + p.v * a1[c] + w * a2[c];
-  if (od) {
-    const float4 db = load4(a.rast_db + 4 * pixel);  // du/dx, du/dy, dv/dx, dv/dy
-    for (int k = 0; k < a.num_diff; ++k) {
-      const int c = a.diff[k];
-      const float da_du = a0[c] - a2[c];
-      const float da_dv = a1[c] - a2[c];
-      od[2 * k] = db.x * da_du + db.z * da_dv;
-      od[2 * k + 1] = db.y * da_du + db.w * da_dv;
+  for (int k = 0; k < 3; ++k) {
+    const float* row = attr + (int64_t)p.row[k] * C + c0;
+#pragma unroll
+    for (int c = 0; c < N; ++c) A[k][c] = (c0 + c < C) ? row[c] : 0.0f;
+  }
+}
+
+// A[k][c] for a channel index c < N known only at run time, without indexing registers.
+template <int N>
+__device__ __forceinline__ float pick(const float (&row)[N], int c) {
+  float v = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) v = (i == c) ? row[i] : v;
+  return v;
+}
+
+// Channels per pass of the generic kernel (any channel count).
+constexpr int kGenericChannels = 4;
+
+// One thread per pixel, in pixel order. Every load of a pixel is issued before its stores.
+template <int NC>
+__global__ __launch_bounds__(256) void interp_fwd_kernel(DrInterpolateArgs a,
+                                                         float* __restrict__ out,
+                                                         float* __restrict__ out_da,
+                                                         uint32_t rows_per_image) {
+  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t image_pixels = (int64_t)a.height * a.width;
+  if (pixel >= (int64_t)a.batch * image_pixels) return;
+  const int image = image_pixels < 0x7fffffff && pixel < 0x7fffffff
+                        ? (int)((uint32_t)pixel / (uint32_t)image_pixels)
+                        : (int)(pixel / image_pixels);
+  const int C = NC > 0 ? NC : a.channels;
+  const Pixel p = load_pixel(a, pixel, image, rows_per_image);
+  const float w = 1.0f - p.u - p.v;
+  float4 db = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (out_da != nullptr && p.valid) db = load4(a.rast_db + 4 * pixel);  // du/dx, du/dy, dv/dx, dv/dy
+  float* o = out + pixel * C;
+  constexpr int N = NC > 0 ? NC : kGenericChannels;
+  for (int c0 = 0; c0 < C; c0 += N) {
+    float A[3][N];
+    if (p.valid) {
+      load_rows<N>(a.attr, p, C, c0, A);
+    } else {
+#pragma unroll
+      for (int c = 0; c < N; ++c) A[0][c] = A[1][c] = A[2][c] = 0.0f;
     }
+    float res[N];
+#pragma unroll
+    for (int c = 0; c < N; ++c) res[c] = p.valid ? p.u * A[0][c] + p.v * A[1][c] + w * A[2][c] : 0.0f;
+    if (out_da != nullptr) {
+      float* od = out_da + pixel * 2 * a.num_diff;
+      for (int k = 0; k < a.num_diff; ++k) {
+        const int c = a.diff[k] - c0;
+        if (c < 0 || c >= N) continue;
+        const float da_du = pick(A[0], c) - pick(A[2], c);
+        const float da_dv = pick(A[1], c) - pick(A[2], c);
+        od[2 * k] = p.valid ? db.x * da_du + db.z * da_dv : 0.0f;
+        od[2 * k + 1] = p.valid ? db.y * da_du + db.w * da_dv : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < N; ++c)
+      if (c0 + c < C) o[c0 + c] = res[c];
   }
 }
 
 template <int NC>
 __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
-                                                         const float* grad_out,
-                                                         const float* grad_da, float* grad_attr,
-                                                         float* grad_rast, float* grad_db) {
-  __shared__ RowTable<512, 8> table;
+                                                         const float* __restrict__ grad_out,
+                                                         const float* __restrict__ grad_da,
+                                                         float* __restrict__ grad_attr,
+                                                         float* __restrict__ grad_rast,
+                                                         float* __restrict__ grad_db,
+                                                         uint32_t rows_per_image) {
+  using Table = RowTable<512, 8>;
+  __shared__ Table table;
   table.init();  // the first pass's barriers order it before any add
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   const int64_t pixel = tp.pixel;
   const int C = NC > 0 ? NC : a.channels;
+  const int D = grad_da != nullptr ? a.num_diff : 0;
   Pixel p;
   p.valid = false;
+  p.t = 0;
   p.u = p.v = 0.0f;
+  p.row[0] = p.row[1] = p.row[2] = 0u;
   float4 db = make_float4(0.f, 0.f, 0.f, 0.f);
   if (tp.inside) {
-    float4 r;
-    p = load_pixel(a, pixel, r);
+    p = load_pixel(a, pixel, tp.b, rows_per_image);
     if (p.valid && a.num_diff > 0) db = load4(a.rast_db + 4 * pixel);
   }
-  const float* g = grad_out + (tp.inside ? pixel * C : 0);
-  const float* gd = (grad_da && tp.inside) ? grad_da + pixel * 2 * a.num_diff : nullptr;
-
-  if (tp.inside && (grad_rast || grad_db)) {
-    float gu = 0.f, gv = 0.f, g_dudx = 0.f, g_dudy = 0.f, g_dvdx = 0.f, g_dvdy = 0.f;
-    if (p.valid) {
-      const float* a0 = a.attr + p.rows[0];
-      const float* a1 = a.attr + p.rows[1];
-      const float* a2 = a.attr + p.rows[2];
-#pragma unroll
-      for (int c = 0; c < C; ++c) {
-        gu += g[c] * (a0[c] - a2[c]);
-        gv += g[c] * (a1[c] - a2[c]);
-      }
-      if (gd) {
-        for (int k = 0; k < a.num_diff; ++k) {
-          const int c = a.diff[k];
-          const float da_du = a0[c] - a2[c], da_dv = a1[c] - a2[c];
-          g_dudx += gd[2 * k] * da_du;
-          g_dudy += gd[2 * k + 1] * da_du;
-          g_dvdx += gd[2 * k] * da_dv;
-          g_dvdy += gd[2 * k + 1] * da_dv;
-        }
-      }
-    }
-    if (grad_rast) store4(grad_rast + 4 * pixel, make_float4(gu, gv, 0.f, 0.f));
-    if (grad_db) store4(grad_db + 4 * pixel, make_float4(g_dudx, g_dudy, g_dvdx, g_dvdy));
-  }
-  if (!grad_attr || C == 0) return;  // uniform over the workgroup
-
-  // Rows of the attribute table are the keys (p.rows holds their float offsets), C floats per
-  // row, 8 per pass. Pixels of a tile row that show one triangle are summed first, so each
-  // run of them makes one table update per vertex.
-  uint32_t keys[3];
-#pragma unroll
-  for (int k = 0; k < 3; ++k)
-    keys[k] = p.valid ? (uint32_t)(p.rows[k] / C) : RowTable<512, 8>::kEmpty;
-  const uint32_t run_key = p.valid ? (uint32_t)p.t : 0xffffffffu;
   const float w = 1.0f - p.u - p.v;
-  for (int c0 = 0; c0 < C; c0 += 8) {
-    const int n = min(8, C - c0);
-    float v[24];  // vertex k, channel c at v[8 k + c]
+  const float* g = grad_out + (tp.inside ? pixel * C : 0);
+  const float* gd = (D > 0 && tp.inside) ? grad_da + pixel * 2 * D : nullptr;
+  const bool scatter = grad_attr != nullptr && C > 0;  // uniform over the workgroup
+  const uint32_t run_key = p.valid ? (uint32_t)p.t : 0xffffffffu;
+  float gu = 0.f, gv = 0.f, g_dudx = 0.f, g_dudy = 0.f, g_dvdx = 0.f, g_dvdy = 0.f;
+
+  constexpr int N = 8;  // channels per pass through the table
+  for (int c0 = 0; c0 < C; c0 += N) {
+    float A[3][N], G[N];
+    const bool live = p.valid;
+    if (live) load_rows<N>(a.attr, p, C, c0, A);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      v[c] = v[8 + c] = v[16 + c] = 0.0f;
-      if (c >= n || !p.valid) continue;
-      const float gc = g[c0 + c];
-      v[c] = gc * p.u;
-      v[8 + c] = gc * p.v;
-      v[16 + c] = gc * w;
-      if (gd) {
-        for (int k = 0; k < a.num_diff; ++k) {
-          if (a.diff[k] != c0 + c) continue;
-          const float t0 = gd[2 * k] * db.x + gd[2 * k + 1] * db.y;
-          const float t1 = gd[2 * k] * db.z + gd[2 * k + 1] * db.w;
-          v[c] += t0;
-          v[8 + c] += t1;
-          v[16 + c] -= t0 + t1;
+    for (int c = 0; c < N; ++c) {
+      if (!live) A[0][c] = A[1][c] = A[2][c] = 0.0f;
+      G[c] = (live && c0 + c < C) ? g[c0 + c] : 0.0f;
+    }
+    // Vertex k, channel c at v[8 k + c].
+    float v[3 * N];
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+      gu += G[c] * (A[0][c] - A[2][c]);
+      gv += G[c] * (A[1][c] - A[2][c]);
+      v[c] = G[c] * p.u;
+      v[N + c] = G[c] * p.v;
+      v[2 * N + c] = G[c] * w;
+    }
+    if (gd != nullptr && live) {
+      for (int k = 0; k < D; ++k) {
+        const int c = a.diff[k] - c0;
+        if (c < 0 || c >= N) continue;
+        const float gx = gd[2 * k], gy = gd[2 * k + 1];
+        const float da_du = pick(A[0], c) - pick(A[2], c);
+        const float da_dv = pick(A[1], c) - pick(A[2], c);
+        g_dudx += gx * da_du;
+        g_dudy += gy * da_du;
+        g_dvdx += gx * da_dv;
+        g_dvdy += gy * da_dv;
+        const float t0 = gx * db.x + gy * db.y;
+        const float t1 = gx * db.z + gy * db.w;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+          if (i != c) continue;
+          v[i] += t0;
+          v[N + i] += t1;
+          v[2 * N + i] -= t0 + t1;
         }
       }
     }
+    if (!scatter) continue;
+    // Pixels of a tile row that show one triangle are summed first, so each run of them makes
+    // one table update per vertex.
+    const int n = min(N, C - c0);
     const bool last = row_run_sums(run_key, v);
     __syncthreads();
-    if (last && p.valid) {
+    if (last && live) {
 #pragma unroll
-      for (int k = 0; k < 3; ++k) table.add_or_global(keys[k], v + 8 * k, n, grad_attr + c0, C);
+      for (int k = 0; k < 3; ++k) table.add_or_global(p.row[k], v + N * k, n, grad_attr + c0, C);
     }
     __syncthreads();
     table.flush(grad_attr + c0, C, n);
-    if (c0 + 8 < C) {
+    if (c0 + N < C) {
       __syncthreads();
       table.reset();
     }
+  }
+  if (tp.inside) {
+    if (grad_rast) store4(grad_rast + 4 * pixel, make_float4(gu, gv, 0.f, 0.f));
+    if (grad_db) store4(grad_db + 4 * pixel, make_float4(g_dudx, g_dudy, g_dvdx, g_dvdy));
   }
 }
 
@@ -183,10 +224,24 @@ int dispatch_channels(int channels, F f) {
   }
 }
 
+// Attribute rows per image: 0 when shared, else attr_batch_stride / channels.
+uint32_t image_rows(const DrInterpolateArgs& a) {
+  return a.attr_batch_stride == 0 || a.channels == 0
+             ? 0u
+             : (uint32_t)(a.attr_batch_stride / a.channels);
+}
+
 bool valid_args(const DrInterpolateArgs* a) {
   if (!a || a->batch < 0 || a->height <= 0 || a->width <= 0 || a->channels < 0) return false;
-  if (a->num_tri < 0 || a->num_diff < 0) return false;
+  if (a->num_tri < 0 || a->num_diff < 0 || a->num_vertices < 0) return false;
   if (a->num_diff > 0 && (!a->rast_db || !a->diff)) return false;
+  // Attribute rows (and the gradient table's keys) are 32-bit: whole rows per image, fewer
+  // than 2^32 - 1 rows in all.
+  if (a->attr_batch_stride < 0) return false;
+  if (a->channels > 0 && a->attr_batch_stride % a->channels != 0) return false;
+  const int64_t per_image = a->channels > 0 ? a->attr_batch_stride / a->channels : 0;
+  const int64_t rows = per_image != 0 ? per_image * a->batch : (int64_t)a->num_vertices;
+  if (rows >= 0xffffffffLL || per_image >= 0xffffffffLL) return false;
   return true;
 }
 
@@ -201,9 +256,10 @@ extern "C" int dr_interpolate_forward(const DrInterpolateArgs* a, float* out, fl
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0 || (a->channels == 0 && a->num_diff == 0)) return DR_OK;
   const DrInterpolateArgs args = *a;
+  const uint32_t rows_per_image = image_rows(args);
   return dispatch_channels(args.channels, [&](auto nc) {
     interp_fwd_kernel<decltype(nc)::value><<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
-        args, out, args.num_diff > 0 ? out_da : nullptr);
+        args, out, args.num_diff > 0 ? out_da : nullptr, rows_per_image);
     return launch_status();
   });
 }
@@ -214,14 +270,13 @@ extern "C" int dr_interpolate_backward(const DrInterpolateArgs* a, const float* 
   if (!valid_args(a) || !grad_out) return DR_ERR_ARGUMENT;
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0) return DR_OK;
-  // Rows of the attribute table are 32-bit keys of the workgroup scatter table.
-  const int64_t rows = (a->attr_batch_stride != 0 ? (int64_t)a->batch : 1) * a->num_vertices;
-  if (grad_attr && rows >= 0xffffffffLL) return DR_ERR_ARGUMENT;
+  const uint32_t rows_per_image = image_rows(*a);
   const float* gda = a->num_diff > 0 ? grad_out_da : nullptr;
   return dispatch_channels(a->channels, [&](auto nc) {
     interp_bwd_kernel<decltype(nc)::value>
         <<<tile_blocks(a->batch, a->height, a->width), 256, 0, (hipStream_t)stream>>>(
-            *a, grad_out, gda, grad_attr, grad_rast, a->num_diff > 0 ? grad_rast_db : nullptr);
+            *a, grad_out, gda, grad_attr, grad_rast, a->num_diff > 0 ? grad_rast_db : nullptr,
+            rows_per_image);
     return launch_status();
   });
 }
