@@ -102,10 +102,10 @@ class KernelTimer:
         return out
 
 
-# Tile rasterization, per tile list entry: the entry (4 B), the binned triangle's record
-# (16 B), its index row (12 B) and its three vertices (48 B); per work chunk: the 256 keys of
-# its tile read and merged (16 B each).
-TILE_ENTRY_BYTES = 4 + 16 + 12 + 48
+# Tile rasterization, per tile list entry: the entry (4 B) and the 64-byte record it names
+# (three clip-space vertices, triangle row, tile rectangle); per work chunk: the 256 keys of its
+# tile read and merged (16 B each).
+TILE_ENTRY_BYTES = 4 + 64
 TILE_CHUNK_BYTES = 256 * 16
 
 
@@ -249,11 +249,17 @@ def profiled_traffic(kernel: str, workload: str) -> dict | None:
 
 
 def copy_probe(mib: int, device) -> None:
-    """One device-to-device copy of ``mib`` MiB, the calibration of the HBM byte counters."""
+    """One device-to-device copy of ``mib`` MiB from memory no cache holds, the calibration of
+    the HBM byte counters: the source is written, then a 2 GiB fill evicts it from the L2s and
+    the Infinity Cache, then it is copied."""
     src = torch.ones(mib << 18, dtype=torch.float32, device=device)
     dst = torch.empty_like(src)
+    evict = torch.empty(1 << 29, dtype=torch.float32, device=device)
+    evict.fill_(0.0)
+    torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
+    del evict
 
 
 def main():
@@ -262,7 +268,7 @@ def main():
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--workload", default="large")
-    parser.add_argument("--cpu-sample-tris", type=int, default=2048)
+    parser.add_argument("--cpu-sample-tris", type=int, default=4096)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="run one copy of this size first (counter calibration)")
