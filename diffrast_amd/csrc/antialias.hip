@@ -169,6 +169,13 @@ __global__ __launch_bounds__(256) void aa_silhouette_kernel(const float* pos, in
 
 // ---- crossings --------------------------------------------------------------------------
 
+// a[k] for a k known only at run time, as selects: indexing a register array with it would
+// move the array to scratch memory.
+template <typename V>
+__device__ __forceinline__ V pick3(const V (&a)[3], int k) {
+  return k == 0 ? a[0] : (k == 1 ? a[1] : a[2]);
+}
+
 struct Triangle {
   int v[3];
   float x[3], y[3], w[3];
@@ -227,8 +234,10 @@ __device__ __forceinline__ Crossing crossing(const Triangle& T, uint8_t sil, boo
   if (!any || !((sil >> edge) & 1u)) return out;
   // The axis whose pixel pairs handle this edge (reference.py:749-765).
   const int i = (edge + 1) % 3, j = (edge + 2) % 3;
-  const float steep = fabsf(T.w[j] * T.y[i] - T.w[i] * T.y[j]) * (float)height * kAxisTie;
-  const float flat = fabsf(T.x[j] * T.w[i] - T.x[i] * T.w[j]) * (float)width;
+  const float xi = pick3(T.x, i), yi = pick3(T.y, i), wi = pick3(T.w, i);
+  const float xj = pick3(T.x, j), yj = pick3(T.y, j), wj = pick3(T.w, j);
+  const float steep = fabsf(wj * yi - wi * yj) * (float)height * kAxisTie;
+  const float flat = fabsf(xj * wi - xi * wj) * (float)width;
   const bool along = horizontal ? (steep >= flat) : (flat > steep);
   if (!along) return out;
   out.found = true;
@@ -242,10 +251,12 @@ __device__ __forceinline__ Crossing crossing(const Triangle& T, uint8_t sil, boo
 __device__ __forceinline__ void crossing_grad(const Triangle& T, int edge, float sx, float sy,
                                               float dx, float dy, float (&g)[6]) {
   const int i = (edge + 1) % 3, j = (edge + 2) % 3;
-  const float asi = T.x[i] - sx * T.w[i], csi = T.y[i] - sy * T.w[i];
-  const float asj = T.x[j] - sx * T.w[j], csj = T.y[j] - sy * T.w[j];
-  const float adi = T.x[i] - dx * T.w[i], cdi = T.y[i] - dy * T.w[i];
-  const float adj = T.x[j] - dx * T.w[j], cdj = T.y[j] - dy * T.w[j];
+  const float xi = pick3(T.x, i), yi = pick3(T.y, i), wi = pick3(T.w, i);
+  const float xj = pick3(T.x, j), yj = pick3(T.y, j), wj = pick3(T.w, j);
+  const float asi = xi - sx * wi, csi = yi - sy * wi;
+  const float asj = xj - sx * wj, csj = yj - sy * wj;
+  const float adi = xi - dx * wi, cdi = yi - dy * wi;
+  const float adj = xj - dx * wj, cdj = yj - dy * wj;
   const float es = asi * csj - asj * csi;
   const float ed = adi * cdj - adj * cdi;
   const float span = es - ed;
@@ -489,7 +500,7 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
           crossing_grad(T, edge, px, py, qcx, qcy, d);
         else
           crossing_grad(T, edge, qcx, qcy, px, py, d);
-        const int vi = T.v[(edge + 1) % 3], vj = T.v[(edge + 2) % 3];
+        const int vi = pick3(T.v, (edge + 1) % 3), vj = pick3(T.v, (edge + 2) % 3);
         rows[2 * n] = (uint32_t)(row0 + vi);
         rows[2 * n + 1] = (uint32_t)(row0 + vj);
         vals[2 * n][0] = g_t * d[0];

@@ -130,16 +130,17 @@ __device__ __forceinline__ void cube_project(const float* dir, const float* dir_
 }
 
 // Gradient of cube_project: from d(loss)/d(st) and d(loss)/d(st_da) to the direction and
-// its derivatives. grad_dir gets 3 values, grad_dir_da 6 (or is nullptr).
+// its derivatives (3 and 6 values); g_sda is used when use_sda is set.
 __device__ __forceinline__ void cube_project_backward(const CubeProj& P, float g_s, float g_t,
-                                                      const float* g_sda, float* grad_dir,
-                                                      float* grad_dir_da) {
+                                                      bool use_sda, const float (&g_sda)[4],
+                                                      float (&grad_dir)[3],
+                                                      float (&grad_dir_da)[6]) {
   const int* M = kMajor[P.face];
   const int* S = kSAxis[P.face];
   const int* T = kTAxis[P.face];
   float g_rs = 0.5f * g_s, g_rt = 0.5f * g_t, g_ma = 0.0f;
   float g_dsc[2] = {0.f, 0.f}, g_dtc[2] = {0.f, 0.f}, g_dma[2] = {0.f, 0.f};
-  if (g_sda != nullptr && !P.undefined) {
+  if (use_sda && !P.undefined) {
     const float gds[2] = {g_sda[0], g_sda[1]}, gdt[2] = {g_sda[2], g_sda[3]};
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -152,16 +153,14 @@ __device__ __forceinline__ void cube_project_backward(const CubeProj& P, float g
       g_dma[j] = -0.5f * (gds[j] * P.rs + gdt[j] * P.rt) / P.ma;
     }
   }
-  if (grad_dir_da != nullptr) {
 #pragma unroll
-    for (int k = 0; k < 3; ++k)
+  for (int k = 0; k < 3; ++k)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        float g = g_dsc[j] * (float)S[k] + g_dtc[j] * (float)T[k] + g_dma[j] * (float)M[k];
-        g = (P.valid && !P.undefined && P.da_pass[k][j]) ? g / P.length : 0.0f;
-        grad_dir_da[2 * k + j] = g;
-      }
-  }
+    for (int j = 0; j < 2; ++j) {
+      float g = g_dsc[j] * (float)S[k] + g_dtc[j] * (float)T[k] + g_dma[j] * (float)M[k];
+      g = (P.valid && !P.undefined && P.da_pass[k][j]) ? g / P.length : 0.0f;
+      grad_dir_da[2 * k + j] = g;
+    }
   g_ma -= (g_rs * P.rs + g_rt * P.rt) / P.ma;
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
@@ -308,21 +307,21 @@ __device__ __forceinline__ void bilinear_grad(const Bilinear& L, const float (&t
 
 // Level of detail from the footprint (reference.py:491-501). uv_da = (du/dx, du/dy, dv/dx,
 // dv/dy); width and height are those of the base level.
-__device__ __forceinline__ float footprint_lod(const float* da, int height, int width) {
+__device__ __forceinline__ float footprint_lod(const float4& da, int height, int width) {
   const float W = (float)width, H = (float)height, L = kFootprintLimit;
-  const float cx0 = fminf(fmaxf(da[0] * W, -L), L), cy0 = fminf(fmaxf(da[2] * H, -L), L);
-  const float cx1 = fminf(fmaxf(da[1] * W, -L), L), cy1 = fminf(fmaxf(da[3] * H, -L), L);
+  const float cx0 = fminf(fmaxf(da.x * W, -L), L), cy0 = fminf(fmaxf(da.z * H, -L), L);
+  const float cx1 = fminf(fmaxf(da.y * W, -L), L), cy1 = fminf(fmaxf(da.w * H, -L), L);
   const float len_x = cx0 * cx0 + cy0 * cy0;
   const float len_y = cx1 * cx1 + cy1 * cy1;
-  if (isnan(da[0]) || isnan(da[1]) || isnan(da[2]) || isnan(da[3]))
+  if (isnan(da.x) || isnan(da.y) || isnan(da.z) || isnan(da.w))
     return __int_as_float(0x7fc00000);
   return 0.5f * log2f(fmaxf(fmaxf(len_x, len_y), kMinFootprint));
 }
 
-__device__ __forceinline__ void footprint_lod_grad(const float* da, int height, int width,
+__device__ __forceinline__ void footprint_lod_grad(const float4& da, int height, int width,
                                                    float g, float* grad) {
   const float W = (float)width, H = (float)height, L = kFootprintLimit;
-  const float v[4] = {da[0] * W, da[1] * W, da[2] * H, da[3] * H};  // du/dx, du/dy, dv/dx, dv/dy
+  const float v[4] = {da.x * W, da.y * W, da.z * H, da.w * H};  // du/dx, du/dy, dv/dx, dv/dy
   float c[4];
   bool pass[4];
 #pragma unroll
@@ -365,8 +364,10 @@ __device__ __forceinline__ void lookup_setup(const DrTextureArgs& a, int64_t pix
   K.mip = mip;
   K.dir_invalid = false;
   K.face = -1;
-  const float* da = nullptr;
-  float st_da[4];
+  // (du/dx, du/dy, dv/dx, dv/dy), held by value: a pointer that could address either this
+  // thread's registers or global memory would force them into scratch memory.
+  bool has_da = false;
+  float4 da = make_float4(0.f, 0.f, 0.f, 0.f);
   if (cube) {
     cube_project(a.uv + 3 * pixel, (mip && a.uv_da) ? a.uv_da + 6 * pixel : nullptr, K.P);
     K.dir_invalid = !K.P.valid;
@@ -374,13 +375,16 @@ __device__ __forceinline__ void lookup_setup(const DrTextureArgs& a, int64_t pix
     K.s = K.P.st[0];
     K.t = K.P.st[1];
     if (mip && a.uv_da) {
-      for (int i = 0; i < 4; ++i) st_da[i] = K.P.st_da[i];
-      da = st_da;
+      da = make_float4(K.P.st_da[0], K.P.st_da[1], K.P.st_da[2], K.P.st_da[3]);
+      has_da = true;
     }
   } else {
     K.s = a.uv[2 * pixel];
     K.t = a.uv[2 * pixel + 1];
-    if (mip && a.uv_da) da = a.uv_da + 4 * pixel;
+    if (mip && a.uv_da) {
+      da = load4(a.uv_da + 4 * pixel);
+      has_da = true;
+    }
   }
   K.bad = false;
   K.lod_grad = false;
@@ -392,7 +396,7 @@ __device__ __forceinline__ void lookup_setup(const DrTextureArgs& a, int64_t pix
     return;
   }
   float lod = 0.0f;
-  if (da) lod = lod + footprint_lod(da, a.level_height[0], a.level_width[0]);
+  if (has_da) lod = lod + footprint_lod(da, a.level_height[0], a.level_width[0]);
   if (a.bias) lod = lod + a.bias[pixel];
   K.lod_raw = lod;
   const int top = a.num_levels - 1;
@@ -479,7 +483,8 @@ __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* ou
 // level weight, and the level's value per channel for the blend-factor gradient.
 __device__ __forceinline__ void level_coordinate_grads(const Bilinear& L, const float* texels,
                                                        const float* g, int C, float level_weight,
-                                                       float& g_fx, float& g_fy, float* g_value) {
+                                                       float& g_fx, float& g_fy,
+                                                       bool want_value, float& g_value) {
   for (int c = 0; c < C; ++c) {
     float t[4], wgt[4], dfx, dfy;
     fetch4(texels, L, C, c, t);
@@ -487,7 +492,7 @@ __device__ __forceinline__ void level_coordinate_grads(const Bilinear& L, const 
     const float gl = g[c] * level_weight;
     g_fx += gl * dfx;
     g_fy += gl * dfy;
-    if (g_value) *g_value += g[c] * bilinear_value(L, t);
+    if (want_value) g_value += g[c] * bilinear_value(L, t);
   }
 }
 
@@ -549,12 +554,12 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
       live = false;
     } else {
       float fx0 = 0.f, fy0 = 0.f, fx1 = 0.f, fy1 = 0.f, v0 = 0.f, v1 = 0.f;
-      level_coordinate_grads(L0, texels, g, C, K.level_weight[0], fx0, fy0, two ? &v0 : nullptr);
+      level_coordinate_grads(L0, texels, g, C, K.level_weight[0], fx0, fy0, two, v0);
       level_taps(L0, K.level_weight[0], tex_off, tap_index, tap_weight);
       if (L0.pass_x) g_s += fx0 * L0.size_x;
       if (L0.pass_y) g_t += fy0 * L0.size_y;
       if (two) {
-        level_coordinate_grads(L1, texels, g, C, K.level_weight[1], fx1, fy1, &v1);
+        level_coordinate_grads(L1, texels, g, C, K.level_weight[1], fx1, fy1, true, v1);
         level_taps(L1, K.level_weight[1], tex_off, tap_index + 4, tap_weight + 4);
         if (L1.pass_x) g_s += fx1 * L1.size_x;
         if (L1.pass_y) g_t += fy1 * L1.size_y;
@@ -567,13 +572,14 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     float g_da[4] = {0.f, 0.f, 0.f, 0.f};
     const bool has_da = K.mip && a.uv_da != nullptr;
     if (live && has_da && g_lod != 0.0f) {
-      const float* da = cube ? K.P.st_da : a.uv_da + 4 * pixel;
+      const float4 da = cube ? make_float4(K.P.st_da[0], K.P.st_da[1], K.P.st_da[2], K.P.st_da[3])
+                             : load4(a.uv_da + 4 * pixel);
       footprint_lod_grad(da, a.level_height[0], a.level_width[0], g_lod, g_da);
     }
     if (grad_bias) grad_bias[pixel] = live ? g_lod : 0.0f;
     if (cube) {
       float gdir[3] = {0.f, 0.f, 0.f}, gdir_da[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      if (live) cube_project_backward(K.P, g_s, g_t, has_da ? g_da : nullptr, gdir, gdir_da);
+      if (live) cube_project_backward(K.P, g_s, g_t, has_da, g_da, gdir, gdir_da);
       if (grad_uv)
         for (int k = 0; k < 3; ++k) grad_uv[3 * pixel + k] = gdir[k];
       if (grad_uv_da)
