@@ -58,7 +58,6 @@ SINGLE_KERNEL = {
     "dr_interpolate_backward": "interp_bwd_kernel",
     "dr_texture_forward": "tex_fwd_kernel",
     "dr_texture_backward": "tex_bwd_kernel",
-    "dr_silhouette_mask": "aa_silhouette_kernel",
     "dr_antialias_backward": "aa_bwd_kernel",
 }
 
@@ -154,7 +153,8 @@ def algorithmic_bytes(w):
         "dr_texture_forward": L * C * 4 + P * 8 + P * 16 + P * C * 4,
         "dr_texture_backward": P * C * 4 + P * 8 + P * 16 + 2 * L * C * 4 + P * 16,
         "dr_mip_build_backward": N0 * C * 4 + (L - N0) * C * 4,
-        "dr_silhouette_mask": pos + tri + T * 4 * 3 + B * T,
+        # rast ids in, the mask cleared and written; the shown triangles' rows and vertices
+        "dr_silhouette_mask": P * 16 + 2 * B * T + pos + tri + T * 4 * 3,
         "dr_antialias_forward": 2 * P * C * 4 + P * 16 + pos + tri + B * T,
         "dr_antialias_backward": 3 * P * C * 4 + P * 16 + 2 * pos + tri + B * T,
     }

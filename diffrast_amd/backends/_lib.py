@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent.parent / "libdiffrast_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 MAX_LEVELS = 32
 
 c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -122,8 +122,8 @@ _SIGNATURES = {
     "dr_edge_hash_workspace_size": ([ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)],
                                     ctypes.c_int),
     "dr_edge_neighbours": ([_P, ctypes.c_int32, _P, ctypes.c_size_t, _P, _P], ctypes.c_int),
-    "dr_silhouette_mask": ([_P, ctypes.c_int64, ctypes.c_int32, _P, ctypes.c_int32, _P, _P, _P],
-                           ctypes.c_int),
+    "dr_silhouette_mask": ([_P, ctypes.c_int64, ctypes.c_int32, _P, ctypes.c_int32, _P, _P,
+                            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _P], ctypes.c_int),
     "dr_antialias_workspace_size": ([_P, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "dr_antialias_forward": ([_P, _P, ctypes.c_size_t, _P, _P], ctypes.c_int),
     "dr_antialias_backward": ([_P, _P, ctypes.c_size_t, _P, _P, _P, _P], ctypes.c_int),

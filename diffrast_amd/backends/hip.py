@@ -449,13 +449,18 @@ def edge_neighbours(tri: Tensor) -> Tensor:
     return out
 
 
-def silhouette_mask(pos: Tensor, tri: Tensor, neighbours: Tensor) -> Tensor:
-    """Silhouette bits per (pos batch, triangle), uint8 (reference.py:790-814)."""
+def silhouette_mask(pos: Tensor, tri: Tensor, neighbours: Tensor,
+                    rast: Tensor | None = None) -> Tensor:
+    """Silhouette bits per (pos batch, triangle), uint8 (reference.py:790-814). Given rast,
+    only for the triangles it shows (antialiasing reads no others); 0 elsewhere."""
     pos3 = pos if pos.ndim == 3 else pos[None]
     pos3 = pos3.contiguous()
     mask = torch.empty(pos3.shape[0], tri.shape[0], dtype=torch.uint8, device=pos.device)
+    batch, height, width = (0, 1, 1) if rast is None else rast.shape[:3]
+    if rast is not None:
+        rast = rast.contiguous()
     call("dr_silhouette_mask", ptr(pos3), pos3.shape[1] * 4, pos3.shape[0], ptr(tri),
-         tri.shape[0], ptr(neighbours), ptr(mask), _stream(pos))
+         tri.shape[0], ptr(neighbours), ptr(rast), batch, height, width, ptr(mask), _stream(pos))
     return mask
 
 
@@ -514,5 +519,5 @@ def antialias(color: Tensor, rast: Tensor, pos: Tensor, tri: Tensor, pos_gradien
         neighbours = edge_neighbours(tri)
     neighbours = neighbours.to(torch.int32).contiguous()
     with torch.no_grad():
-        mask = silhouette_mask(pos.detach(), tri, neighbours)
+        mask = silhouette_mask(pos.detach(), tri, neighbours, rast.detach())
     return _Antialias.apply(color, rast, pos, tri, mask, float(pos_gradient_boost))

@@ -18,6 +18,8 @@
 // gathers the colour gradient the same way and sends the position gradient of each active
 // pair (two vertices; x, y and w) through the workgroup's scatter table. No pass needs a
 // colour atomic.
+#include <algorithm>
+
 #include "common.h"
 
 namespace dr {
@@ -139,12 +141,34 @@ __device__ __forceinline__ float side(const float (&line)[3], const XYW& p) {
   return v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f);
 }
 
+// Marks the triangles that rast shows (only their silhouette bits are ever read).
+constexpr uint8_t kShown = 0x80;
+
+__global__ void aa_clear_mask(uint8_t* mask, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i < n; i += (int64_t)gridDim.x * blockDim.x) mask[i] = 0;
+}
+
+__global__ __launch_bounds__(256) void aa_mark_shown(const float* rast, int64_t image_pixels,
+                                                     int64_t pixels, int num_tri, int pos_batch,
+                                                     uint8_t* mask) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= pixels) return;
+  const float id = rintf(rast[4 * i + 3]);
+  if (!(id >= 1.0f && id <= (float)num_tri)) return;
+  const int64_t row = pos_batch > 1 ? i / image_pixels : 0;
+  mask[row * num_tri + (int64_t)id - 1] = kShown;
+}
+
+// Silhouette bits of each (pos batch, triangle); with shown_only, of the marked ones only (the
+// others stay 0).
 __global__ __launch_bounds__(256) void aa_silhouette_kernel(const float* pos, int64_t stride,
                                                             int pos_batch, const int32_t* tri,
                                                             int num_tri, const int32_t* nbr,
-                                                            uint8_t* mask) {
+                                                            bool shown_only, uint8_t* mask) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (int64_t)pos_batch * num_tri) return;
+  if (shown_only && mask[i] != kShown) return;
   const int b = (int)(i / num_tri);
   const int t = (int)(i - (int64_t)b * num_tri);
   const float* P = pos + (int64_t)b * stride;
@@ -555,13 +579,24 @@ extern "C" int dr_edge_neighbours(const int32_t* tri, int32_t num_tri, void* wor
 
 extern "C" int dr_silhouette_mask(const float* pos, int64_t pos_batch_stride, int32_t pos_batch,
                                   const int32_t* tri, int32_t num_tri, const int32_t* neighbours,
+                                  const float* rast, int32_t batch, int32_t height, int32_t width,
                                   uint8_t* mask, void* stream) {
   if (pos_batch < 0 || num_tri < 0) return DR_ERR_ARGUMENT;
   const int64_t n = (int64_t)pos_batch * num_tri;
   if (n == 0) return DR_OK;
   if (!pos || !tri || !neighbours || !mask) return DR_ERR_ARGUMENT;
-  aa_silhouette_kernel<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>(
-      pos, pos_batch_stride, pos_batch, tri, num_tri, neighbours, mask);
+  hipStream_t s = (hipStream_t)stream;
+  if (rast != nullptr) {
+    if (batch < 0 || height <= 0 || width <= 0) return DR_ERR_ARGUMENT;
+    if (pos_batch > 1 && pos_batch != batch) return DR_ERR_ARGUMENT;
+    const int64_t image_pixels = (int64_t)height * width, pixels = image_pixels * batch;
+    aa_clear_mask<<<(int)std::min<int64_t>(blocks_for(n, 256), 65536), 256, 0, s>>>(mask, n);
+    if (pixels > 0)
+      aa_mark_shown<<<blocks_for(pixels, 256), 256, 0, s>>>(rast, image_pixels, pixels, num_tri,
+                                                           pos_batch, mask);
+  }
+  aa_silhouette_kernel<<<blocks_for(n, 256), 256, 0, s>>>(
+      pos, pos_batch_stride, pos_batch, tri, num_tri, neighbours, rast != nullptr, mask);
   return launch_status();
 }
 

@@ -204,9 +204,13 @@ int dr_edge_neighbours(const int32_t* tri, int32_t num_tri, void* workspace,
                        size_t workspace_bytes, int32_t* neighbours, void* stream);
 
 /* mask [pos_batch, num_tri] uint8, bit k set when edge k is a silhouette: unshared,
- * non-manifold, or folded in this projection (reference.py:790-814). */
+ * non-manifold, or folded in this projection (reference.py:790-814). With rast
+ * ([batch, height, width, 4], not NULL) only the triangles that rast shows get their bits and
+ * every other entry is 0: antialiasing reads the bits of shown triangles only
+ * (reference.py:228-258). pos_batch is 1 or batch. */
 int dr_silhouette_mask(const float* pos, int64_t pos_batch_stride, int32_t pos_batch,
                        const int32_t* tri, int32_t num_tri, const int32_t* neighbours,
+                       const float* rast, int32_t batch, int32_t height, int32_t width,
                        uint8_t* mask, void* stream);
 
 typedef struct DrAntialiasArgs {
