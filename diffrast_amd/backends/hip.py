@@ -204,6 +204,20 @@ def _interp_args(attr, rast, rast_db, tri, diff_dev, num_diff):
         width=width, num_diff=num_diff, diff=ptr(diff_dev))
 
 
+_channel_lists: dict[tuple, Tensor] = {}
+
+
+def _channel_list(channels: tuple[int, ...], device: torch.device) -> Tensor:
+    """The channel list as a device int32 tensor, made once per list and device (a fresh
+    host-to-device copy would wait for the stream before every call)."""
+    key = (channels, device)
+    found = _channel_lists.get(key)
+    if found is None:
+        found = torch.tensor(channels, dtype=torch.int32).to(device)
+        _channel_lists[key] = found
+    return found
+
+
 class _Interpolate(torch.autograd.Function):
     """(reference: _triton_interpolate.py:185-254, reference.py:117-146)"""
 
@@ -212,7 +226,7 @@ class _Interpolate(torch.autograd.Function):
         attr, rast, tri = attr.contiguous(), rast.contiguous(), tri.contiguous()
         rast_db = _dense(rast_db) if diff else None
         batch, height, width, _ = rast.shape
-        diff_dev = torch.tensor(diff, dtype=torch.int32).to(rast.device) if diff else None
+        diff_dev = _channel_list(diff, rast.device) if diff else None
         out = attr.new_empty(batch, height, width, attr.shape[-1])
         out_da = attr.new_empty(batch, height, width, 2 * len(diff))
         args = _interp_args(attr, rast, rast_db, tri, diff_dev, len(diff))
