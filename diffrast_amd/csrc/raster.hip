@@ -18,9 +18,11 @@
 //    the workgroup before one global atomic per distinct tile.
 // 3. A three-phase scan turns tile counts into list offsets and work chunks; the bin pass
 //    reserves each workgroup's share of a tile's list with one global atomic and fills it.
-// 4. One 256-thread workgroup per (tile, chunk of <= 256 triangles) stages its triangles in LDS,
-//    keeps the tile's best keys in LDS, and lets each wave sweep one triangle's box inside the
-//    tile (LDS 64-bit min), then merges the tile into the key buffer, one atomic per pixel.
+// 4. One 256-thread workgroup per (tile, chunk of <= 256 triangles) starts from the tile's keys
+//    so far, skips triangles that lie entirely behind the farthest of them, stages the others
+//    in LDS and tests the pixels of their boxes inside the tile as one flat list of work items
+//    (every lane busy whatever the box sizes), merging into the tile's keys in LDS (64-bit
+//    min); improved keys then go to the key buffer, one atomic per pixel.
 //
 // The resolve kernels turn keys into rast / rast_db (reference.py:69-114) and carry gradients
 // back to the vertices.
@@ -239,6 +241,12 @@ __device__ __forceinline__ void candidate_box(const DrRasterGeometry& g, const T
     x_hi = g.width - 1;
     y_hi = g.height - 1;
   }
+}
+
+// The depth a key holds (depth_key's inverse on the upper 32 bits).
+__device__ __forceinline__ float key_depth(uint64_t key) {
+  const uint32_t ordered = (uint32_t)(key >> 32);
+  return __uint_as_float((ordered & 0x80000000u) ? (ordered & 0x7fffffffu) : ~ordered);
 }
 
 // Merges a key into the key buffer, unless the previous layer rules it out. The atomic
@@ -737,6 +745,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   __shared__ unsigned long long s_key[kTile * kTile];
   __shared__ unsigned long long s_prev[kTile * kTile];
   __shared__ float s_px[kTile], s_py[kTile];
+  __shared__ uint64_t s_far[256 / DR_WAVE];
 
   // Neighbouring chunks (the chunks of one tile, then nearby tiles) run on one XCD and share
   // its L2.
@@ -749,16 +758,20 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
 
   const int per_image = ws.tiles_x * ws.tiles_y;
   const int b = (int)(tile / per_image);
-  const int in_image = (int)(tile - (int64_t)b * per_image);
-  const int tile_x0 = (in_image % ws.tiles_x) * kTile;
-  const int tile_y0 = (in_image / ws.tiles_x) * kTile;
+  const int tile_in_image = (int)(tile - (int64_t)b * per_image);
+  const int tile_x0 = (tile_in_image % ws.tiles_x) * kTile;
+  const int tile_y0 = (tile_in_image / ws.tiles_x) * kTile;
 
-  {  // this thread's pixel of the tile: clear its key, stage the previous layer's key
-    const int x = tile_x0 + (threadIdx.x % kTile), y = tile_y0 + (threadIdx.x / kTile);
-    s_key[threadIdx.x] = kEmptyKey;
+  // This thread's pixel of the tile: its key so far (the small-triangle pass and other chunks
+  // of this tile have already merged theirs) and the previous layer's key.
+  const int x = tile_x0 + (threadIdx.x % kTile), y = tile_y0 + (threadIdx.x / kTile);
+  const bool inside = x < g.width && y < g.height;
+  const int64_t pixel = ((int64_t)b * g.height + y) * g.width + x;
+  const uint64_t start_key = inside ? keys[pixel] : kEmptyKey;
+  {
+    s_key[threadIdx.x] = start_key;
     uint64_t floor_key = 0ull;
-    if (prev != nullptr && x < g.width && y < g.height)
-      floor_key = prev[((int64_t)b * g.height + y) * g.width + x];
+    if (prev != nullptr && inside) floor_key = prev[pixel];
     s_prev[threadIdx.x] = floor_key;
     if (threadIdx.x < kTile && tile_x0 + (int)threadIdx.x < g.width)
       s_px[threadIdx.x] = ws.px[tile_x0 + threadIdx.x];
@@ -766,6 +779,24 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
         tile_y0 + (int)threadIdx.x - 32 < g.height)
       s_py[threadIdx.x - 32] = ws.py[tile_y0 + threadIdx.x - 32];
   }
+  // The farthest key of the tile so far (pixels outside the image count as nearest). A
+  // triangle whose nearest vertex lies beyond it, by more than the rounding of the depth,
+  // cannot win any pixel of the tile and is skipped: the depth computed at a covered pixel is
+  // a convex combination of the vertex depths z_k / w_k up to a few float32 roundings
+  // (~6 * 2^-24 of the largest |z_k / w_k|), and equal depths cannot be skipped.
+  uint64_t far_key = inside ? start_key : 0ull;
+#pragma unroll
+  for (int d = 1; d < DR_WAVE; d <<= 1) {
+    const uint64_t other = __shfl_xor(far_key, d);
+    far_key = other > far_key ? other : far_key;
+  }
+  if (lane_id() == 0) s_far[threadIdx.x / DR_WAVE] = far_key;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < 256 / DR_WAVE; ++w) far_key = s_far[w] > far_key ? s_far[w] : far_key;
+  const bool cull = far_key != kEmptyKey;
+  const float far_depth = key_depth(far_key);
+
   int area = 0;
   if ((int)threadIdx.x < n) {
     const float4* rec = ws.records + (size_t)entries[first + threadIdx.x] * kRecord;
@@ -783,8 +814,15 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
     const int bx0 = max(x_lo - tile_x0, 0), bx1 = min(x_hi - tile_x0, kTile - 1);
     const int by0 = max(y_lo - tile_y0, 0), by1 = min(y_hi - tile_y0, kTile - 1);
+    bool behind = false;
+    if (cull && T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
+      const float d0 = T.z[0] / T.w[0], d1 = T.z[1] / T.w[1], d2 = T.z[2] / T.w[2];
+      const float nearest = fminf(fminf(d0, d1), d2);
+      const float scale = fmaxf(fmaxf(fabsf(d0), fabsf(d1)), fabsf(d2));
+      behind = nearest - 1e-5f * scale > far_depth;
+    }
     uint32_t box = 0u;
-    if (bx0 <= bx1 && by0 <= by1) {
+    if (bx0 <= bx1 && by0 <= by1 && !behind) {
       area = (bx1 - bx0 + 1) * (by1 - by0 + 1);
       box = pack_box(bx0, bx1 - bx0 + 1, by0, by1 - by0 + 1);
     }
@@ -835,10 +873,8 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     }
   }
   __syncthreads();
-  const int x = tile_x0 + (threadIdx.x % kTile), y = tile_y0 + (threadIdx.x / kTile);
   const uint64_t best = s_key[threadIdx.x];
-  if (best == kEmptyKey || x >= g.width || y >= g.height) return;
-  const int64_t pixel = ((int64_t)b * g.height + y) * g.width + x;
+  if (!inside || best >= start_key) return;
   atomicMin((unsigned long long*)(keys + pixel), (unsigned long long)best);
 }
 

@@ -120,6 +120,31 @@ def test_large_mesh_in_spatial_order_keeps_index_tie_break():
     assert (ids > 0).any() and not (ids > tri.shape[0] - 700).any()
 
 
+def test_triangles_behind_a_covered_tile_are_skipped_exactly():
+    # A dense front layer of small quads (drawn before the tile pass) covers every pixel; large
+    # triangles entirely behind it may be skipped, large ones that reach in front, touch its
+    # farthest depth or intersect it may not. Every layer must match the oracle.
+    gen = torch.Generator().manual_seed(23)
+    n = 20  # quads per side
+    ys, xs = torch.meshgrid(torch.linspace(-1.05, 1.05, n + 1), torch.linspace(-1.05, 1.05, n + 1),
+                            indexing="ij")
+    z = (torch.rand(n + 1, n + 1, generator=gen) - 0.5) * 0.4
+    grid = torch.stack([xs, ys, z, torch.ones_like(z)], -1).reshape(-1, 4)
+    idx = torch.arange((n + 1) * (n + 1)).view(n + 1, n + 1)
+    a, b_, c, d = idx[:-1, :-1], idx[:-1, 1:], idx[1:, :-1], idx[1:, 1:]
+    front_tri = torch.cat([torch.stack([a, b_, c], -1), torch.stack([b_, d, c], -1)]).view(-1, 3)
+    behind, _ = random_mesh(150, gen, z_range=1.0, xy_range=1.0)
+    behind[..., 2] = (0.3 + 0.6 * torch.rand(behind.shape[1], generator=gen)) * behind[..., 3]
+    across, _ = random_mesh(60, gen, z_range=0.5, xy_range=1.0)
+    touching, _ = random_mesh(20, gen, xy_range=1.0)
+    touching[..., 2] = z.max() * touching[..., 3]
+    extra = torch.cat([behind[0], across[0], touching[0]])
+    pos = torch.cat([grid, extra])[None]
+    tri = torch.cat([front_tri.to(torch.int32),
+                     (torch.arange(extra.shape[0]) + grid.shape[0]).view(-1, 3).to(torch.int32)])
+    assert_layers_match(pos, tri, (64, 64), count=3)
+
+
 def test_subdivided_sphere_in_spatial_order():
     from diffrast_amd import workloads as W
     gen = torch.Generator().manual_seed(22)
