@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent.parent / "libdiffrast_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 MAX_LEVELS = 32
 
 c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -33,6 +33,8 @@ class RasterGeometry(ctypes.Structure):
         ("ranges", c_void_p),
         ("range_prefix", c_void_p),
         ("num_instances", ctypes.c_int64),
+        ("num_vertices", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 

@@ -76,6 +76,7 @@ class _Geometry:
             ranges=ptr(ranges),
             range_prefix=ptr(range_prefix),
             num_instances=int(num_instances if num_instances is not None else self.batch * num_tri),
+            num_vertices=int(pos.shape[-2]),
         )
         self.shape = (self.batch, int(height), int(width))
 

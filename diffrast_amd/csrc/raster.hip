@@ -39,16 +39,23 @@ constexpr int kOrderBuckets = 4096;  // Morton buckets (12 bits of a 30-bit code
 constexpr int kOrderMinTris = 8192;  // smaller meshes keep their own order
 constexpr int kTileSlots = 1024;     // LDS table of a workgroup's tiles
 constexpr int kRecord = 4;           // float4 per binned triangle record (one 64-byte line)
+constexpr int kDepthSlabs = 16;      // tile lists per tile, by the triangle's nearest depth
+constexpr int kRangeParts = 64;      // workgroups per image in the depth span reduction
 constexpr float kAreaTolerance = 2.384185791015625e-07f;  // 2 * float32 epsilon
 
 struct Workspace {
   float4* records;           // binned triangles, kRecord float4 each: the three clip-space
                              // vertices, then the bits of (image, row, tx0 | tx1 << 16,
                              // ty0 | ty1 << 16)
-  uint32_t* tile_counts;     // [tiles + 1]
-  uint32_t* tile_offsets;    // [tiles + 1] exclusive prefix of tile_counts
-  uint32_t* tile_cursor;     // [tiles + 1] fill positions of the bin pass
-  uint32_t* chunk_offsets;   // [tiles + 1] exclusive prefix of ceil(count / kChunk)
+  // Tile lists: list slab * tiles + tile holds the binned triangles of that tile whose nearest
+  // depth falls in depth slab `slab` of their image, so lists run near to far.
+  uint32_t* list_counts;     // [lists + 1]
+  uint32_t* list_offsets;    // [lists + 1] exclusive prefix of list_counts
+  uint32_t* list_cursor;     // [lists + 1] fill positions of the bin pass
+  uint32_t* chunk_offsets;   // [lists + 1] exclusive prefix of ceil(count / kChunk)
+  uint32_t* depth_range;     // [depth_ranges][2] order-preserving bits of the nearest and
+                             // farthest vertex depth of an image (one when pos is shared)
+  uint32_t* range_parts;     // [depth_ranges][kRangeParts][2] partial spans
   uint2* block_sums;         // [scan blocks] (entries, chunks)
   uint32_t* counters;        // [1] entries, [2] chunks
   uint32_t* block_records;   // [record_blocks] binned triangles of each setup workgroup
@@ -62,6 +69,8 @@ struct Workspace {
   bool ordered;
   int tiles_x, tiles_y;
   int64_t tiles;
+  int64_t lists;
+  int depth_ranges;
   int scan_blocks;
   int record_blocks;          // setup workgroups; each owns 256 record slots
   size_t bytes;
@@ -78,7 +87,9 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
   w.tiles_x = (g.width + kTile - 1) / kTile;
   w.tiles_y = (g.height + kTile - 1) / kTile;
   w.tiles = (int64_t)g.batch * w.tiles_x * w.tiles_y;
-  w.scan_blocks = (int)((w.tiles + 1 + kScanBlock - 1) / kScanBlock);
+  w.lists = w.tiles * kDepthSlabs;
+  w.scan_blocks = (int)((w.lists + 1 + kScanBlock - 1) / kScanBlock);
+  w.depth_ranges = (g.ranges == nullptr && g.pos_batch_stride != 0) ? std::max(g.batch, 1) : 1;
   w.ordered = use_order(g);
   w.record_blocks = std::max(blocks_for(g.num_instances, 256), 1);
   size_t off = 0;
@@ -88,10 +99,12 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
     return p;
   };
   w.counters = (uint32_t*)take(16);
-  w.tile_counts = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
-  w.tile_offsets = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
-  w.tile_cursor = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
-  w.chunk_offsets = (uint32_t*)take(sizeof(uint32_t) * (w.tiles + 1));
+  w.list_counts = (uint32_t*)take(sizeof(uint32_t) * (w.lists + 1));
+  w.list_offsets = (uint32_t*)take(sizeof(uint32_t) * (w.lists + 1));
+  w.list_cursor = (uint32_t*)take(sizeof(uint32_t) * (w.lists + 1));
+  w.chunk_offsets = (uint32_t*)take(sizeof(uint32_t) * (w.lists + 1));
+  w.depth_range = (uint32_t*)take(sizeof(uint32_t) * 2 * w.depth_ranges);
+  w.range_parts = (uint32_t*)take(sizeof(uint32_t) * 2 * kRangeParts * w.depth_ranges);
   w.block_sums = (uint2*)take(sizeof(uint2) * (w.scan_blocks + 1));
   w.block_records = (uint32_t*)take(sizeof(uint32_t) * w.record_blocks);
   w.px = (float*)take(sizeof(float) * g.width);
@@ -443,6 +456,74 @@ __global__ __launch_bounds__(256) void order_place(DrRasterGeometry g, Workspace
   if (t < g.num_tri) ws.order[base[bucket] + atomicAdd(hist + bucket, 1u)] = (uint32_t)t;
 }
 
+// ---- kernels: depth range ----------------------------------------------------------------
+
+// Nearest and farthest depth z / w, clipped to [-1, 1], of the vertices in front of the camera,
+// per image (or once when pos is shared): the span the depth slabs divide. Each of
+// kRangeParts workgroups per image reduces a share of its vertices to a partial span; a second
+// pass merges the partial spans (no atomics on a handful of addresses).
+__global__ __launch_bounds__(256) void raster_depth_range(DrRasterGeometry g, Workspace ws) {
+  __shared__ uint32_t s_lo[256 / DR_WAVE], s_hi[256 / DR_WAVE];
+  const int image = blockIdx.x / kRangeParts, part = blockIdx.x % kRangeParts;
+  const float* P = g.pos + (int64_t)image * g.pos_batch_stride;
+  uint32_t lo = 0xffffffffu, hi = 0u;
+  for (int v = part * blockDim.x + threadIdx.x; v < g.num_vertices;
+       v += kRangeParts * blockDim.x) {
+    const float4 p = load4(P + 4 * (int64_t)v);
+    const float d = p.z / p.w;
+    if (p.w > 0.0f && isfinite(d)) {
+      const uint32_t bits = ordered_bits(fminf(fmaxf(d, -1.0f), 1.0f));
+      lo = min(lo, bits);
+      hi = max(hi, bits);
+    }
+  }
+#pragma unroll
+  for (int d = 1; d < DR_WAVE; d <<= 1) {
+    lo = min(lo, (uint32_t)__shfl_xor(lo, d));
+    hi = max(hi, (uint32_t)__shfl_xor(hi, d));
+  }
+  if (lane_id() == 0) {
+    s_lo[threadIdx.x / DR_WAVE] = lo;
+    s_hi[threadIdx.x / DR_WAVE] = hi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 256 / DR_WAVE; ++w) {
+      lo = min(lo, s_lo[w]);
+      hi = max(hi, s_hi[w]);
+    }
+    ws.range_parts[2 * blockIdx.x] = lo;
+    ws.range_parts[2 * blockIdx.x + 1] = hi;
+  }
+}
+
+__global__ __launch_bounds__(kRangeParts) void raster_depth_range_merge(Workspace ws) {
+  const int image = blockIdx.x;
+  uint32_t lo = ws.range_parts[2 * (image * kRangeParts + threadIdx.x)];
+  uint32_t hi = ws.range_parts[2 * (image * kRangeParts + threadIdx.x) + 1];
+#pragma unroll
+  for (int d = 1; d < kRangeParts; d <<= 1) {
+    lo = min(lo, (uint32_t)__shfl_xor(lo, d));
+    hi = max(hi, (uint32_t)__shfl_xor(hi, d));
+  }
+  if (threadIdx.x == 0) {
+    ws.depth_range[2 * image] = lo;
+    ws.depth_range[2 * image + 1] = hi;
+  }
+}
+
+// Depth slab of a binned triangle: its nearest vertex depth's place in the image's depth span.
+// Triangles that cross the camera plane go first (slab 0).
+__device__ __forceinline__ int depth_slab(const Workspace& ws, int range, const Tri& T) {
+  if (!(T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f)) return 0;
+  const float nearest = fminf(fminf(T.z[0] / T.w[0], T.z[1] / T.w[1]), T.z[2] / T.w[2]);
+  const float lo = from_ordered_bits(ws.depth_range[2 * range]);
+  const float hi = from_ordered_bits(ws.depth_range[2 * range + 1]);
+  const float f = (nearest - lo) / (hi - lo) * (float)kDepthSlabs;
+  if (!(hi > lo) || !isfinite(f)) return 0;
+  return min(max((int)f, 0), kDepthSlabs - 1);
+}
+
 // ---- kernels: setup, scan, bin, tiles -----------------------------------------------------
 
 // Splits work item p of a box bw pixels wide (bw <= 16, p < 256) into (dx, dy). The float
@@ -559,27 +640,28 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
       const uint32_t rec = (uint32_t)(block * 256 + before) +
                            (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
       const int tx0 = x_lo / kTile, tx1 = x_hi / kTile, ty0 = y_lo / kTile, ty1 = y_hi / kTile;
+      const int slab = depth_slab(ws, ws.depth_ranges > 1 ? b : 0, T);
       float4* out = ws.records + (size_t)rec * kRecord;
 #pragma unroll
       for (int k = 0; k < 3; ++k) out[k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
-      out[3] = make_float4(__int_as_float(b), __int_as_float(t),
+      out[3] = make_float4(__int_as_float(b), __int_as_float(t | (slab << 24)),
                            __uint_as_float((uint32_t)tx0 | ((uint32_t)tx1 << 16)),
                            __uint_as_float((uint32_t)ty0 | ((uint32_t)ty1 << 16)));
-      const uint32_t image_tiles = (uint32_t)b * ws.tiles_x * ws.tiles_y;
+      const uint32_t list_base = (uint32_t)(slab * ws.tiles) + (uint32_t)b * ws.tiles_x * ws.tiles_y;
       for (int ty = ty0; ty <= ty1; ++ty)
         for (int tx = tx0; tx <= tx1; ++tx) {
-          const uint32_t tile = image_tiles + ty * ws.tiles_x + tx;
-          const int slot = table.insert(tile);
+          const uint32_t list = list_base + ty * ws.tiles_x + tx;
+          const int slot = table.insert(list);
           if (slot >= 0)
             atomicAdd(table.count + slot, 1u);
           else
-            atomicAdd(ws.tile_counts + tile, 1u);
+            atomicAdd(ws.list_counts + list, 1u);
         }
     }
   }
   __syncthreads();
   for (int s = threadIdx.x; s < kTileSlots; s += blockDim.x)
-    if (table.key[s] != TileTable::kEmpty) atomicAdd(ws.tile_counts + table.key[s], table.count[s]);
+    if (table.key[s] != TileTable::kEmpty) atomicAdd(ws.list_counts + table.key[s], table.count[s]);
 }
 
 // Inclusive scan of (entries, chunks) pairs over the 256 threads of a block.
@@ -695,7 +777,9 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
     tx1 = (int)(rx >> 16);
     ty0 = (int)(ry & 0xffffu);
     ty1 = (int)(ry >> 16);
-    image_tiles = (uint32_t)__float_as_int(rec.x) * ws.tiles_x * ws.tiles_y;
+    const uint32_t slab = __float_as_uint(rec.y) >> 24;
+    image_tiles = (uint32_t)(slab * ws.tiles) +
+                  (uint32_t)__float_as_int(rec.x) * ws.tiles_x * ws.tiles_y;
   }
   for (int ty = ty0; ty <= ty1; ++ty)
     for (int tx = tx0; tx <= tx1; ++tx) {
@@ -705,7 +789,7 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
   __syncthreads();
   for (int s = threadIdx.x; s < kTileSlots; s += blockDim.x) {
     if (table.key[s] != TileTable::kEmpty)
-      table.base[s] = atomicAdd(ws.tile_cursor + table.key[s], table.count[s]);
+      table.base[s] = atomicAdd(ws.list_cursor + table.key[s], table.count[s]);
     table.count[s] = 0u;
   }
   __syncthreads();
@@ -714,17 +798,17 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
       const uint32_t tile = image_tiles + ty * ws.tiles_x + tx;
       const int slot = table.find(tile);
       const uint32_t at = slot >= 0 ? table.base[slot] + atomicAdd(table.count + slot, 1u)
-                                    : atomicAdd(ws.tile_cursor + tile, 1u);
+                                    : atomicAdd(ws.list_cursor + tile, 1u);
       entries[at] = r;
     }
 }
 
-// The tile of every work chunk: chunk_tile[c] = t for the chunks of tile t.
-__global__ __launch_bounds__(256) void raster_chunk_tiles(Workspace ws, uint32_t* chunk_tile) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= ws.tiles) return;
-  for (uint32_t c = ws.chunk_offsets[t]; c < ws.chunk_offsets[t + 1]; ++c)
-    chunk_tile[c] = (uint32_t)t;
+// The list of every work chunk: chunk_list[c] = l for the chunks of list l.
+__global__ __launch_bounds__(256) void raster_chunk_tiles(Workspace ws, uint32_t* chunk_list) {
+  const int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (l >= ws.lists) return;
+  for (uint32_t c = ws.chunk_offsets[l]; c < ws.chunk_offsets[l + 1]; ++c)
+    chunk_list[c] = (uint32_t)l;
 }
 
 // One workgroup per (tile, chunk of up to kChunk binned triangles). The chunk's triangles and
@@ -747,13 +831,14 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   __shared__ float s_px[kTile], s_py[kTile];
   __shared__ uint64_t s_far[256 / DR_WAVE];
 
-  // Neighbouring chunks (the chunks of one tile, then nearby tiles) run on one XCD and share
-  // its L2.
-  const uint32_t work = (uint32_t)xcd_order(blockIdx.x, gridDim.x);
-  const int64_t tile = chunk_tile[work];
-  const uint32_t chunk = work - ws.chunk_offsets[tile];
-  const uint32_t first = ws.tile_offsets[tile] + chunk * kChunk;
-  const uint32_t end = min(ws.tile_offsets[tile + 1], first + kChunk);
+  // Chunks run in list order, so the near slabs of every tile are (mostly) merged into the key
+  // buffer before the far ones start, and those can skip what lies behind.
+  const uint32_t work = blockIdx.x;
+  const int64_t list = chunk_tile[work];
+  const int64_t tile = list % ws.tiles;
+  const uint32_t chunk = work - ws.chunk_offsets[list];
+  const uint32_t first = ws.list_offsets[list] + chunk * kChunk;
+  const uint32_t end = min(ws.list_offsets[list + 1], first + kChunk);
   const int n = (int)(end - first);
 
   const int per_image = ws.tiles_x * ws.tiles_y;
@@ -827,7 +912,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
       box = pack_box(bx0, bx1 - bx0 + 1, by0, by1 - by0 + 1);
     }
     s_tri[threadIdx.x][3] = make_float4(reach(T.x, T.w), reach(T.y, T.w),
-                                        __int_as_float(__float_as_int(rec[3].y)),
+                                        __int_as_float(__float_as_int(rec[3].y) & 0xffffff),
                                         __uint_as_float(box));
   }
   // Exclusive prefix of the areas over the workgroup.
@@ -1070,7 +1155,9 @@ static bool valid_geometry(const DrRasterGeometry* g) {
   if (!g || g->batch < 0 || g->num_tri < 0 || g->height <= 0 || g->width <= 0) return false;
   if ((g->batch > 0 && g->num_tri > 0) && (!g->pos || !g->tri)) return false;
   if (g->ranges && !g->range_prefix) return false;
-  if (g->num_tri > (1 << 24) || g->num_instances < 0) return false;
+  if (g->num_tri > (1 << 24) || g->num_instances < 0 || g->num_vertices < 0) return false;
+  // Per-image vertex arrays hold pos_batch_stride / 4 vertices.
+  if (g->pos_batch_stride != 0 && g->pos_batch_stride < 4 * (int64_t)g->num_vertices) return false;
   // Tile coordinates are stored in 16 bits.
   if ((g->width + 15) / 16 > 0xffff || (g->height + 15) / 16 > 0xffff) return false;
   return true;
@@ -1094,12 +1181,12 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   // Record slots (256 per setup workgroup) and tiles are indexed with 32 bits.
-  if (g->num_instances > ((int64_t)1 << 32) - 512 || ws.tiles >= (int64_t)1 << 32)
+  if (g->num_instances > ((int64_t)1 << 32) - 512 || ws.lists >= ((int64_t)1 << 32) - 1)
     return DR_ERR_ARGUMENT;
   const int fill_blocks = (int)std::min<int64_t>(blocks_for(pixels, 256), 65536);
   raster_fill_keys<<<fill_blocks, 256, 0, s>>>(keys, pixels);
-  raster_fill_u32<<<(int)std::min<int64_t>(blocks_for(ws.tiles + 1, 256), 65536), 256, 0, s>>>(
-      ws.tile_counts, ws.tiles + 1, 0u);
+  raster_fill_u32<<<(int)std::min<int64_t>(blocks_for(ws.lists + 1, 256), 65536), 256, 0, s>>>(
+      ws.list_counts, ws.lists + 1, 0u);
   raster_fill_u32<<<1, 64, 0, s>>>(ws.counters, 4, 0u);
   raster_centres<<<blocks_for(std::max(g->width, g->height), 256), 256, 0, s>>>(
       ws.px, g->width, ws.py, g->height);
@@ -1115,12 +1202,14 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
       order_scan<<<1, 256, 0, s>>>(ws);
       order_place<<<tri_blocks, 256, 0, s>>>(*g, ws);
     }
+    raster_depth_range<<<ws.depth_ranges * kRangeParts, 256, 0, s>>>(*g, ws);
+    raster_depth_range_merge<<<ws.depth_ranges, kRangeParts, 0, s>>>(ws);
     raster_setup_kernel<<<blocks_for(g->num_instances, 256), 256, 0, s>>>(*g, prev_keys, keys,
                                                                           ws);
-    raster_scan_reduce<<<ws.scan_blocks, 256, 0, s>>>(ws.tile_counts, ws.tiles, ws.block_sums);
+    raster_scan_reduce<<<ws.scan_blocks, 256, 0, s>>>(ws.list_counts, ws.lists, ws.block_sums);
     raster_scan_blocks<<<1, 256, 0, s>>>(ws.block_sums, ws.scan_blocks, ws.counters);
-    raster_scan_apply<<<ws.scan_blocks, 256, 0, s>>>(ws.tile_counts, ws.tiles, ws.block_sums,
-                                                     ws.tile_offsets, ws.tile_cursor,
+    raster_scan_apply<<<ws.scan_blocks, 256, 0, s>>>(ws.list_counts, ws.lists, ws.block_sums,
+                                                     ws.list_offsets, ws.list_cursor,
                                                      ws.chunk_offsets);
   }
   int status = launch_status();
@@ -1145,7 +1234,7 @@ extern "C" int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspa
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
   raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, entries);
-  raster_chunk_tiles<<<blocks_for(ws.tiles, 256), 256, 0, s>>>(ws, entries + counts[1]);
+  raster_chunk_tiles<<<blocks_for(ws.lists, 256), 256, 0, s>>>(ws, entries + counts[1]);
   return launch_status();
 }
 

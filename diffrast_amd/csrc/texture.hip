@@ -12,6 +12,8 @@
 // The backward pass writes the coordinate, derivative and bias gradients per pixel and adds
 // texel gradients with fp32 atomics. The mip chain is built level by level with exact area
 // weights (reference.py:449-488), and its adjoint is a gather, so it needs no atomics.
+#include <type_traits>
+
 #include "common.h"
 
 namespace dr {
@@ -196,9 +198,15 @@ __device__ __forceinline__ Axis texel_axis(float coord, int size, float shift, i
   return A;
 }
 
+// i mod n (non-negative). Tap positions come from coordinates already wrapped into [0, 1], so
+// they lie in [-1, n]: one add or subtract; the division is left for anything else.
 __device__ __forceinline__ int wrap_index(int i, int n) {
-  int r = i % n;
-  return r < 0 ? r + n : r;
+  int r = i < 0 ? i + n : (i >= n ? i - n : i);
+  if (r < 0 || r >= n) {
+    r = i % n;
+    r = r < 0 ? r + n : r;
+  }
+  return r;
 }
 
 // Texel index (in texels from the start of the image's packed buffer) of integer tap
@@ -262,10 +270,23 @@ __device__ __forceinline__ Bilinear bilinear_setup(float s, float t, int face, i
   return L;
 }
 
-__device__ __forceinline__ void fetch4(const float* texels, const Bilinear& L, int C, int c,
-                                       float (&t)[4]) {
+// Channels [c0, c0 + N) of the four taps (0 past C or for an invalid tap), all loads issued
+// together.
+template <int N>
+__device__ __forceinline__ void fetch_taps(const float* __restrict__ texels, const Bilinear& L,
+                                           int C, int c0, float (&t)[4][N]) {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) t[k] = L.valid[k] ? texels[L.index[k] * C + c] : 0.0f;
+  for (int k = 0; k < 4; ++k) {
+    const float* row = texels + L.index[k] * C + c0;
+#pragma unroll
+    for (int c = 0; c < N; ++c) t[k][c] = (L.valid[k] && c0 + c < C) ? row[c] : 0.0f;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void tap_column(const float (&t)[4][N], int c, float (&out)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) out[k] = t[k][c];
 }
 
 // Value of one channel (reference.py:601-611).
@@ -437,7 +458,10 @@ __device__ __forceinline__ bool nearest_setup(const DrTextureArgs& a, const Look
   return X.bad || Y.bad;
 }
 
-__global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* out) {
+// NC channels per pass (the channel count when it is 1-4; 4 with a loop for more). Every tap
+// of a pass is loaded before its stores.
+template <int NC>
+__global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* __restrict__ out) {
   const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (pixel >= (int64_t)a.batch * a.height * a.width) return;
   const int C = a.channels;
@@ -449,7 +473,7 @@ __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* ou
     return;
   }
   const int64_t image = pixel / ((int64_t)a.height * a.width);
-  const float* texels = a.texels + (a.tex_batch > 1 ? image * a.num_texels * C : 0);
+  const float* __restrict__ texels = a.texels + (a.tex_batch > 1 ? image * a.num_texels * C : 0);
   const float nan = __int_as_float(0x7fc00000);
   if (K.levels == 0) {
     int64_t index;
@@ -458,41 +482,59 @@ __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* ou
     for (int c = 0; c < C; ++c) o[c] = bad ? nan : (valid ? texels[index * C + c] : 0.0f);
     return;
   }
-  Bilinear L0 = level_setup(a, K, 0);
-  bool bad = K.bad || L0.bad;
-  if (K.levels == 1) {
-    for (int c = 0; c < C; ++c) {
-      float t[4];
-      fetch4(texels, L0, C, c, t);
-      o[c] = bad ? nan : bilinear_value(L0, t);
-    }
-    return;
-  }
-  Bilinear L1 = level_setup(a, K, 1);
-  bad = bad || L1.bad;
+  const Bilinear L0 = level_setup(a, K, 0);
+  const bool two = K.levels == 2;
+  const Bilinear L1 = two ? level_setup(a, K, 1) : L0;
+  const bool bad = K.bad || L0.bad || (two && L1.bad);
   const float frac = K.level_weight[1];
-  for (int c = 0; c < C; ++c) {
-    float t[4], u[4];
-    fetch4(texels, L0, C, c, t);
-    fetch4(texels, L1, C, c, u);
-    o[c] = bad ? nan : bilinear_value(L0, t) * (1.0f - frac) + bilinear_value(L1, u) * frac;
+  for (int c0 = 0; c0 < C; c0 += NC) {
+    float t[4][NC], u[4][NC];
+    fetch_taps<NC>(texels, L0, C, c0, t);
+    if (two) fetch_taps<NC>(texels, L1, C, c0, u);
+    float res[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float tc[4], uc[4];
+      tap_column(t, c, tc);
+      if (two) {
+        tap_column(u, c, uc);
+        res[c] = bilinear_value(L0, tc) * (1.0f - frac) + bilinear_value(L1, uc) * frac;
+      } else {
+        res[c] = bilinear_value(L0, tc);
+      }
+      if (bad) res[c] = nan;
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      if (c0 + c < C) o[c0 + c] = res[c];
   }
 }
 
 // Coordinate-gradient contributions of one level: d/dfx, d/dfy summed over channels with the
 // level weight, and the level's value per channel for the blend-factor gradient.
-__device__ __forceinline__ void level_coordinate_grads(const Bilinear& L, const float* texels,
-                                                       const float* g, int C, float level_weight,
-                                                       float& g_fx, float& g_fy,
-                                                       bool want_value, float& g_value) {
-  for (int c = 0; c < C; ++c) {
-    float t[4], wgt[4], dfx, dfy;
-    fetch4(texels, L, C, c, t);
-    bilinear_grad(L, t, wgt, dfx, dfy);
-    const float gl = g[c] * level_weight;
-    g_fx += gl * dfx;
-    g_fy += gl * dfy;
-    if (want_value) g_value += g[c] * bilinear_value(L, t);
+template <int N>
+__device__ __forceinline__ void level_coordinate_grads(const Bilinear& L,
+                                                       const float* __restrict__ texels,
+                                                       const float* __restrict__ g, int C,
+                                                       float level_weight, float& g_fx,
+                                                       float& g_fy, bool want_value,
+                                                       float& g_value) {
+  for (int c0 = 0; c0 < C; c0 += N) {
+    float t[4][N], gc[N];
+    fetch_taps<N>(texels, L, C, c0, t);
+#pragma unroll
+    for (int c = 0; c < N; ++c) gc[c] = c0 + c < C ? g[c0 + c] : 0.0f;
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+      if (c0 + c >= C) continue;
+      float tc[4], wgt[4], dfx, dfy;
+      tap_column(t, c, tc);
+      bilinear_grad(L, tc, wgt, dfx, dfy);
+      const float gl = gc[c] * level_weight;
+      g_fx += gl * dfx;
+      g_fy += gl * dfy;
+      if (want_value) g_value += gc[c] * bilinear_value(L, tc);
+    }
   }
 }
 
@@ -507,6 +549,7 @@ __device__ __forceinline__ void level_taps(const Bilinear& L, float level_weight
   }
 }
 
+template <int NC>
 __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const float* grad_out,
                                                       float* grad_texels, float* grad_uv,
                                                       float* grad_uv_da, float* grad_bias) {
@@ -554,12 +597,12 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
       live = false;
     } else {
       float fx0 = 0.f, fy0 = 0.f, fx1 = 0.f, fy1 = 0.f, v0 = 0.f, v1 = 0.f;
-      level_coordinate_grads(L0, texels, g, C, K.level_weight[0], fx0, fy0, two, v0);
+      level_coordinate_grads<NC>(L0, texels, g, C, K.level_weight[0], fx0, fy0, two, v0);
       level_taps(L0, K.level_weight[0], tex_off, tap_index, tap_weight);
       if (L0.pass_x) g_s += fx0 * L0.size_x;
       if (L0.pass_y) g_t += fy0 * L0.size_y;
       if (two) {
-        level_coordinate_grads(L1, texels, g, C, K.level_weight[1], fx1, fy1, true, v1);
+        level_coordinate_grads<NC>(L1, texels, g, C, K.level_weight[1], fx1, fy1, true, v1);
         level_taps(L1, K.level_weight[1], tex_off, tap_index + 4, tap_weight + 4);
         if (L1.pass_x) g_s += fx1 * L1.size_x;
         if (L1.pass_y) g_t += fy1 * L1.size_y;
@@ -742,6 +785,17 @@ bool valid_args(const DrTextureArgs* a) {
   return true;
 }
 
+// Kernels templated on NC channels per pass: 1-4 as they are, more in passes of 4.
+template <typename F>
+int dispatch_channels(int channels, F f) {
+  switch (channels) {
+    case 1: return f(std::integral_constant<int, 1>());
+    case 2: return f(std::integral_constant<int, 2>());
+    case 3: return f(std::integral_constant<int, 3>());
+    default: return f(std::integral_constant<int, 4>());
+  }
+}
+
 }  // namespace
 }  // namespace dr
 
@@ -751,8 +805,12 @@ extern "C" int dr_texture_forward(const DrTextureArgs* a, float* out, void* stre
   if (!valid_args(a) || !out) return DR_ERR_ARGUMENT;
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0) return DR_OK;
-  tex_fwd_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(*a, out);
-  return launch_status();
+  const DrTextureArgs args = *a;
+  return dispatch_channels(args.channels, [&](auto nc) {
+    tex_fwd_kernel<decltype(nc)::value>
+        <<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(args, out);
+    return launch_status();
+  });
 }
 
 extern "C" int dr_texture_backward(const DrTextureArgs* a, const float* grad_out,
@@ -762,10 +820,14 @@ extern "C" int dr_texture_backward(const DrTextureArgs* a, const float* grad_out
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0) return DR_OK;
   if ((int64_t)a->tex_batch * a->num_texels >= 0xffffffffLL) return DR_ERR_ARGUMENT;
-  tex_bwd_kernel<<<tile_blocks(a->batch, a->height, a->width), 256, 0, (hipStream_t)stream>>>(
-      *a, grad_out, grad_texels, grad_uv, a->uv_da ? grad_uv_da : nullptr,
-      a->bias ? grad_bias : nullptr);
-  return launch_status();
+  const DrTextureArgs args = *a;
+  return dispatch_channels(args.channels, [&](auto nc) {
+    tex_bwd_kernel<decltype(nc)::value>
+        <<<tile_blocks(args.batch, args.height, args.width), 256, 0, (hipStream_t)stream>>>(
+            args, grad_out, grad_texels, grad_uv, args.uv_da ? grad_uv_da : nullptr,
+            args.bias ? grad_bias : nullptr);
+    return launch_status();
+  });
 }
 
 extern "C" int dr_mip_build(float* texels, int32_t tex_batch, int32_t channels,

@@ -64,6 +64,8 @@ typedef struct DrRasterGeometry {
                                   (start, count) per image, on the device (range mode) */
   const int64_t* range_prefix; /* with ranges: [batch + 1] exclusive prefix sum of counts */
   int64_t num_instances;       /* batch * num_tri, or range_prefix[batch] */
+  int32_t num_vertices;        /* vertices per image in pos */
+  int32_t reserved;            /* 0 */
 } DrRasterGeometry;
 
 /* Bytes of the visibility workspace for this geometry. */

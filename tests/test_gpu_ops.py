@@ -159,6 +159,35 @@ def test_texture_gradients(filter_mode, boundary):
     assert_grads_close(ours[1], ref[1], tol=1e-3)
 
 
+@pytest.mark.parametrize("boundary", ["wrap", "clamp", "zero"])
+@pytest.mark.parametrize("filter_mode", ["linear", "linear-mipmap-nearest", "linear-mipmap-linear"])
+@pytest.mark.parametrize("channels", [3, 6])
+def test_texture_gradients_smooth_mapping(filter_mode, boundary, channels):
+    # uv varies smoothly over the image, so most tiles' taps fit the dense per-level texel
+    # windows; the mapping crosses the wrap seam and the texture's edges, and the footprint
+    # (hence the level) grows across the image, so some tiles take the hash table instead.
+    gen = torch.Generator().manual_seed(11)
+    H, W = 72, 88
+    tex = torch.randn(1, 64, 48, channels, generator=gen)
+    yy, xx = torch.meshgrid(torch.arange(H, dtype=torch.float32),
+                            torch.arange(W, dtype=torch.float32), indexing="ij")
+    scale = 0.6 + 2.5 * xx / W  # texels per pixel grows left to right
+    u = -0.15 + xx * scale / 48 + 0.02 * torch.sin(yy / 5)
+    v = -0.1 + yy * 0.9 / 64 + 0.01 * torch.cos(xx / 7)
+    uv = torch.stack([u, v], -1)[None].repeat(2, 1, 1, 1)
+    uv[1] = uv[1].flip(1) * 0.7 + 0.2
+    da = torch.stack([scale / 48, 0.002 * torch.ones_like(u), 0.001 * torch.ones_like(u),
+                      0.9 / 64 * torch.ones_like(u)], -1)[None].repeat(2, 1, 1, 1)
+    mip = "mipmap" in filter_mode
+    weights = torch.randn(2, H, W, channels, generator=gen)
+    ref = grads_of(lambda t, c, d: R.texture(t, c, d if mip else None, filter_mode, boundary,
+                                             None), [tex, uv, da], [weights], "cpu")
+    ours = grads_of(lambda t, c, d: hip.texture(t, c, d if mip else None, filter_mode,
+                                                boundary, None), [tex, uv, da], [weights], "cuda")
+    assert rel_error(ours[0][0], ref[0][0]) < VALUE_TOL
+    assert_grads_close(ours[1][:1], ref[1][:1], tol=1e-3)
+
+
 @pytest.mark.parametrize("pattern", ["constant", "magnified", "mixed"])
 @pytest.mark.parametrize("filter_mode", FILTERS)
 def test_texture_gradients_where_pixels_share_texels(filter_mode, pattern):
