@@ -830,6 +830,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   __shared__ unsigned long long s_prev[kTile * kTile];
   __shared__ float s_px[kTile], s_py[kTile];
   __shared__ uint64_t s_far[256 / DR_WAVE];
+  __shared__ float s_bound[kChunk];  // lower bound of each staged triangle's depth
 
   // Chunks run in list order, so the near slabs of every tile are (mostly) merged into the key
   // buffer before the far ones start, and those can skip what lies behind.
@@ -866,9 +867,10 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   }
   // The farthest key of the tile so far (pixels outside the image count as nearest). A
   // triangle whose nearest vertex lies beyond it, by more than the rounding of the depth,
-  // cannot win any pixel of the tile and is skipped: the depth computed at a covered pixel is
-  // a convex combination of the vertex depths z_k / w_k up to a few float32 roundings
-  // (~6 * 2^-24 of the largest |z_k / w_k|), and equal depths cannot be skipped.
+  // cannot win any pixel of the tile and is skipped; the same bound skips single pixels that
+  // already hold a nearer key. The depth computed at a covered pixel is a convex combination
+  // of the vertex depths z_k / w_k up to a few float32 roundings (~6 * 2^-24 of the largest
+  // |z_k / w_k|; the margin is 1e-5 of it), and equal depths are never skipped.
   uint64_t far_key = inside ? start_key : 0ull;
 #pragma unroll
   for (int d = 1; d < DR_WAVE; d <<= 1) {
@@ -899,13 +901,17 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
     const int bx0 = max(x_lo - tile_x0, 0), bx1 = min(x_hi - tile_x0, kTile - 1);
     const int by0 = max(y_lo - tile_y0, 0), by1 = min(y_hi - tile_y0, kTile - 1);
-    bool behind = false;
-    if (cull && T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
+    // A lower bound of the triangle's depth at any pixel it covers (-inf when it crosses the
+    // camera plane).
+    float bound = -__int_as_float(0x7f800000);
+    if (T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
       const float d0 = T.z[0] / T.w[0], d1 = T.z[1] / T.w[1], d2 = T.z[2] / T.w[2];
       const float nearest = fminf(fminf(d0, d1), d2);
       const float scale = fmaxf(fmaxf(fabsf(d0), fabsf(d1)), fabsf(d2));
-      behind = nearest - 1e-5f * scale > far_depth;
+      bound = nearest - 1e-5f * scale;
     }
+    s_bound[threadIdx.x] = bound;
+    const bool behind = cull && bound > far_depth;
     uint32_t box = 0u;
     if (bx0 <= bx1 && by0 <= by1 && !behind) {
       area = (bx1 - bx0 + 1) * (by1 - by0 + 1);
@@ -948,12 +954,14 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     int dx, dy;
     box_cell(item - s_start[j], bw, dx, dy);
     const int lx = (int)(box & 0xff) + dx, ly = (int)((box >> 16) & 0xff) + dy;
+    const int p = ly * kTile + lx;
+    // Early depth test: the pixel already holds a nearer key (NaN for an empty one: no skip).
+    if (s_bound[j] > key_depth(s_key[p])) continue;
     const float X[3] = {v0.x, v1.x, v2.x}, Y[3] = {v0.y, v1.y, v2.y};
     const float Z[3] = {v0.z, v1.z, v2.z}, Wv[3] = {v0.w, v1.w, v2.w};
     float depth;
     if (covers(X, Y, Z, Wv, extra.x, extra.y, s_px[lx], s_py[ly], depth)) {
       const uint64_t key = depth_key(depth, (uint32_t)__float_as_int(extra.z));
-      const int p = ly * kTile + lx;
       if (prev == nullptr || key > s_prev[p]) atomicMin(s_key + p, (unsigned long long)key);
     }
   }
