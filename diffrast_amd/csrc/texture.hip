@@ -646,7 +646,9 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     for (int k = 0; k < 8; ++k) {
       float v[4] = {0.f, 0.f, 0.f, 0.f};
       uint32_t key = Table::kEmpty;
-      if (tap_index[k] >= 0) {
+      // A tap of weight 0 (the second level when the blend factor is 0, or an axis with
+      // fraction 0) adds nothing: no table row.
+      if (tap_index[k] >= 0 && tap_weight[k] != 0.0f) {
         key = (uint32_t)tap_index[k];
         for (int c = 0; c < n; ++c) v[c] = g[c0 + c] * tap_weight[k];
       }
