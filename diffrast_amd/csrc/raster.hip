@@ -66,6 +66,7 @@ struct Workspace {
   uint32_t* bucket_counts;   // [kOrderBuckets]
   uint32_t* bucket_cursor;   // [kOrderBuckets]
   uint32_t* bounds;          // [6] order-preserving bits of min x, y, z and max x, y, z
+  uint32_t* bound_parts;     // [centroid workgroups][6] the same per workgroup
   bool ordered;
   int tiles_x, tiles_y;
   int64_t tiles;
@@ -115,6 +116,7 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
     w.bucket_counts = (uint32_t*)take(sizeof(uint32_t) * kOrderBuckets);
     w.bucket_cursor = (uint32_t*)take(sizeof(uint32_t) * kOrderBuckets);
     w.bounds = (uint32_t*)take(sizeof(uint32_t) * 8);
+    w.bound_parts = (uint32_t*)take(sizeof(uint32_t) * 6 * (size_t)blocks_for(g.num_tri, 256));
   }
   w.records = (float4*)take(sizeof(float4) * kRecord * 256 * (size_t)w.record_blocks);
   w.bytes = off;
@@ -343,15 +345,12 @@ __device__ __forceinline__ float from_ordered_bits(uint32_t u) {
   return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
 }
 
-// Centroid of every triangle in the first view and the bounds of the finite ones.
+// Centroid of every triangle in the first view, and per workgroup the bounds of the finite
+// ones (order-preserving bits: min x, y, z, then max x, y, z).
 __global__ __launch_bounds__(256) void order_centroids(DrRasterGeometry g, Workspace ws) {
-  __shared__ uint32_t lo[3], hi[3];
-  if (threadIdx.x < 3) {
-    lo[threadIdx.x] = 0xffffffffu;
-    hi[threadIdx.x] = 0u;
-  }
-  __syncthreads();
+  __shared__ uint32_t s_part[256 / DR_WAVE][6];
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t b[6] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0u, 0u, 0u};
   if (t < g.num_tri) {
     const int32_t* row = g.tri + 3 * (int64_t)t;
     float c[3] = {0.f, 0.f, 0.f};
@@ -365,16 +364,54 @@ __global__ __launch_bounds__(256) void order_centroids(DrRasterGeometry g, Works
     ws.centroids[t] = make_float4(c[0], c[1], c[2], 0.0f);
     if (isfinite(c[0]) && isfinite(c[1]) && isfinite(c[2])) {
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        atomicMin(lo + k, ordered_bits(c[k]));
-        atomicMax(hi + k, ordered_bits(c[k]));
-      }
+      for (int k = 0; k < 3; ++k) b[k] = b[3 + k] = ordered_bits(c[k]);
     }
   }
+#pragma unroll
+  for (int d = 1; d < DR_WAVE; d <<= 1)
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      b[k] = min(b[k], (uint32_t)__shfl_xor(b[k], d));
+      b[3 + k] = max(b[3 + k], (uint32_t)__shfl_xor(b[3 + k], d));
+    }
+  if (lane_id() == 0)
+#pragma unroll
+    for (int k = 0; k < 6; ++k) s_part[threadIdx.x / DR_WAVE][k] = b[k];
   __syncthreads();
-  if (threadIdx.x < 3) {
-    atomicMin(ws.bounds + threadIdx.x, lo[threadIdx.x]);
-    atomicMax(ws.bounds + 3 + threadIdx.x, hi[threadIdx.x]);
+  if (threadIdx.x < 6) {
+    const int k = threadIdx.x;
+    uint32_t v = s_part[0][k];
+    for (int w = 1; w < 256 / DR_WAVE; ++w) v = k < 3 ? min(v, s_part[w][k]) : max(v, s_part[w][k]);
+    ws.bound_parts[6 * blockIdx.x + k] = v;
+  }
+}
+
+// The bounds over all workgroups' parts (one workgroup).
+__global__ __launch_bounds__(256) void order_bounds(Workspace ws, int parts) {
+  __shared__ uint32_t s_part[256 / DR_WAVE][6];
+  uint32_t b[6] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0u, 0u, 0u};
+  for (int i = threadIdx.x; i < parts; i += blockDim.x)
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      const uint32_t v = ws.bound_parts[6 * i + k];
+      b[k] = k < 3 ? min(b[k], v) : max(b[k], v);
+    }
+#pragma unroll
+  for (int d = 1; d < DR_WAVE; d <<= 1)
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      b[k] = min(b[k], (uint32_t)__shfl_xor(b[k], d));
+      b[3 + k] = max(b[3 + k], (uint32_t)__shfl_xor(b[3 + k], d));
+    }
+  if (lane_id() == 0)
+#pragma unroll
+    for (int k = 0; k < 6; ++k) s_part[threadIdx.x / DR_WAVE][k] = b[k];
+  __syncthreads();
+  if (threadIdx.x < 6) {
+    const int k = threadIdx.x;
+    uint32_t v = s_part[0][k];
+    for (int w = 1; w < 256 / DR_WAVE; ++w) v = k < 3 ? min(v, s_part[w][k]) : max(v, s_part[w][k]);
+    ws.bounds[k] = v;
   }
 }
 
@@ -1203,9 +1240,8 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
       const int tri_blocks = blocks_for(g->num_tri, 256);
       raster_fill_u32<<<blocks_for(kOrderBuckets, 256), 256, 0, s>>>(ws.bucket_counts,
                                                                      kOrderBuckets, 0u);
-      raster_fill_u32<<<1, 64, 0, s>>>(ws.bounds, 3, 0xffffffffu);
-      raster_fill_u32<<<1, 64, 0, s>>>(ws.bounds + 3, 3, 0u);
       order_centroids<<<tri_blocks, 256, 0, s>>>(*g, ws);
+      order_bounds<<<1, 256, 0, s>>>(ws, tri_blocks);
       order_count<<<tri_blocks, 256, 0, s>>>(*g, ws);
       order_scan<<<1, 256, 0, s>>>(ws);
       order_place<<<tri_blocks, 256, 0, s>>>(*g, ws);
