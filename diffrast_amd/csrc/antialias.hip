@@ -537,11 +537,15 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
     }
   }
   if (grad_pos == nullptr) return;  // uniform over the workgroup
-  __syncthreads();
+  float lane_max = 0.0f;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) table.add_wave(rows[k], vals[k], 4, grad_pos, 4);
+  for (int k = 0; k < 4; ++k)
+    if (rows[k] != Table::kEmpty) lane_max = fmaxf(lane_max, max_magnitude(vals[k], 4));
+  const FixedPass f = table.begin(lane_max);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) table.add_wave(rows[k], vals[k], 4, grad_pos, 4, f);
   __syncthreads();
-  table.flush(grad_pos, 4, 4);
+  table.flush(grad_pos, 4, 4, f);
 }
 
 bool valid_args(const DrAntialiasArgs* a) {

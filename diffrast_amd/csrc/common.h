@@ -184,30 +184,92 @@ inline int64_t tile_blocks(int batch, int height, int width) {
 
 // ---- workgroup scatter table --------------------------------------------------------------
 
+// Fixed-point scale of one accumulation pass of a workgroup. LDS float atomics are slow on
+// gfx950 (one lane per clock per CU), 64-bit integer ones an order of magnitude faster, so the
+// row table accumulates value * 2^shift as 64-bit integers. With every added value at most M
+// in magnitude, M < 2^(e + 1), shift = 50 - e keeps each value below 2^51 and any sum of up to
+// 2^11 of them below 2^62; the rounding of each value is at most 2^-51 M, far below float32
+// accumulation. A non-finite value anywhere in the pass sends the whole pass to global float
+// atomics instead.
+// Largest magnitude among n values, +inf if any is not finite.
+__device__ __forceinline__ float max_magnitude(const float* v, int n) {
+  float m = 0.0f;
+  bool bad = false;
+  for (int i = 0; i < n; ++i) {
+    bad = bad || !isfinite(v[i]);
+    m = fmaxf(m, fabsf(v[i]));
+  }
+  return bad ? __int_as_float(0x7f800000) : m;
+}
+
+struct FixedPass {
+  double scale;  // 2^shift
+  double inv;    // 2^-shift
+  bool direct;   // no table: values go straight to global memory
+};
+
+__device__ __forceinline__ long long to_fixed(float v, const FixedPass& f) {
+  return __double2ll_rn((double)v * f.scale);
+}
+
+__device__ __forceinline__ float from_fixed(long long x, const FixedPass& f) {
+  return (float)((double)x * f.inv);
+}
+
 // Accumulates gradient rows in LDS before they reach global memory. A row is CH floats at
 // dst + key * stride. Lanes add rows here: open addressing on the key, where a plain read finds
 // a key already present and a compare-and-swap claims a free slot, which then joins the list
-// of used slots. flush() adds each used row to global memory once, CH consecutive lanes per
-// row, and zeroes it, so clearing and flushing cost what the workgroup touched, not the table
-// size. A key that finds no slot within kProbe steps goes straight to global memory. Keys must
-// be < 0xffffffff.
+// of used slots; values add as 64-bit fixed point (FixedPass). flush() adds each used row to
+// global memory once, CH consecutive lanes per row, and zeroes it, so clearing and flushing
+// cost what the workgroup touched, not the table size. A key that finds no slot within kProbe
+// steps goes straight to global memory. Keys must be < 0xffffffff.
 template <int SLOTS, int CH>
 struct RowTable {
   static constexpr uint32_t kEmpty = 0xffffffffu;
   static constexpr int kProbe = 16;
-  static_assert((SLOTS & (SLOTS - 1)) == 0 && CH % 4 == 0, "power-of-two slots, CH % 4 == 0");
+  static_assert((SLOTS & (SLOTS - 1)) == 0 && CH % 2 == 0, "power-of-two slots, even CH");
   uint32_t keys[SLOTS];
-  float vals[SLOTS * CH];
+  long long vals[SLOTS * CH];
   uint32_t used[SLOTS];
   uint32_t count;
+  float wave_max[256 / DR_WAVE];
+  int wave_bad[256 / DR_WAVE];
 
-  // Empties the table. Every thread of the workgroup calls it; a barrier must follow.
+  // Empties the table. Every thread of the workgroup calls it; begin() orders it before adds.
   __device__ __forceinline__ void init() {
     for (int i = threadIdx.x; i < SLOTS; i += blockDim.x) keys[i] = kEmpty;
-    float4* v4 = reinterpret_cast<float4*>(vals);
-    for (int i = threadIdx.x; i < SLOTS * CH / 4; i += blockDim.x)
-      v4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    longlong2* v2 = reinterpret_cast<longlong2*>(vals);
+    for (int i = threadIdx.x; i < SLOTS * CH / 2; i += blockDim.x) v2[i] = make_longlong2(0, 0);
     if (threadIdx.x == 0) count = 0u;
+  }
+
+  // Starts a pass: every thread gives the largest magnitude it will add (NaN or inf for a
+  // non-finite value). Contains a barrier, which also orders init() or reset() before the adds.
+  __device__ __forceinline__ FixedPass begin(float lane_max) {
+    const bool bad = !isfinite(lane_max);
+    float m = bad ? 0.0f : lane_max;
+#pragma unroll
+    for (int d = 1; d < DR_WAVE; d <<= 1) m = fmaxf(m, __shfl_xor(m, d));
+    const bool wave_bad_now = __ballot(bad) != 0;
+    if (lane_id() == 0) {
+      wave_max[threadIdx.x / DR_WAVE] = m;
+      wave_bad[threadIdx.x / DR_WAVE] = wave_bad_now;
+    }
+    __syncthreads();
+    float M = 0.0f;
+    bool any_bad = false;
+#pragma unroll
+    for (int w = 0; w < 256 / DR_WAVE; ++w) {
+      M = fmaxf(M, wave_max[w]);
+      any_bad = any_bad || wave_bad[w];
+    }
+    FixedPass f;
+    f.direct = any_bad;
+    int e = 0;
+    if (M > 0.0f) e = ilogbf(M);
+    f.scale = ldexp(1.0, 50 - e);
+    f.inv = ldexp(1.0, e - 50);
+    return f;
   }
 
   __device__ __forceinline__ static uint32_t hash(uint32_t k) {
@@ -237,19 +299,24 @@ struct RowTable {
     return -1;
   }
 
-  // Adds n (<= CH) values of row `key`; false if the table had no room.
-  __device__ __forceinline__ bool add(uint32_t key, const float* v, int n) {
+  // Adds n (<= CH) values of row `key`; false if the table had no room (or the pass is direct).
+  __device__ __forceinline__ bool add(uint32_t key, const float* v, int n, const FixedPass& f) {
+    if (f.direct) return false;
     const int slot = slot_of(key);
     if (slot < 0) return false;
-    for (int c = 0; c < n; ++c)
-      if (v[c] != 0.0f) atomicAdd(vals + slot * CH + c, v[c]);
+    for (int c = 0; c < n; ++c) {
+      const long long x = to_fixed(v[c], f);
+      if (x != 0)
+        atomicAdd(reinterpret_cast<unsigned long long*>(vals + slot * CH + c),
+                  (unsigned long long)x);
+    }
     return true;
   }
 
   // Adds a row to the table, or to global memory if the table has no room.
   __device__ __forceinline__ void add_or_global(uint32_t key, const float* v, int n, float* dst,
-                                                int64_t stride) {
-    if (!add(key, v, n))
+                                                int64_t stride, const FixedPass& f) {
+    if (!add(key, v, n, f))
       for (int c = 0; c < n; ++c)
         if (v[c] != 0.0f) atomic_add(dst + (int64_t)key * stride + c, v[c]);
   }
@@ -258,7 +325,7 @@ struct RowTable {
   // has the same key, the wave sums first and one lane adds, which keeps a hot row from
   // serialising 64 LDS atomics.
   __device__ __forceinline__ void add_wave(uint32_t key, const float* v, int n, float* dst,
-                                           int64_t stride) {
+                                           int64_t stride, const FixedPass& f) {
     const uint64_t live = __ballot(key != kEmpty);
     if (live == 0) return;
     const int first = __ffsll((unsigned long long)live) - 1;
@@ -266,25 +333,25 @@ struct RowTable {
     if (__ballot(key == lead) == live && __popcll(live) > 1) {
       float sums[CH];
       for (int c = 0; c < n; ++c) sums[c] = wave_masked_sum(v[c], live);
-      if (lane_id() == first) add_or_global(lead, sums, n, dst, stride);
+      if (lane_id() == first) add_or_global(lead, sums, n, dst, stride, f);
       return;
     }
-    if (key != kEmpty) add_or_global(key, v, n, dst, stride);
+    if (key != kEmpty) add_or_global(key, v, n, dst, stride, f);
   }
 
   // Adds the used rows to global memory and zeroes them; call after a barrier that follows
   // every add. Lanes take (row, channel) pairs, a power of two >= n lanes per row.
-  __device__ __forceinline__ void flush(float* dst, int64_t stride, int n) {
+  __device__ __forceinline__ void flush(float* dst, int64_t stride, int n, const FixedPass& f) {
     const int shift = n <= 1 ? 0 : (n <= 2 ? 1 : (n <= 4 ? 2 : 3));
     const uint32_t rows = count;
     for (uint32_t i = threadIdx.x; i < (rows << shift); i += blockDim.x) {
       const int c = (int)(i & ((1u << shift) - 1u));
       if (c >= n) continue;
       const uint32_t slot = used[i >> shift];
-      float* p = vals + slot * CH + c;
-      const float v = *p;
-      if (v != 0.0f) atomic_add(dst + (int64_t)keys[slot] * stride + c, v);
-      *p = 0.0f;
+      long long* p = vals + slot * CH + c;
+      const long long x = *p;
+      if (x != 0) atomic_add(dst + (int64_t)keys[slot] * stride + c, from_fixed(x, f));
+      *p = 0;
     }
   }
 

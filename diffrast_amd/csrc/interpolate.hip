@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
                                                          float* __restrict__ grad_rast,
                                                          float* __restrict__ grad_db,
                                                          uint32_t rows_per_image) {
-  using Table = RowTable<512, 8>;
+  using Table = RowTable<256, 8>;
   __shared__ Table table;
   table.init();  // the first pass's barriers order it before any add
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
@@ -194,13 +194,15 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
     // one table update per vertex.
     const int n = min(N, C - c0);
     const bool last = row_run_sums(run_key, v);
-    __syncthreads();
-    if (last && live) {
+    const bool adds = last && live;
+    const FixedPass f = table.begin(adds ? max_magnitude(v, 3 * N) : 0.0f);
+    if (adds) {
 #pragma unroll
-      for (int k = 0; k < 3; ++k) table.add_or_global(p.row[k], v + N * k, n, grad_attr + c0, C);
+      for (int k = 0; k < 3; ++k)
+        table.add_or_global(p.row[k], v + N * k, n, grad_attr + c0, C, f);
     }
     __syncthreads();
-    table.flush(grad_attr + c0, C, n);
+    table.flush(grad_attr + c0, C, n, f);
     if (c0 + N < C) {
       __syncthreads();
       table.reset();

@@ -1182,13 +1182,14 @@ __global__ __launch_bounds__(256) void resolve_bwd_kernel(
 #pragma unroll
     for (int c = 0; c < 4; ++c) run[4 * k + c] = vals[k][c];
   const bool last = row_run_sums(key != kEmptyKey ? (uint32_t)key : 0xffffffffu, run);
-  __syncthreads();
-  if (last && key != kEmptyKey) {
+  const bool adds = last && key != kEmptyKey;
+  const FixedPass f = table.begin(adds ? max_magnitude(run, 12) : 0.0f);
+  if (adds) {
 #pragma unroll
-    for (int k = 0; k < 3; ++k) table.add_or_global(rows[k], run + 4 * k, 4, grad_pos, 4);
+    for (int k = 0; k < 3; ++k) table.add_or_global(rows[k], run + 4 * k, 4, grad_pos, 4, f);
   }
   __syncthreads();
-  table.flush(grad_pos, 4, 4);
+  table.flush(grad_pos, 4, 4, f);
 }
 
 }  // namespace

@@ -553,7 +553,7 @@ template <int NC>
 __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const float* grad_out,
                                                       float* grad_texels, float* grad_uv,
                                                       float* grad_uv_da, float* grad_bias) {
-  using Table = RowTable<1024, 4>;
+  using Table = RowTable<512, 4>;
   __shared__ Table table;
   table.init();
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
@@ -641,21 +641,27 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
   // Texel gradients, four channels per pass through the workgroup's table.
   for (int c0 = 0; c0 < C; c0 += 4) {
     const int n = min(4, C - c0);
-    __syncthreads();
+    uint32_t keys[8];
+    float v[8][4];
+    float lane_max = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      float v[4] = {0.f, 0.f, 0.f, 0.f};
-      uint32_t key = Table::kEmpty;
+      keys[k] = Table::kEmpty;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[k][c] = 0.0f;
       // A tap of weight 0 (the second level when the blend factor is 0, or an axis with
       // fraction 0) adds nothing: no table row.
       if (tap_index[k] >= 0 && tap_weight[k] != 0.0f) {
-        key = (uint32_t)tap_index[k];
-        for (int c = 0; c < n; ++c) v[c] = g[c0 + c] * tap_weight[k];
+        keys[k] = (uint32_t)tap_index[k];
+        for (int c = 0; c < n; ++c) v[k][c] = g[c0 + c] * tap_weight[k];
+        lane_max = fmaxf(lane_max, max_magnitude(v[k], n));
       }
-      table.add_wave(key, v, n, grad_texels + c0, C);
     }
+    const FixedPass f = table.begin(lane_max);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) table.add_wave(keys[k], v[k], n, grad_texels + c0, C, f);
     __syncthreads();
-    table.flush(grad_texels + c0, C, n);
+    table.flush(grad_texels + c0, C, n, f);
     if (c0 + 4 < C) {
       __syncthreads();
       table.reset();
