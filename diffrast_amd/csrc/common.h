@@ -157,6 +157,18 @@ __device__ __forceinline__ int64_t xcd_order(int64_t block, int64_t blocks) {
   return slot < own ? start + slot : block;  // the tail beyond own items keeps its order
 }
 
+// xcd_order within consecutive groups of 8 * K blocks: each XCD takes a contiguous run of K
+// blocks of every group, so neighbouring work shares an L2 while the groups still run roughly
+// in order (the last, partial group keeps dispatch order).
+__device__ __forceinline__ int64_t xcd_order_grouped(int64_t block, int64_t blocks, int k) {
+  constexpr int kXcds = 8;
+  const int64_t group_size = (int64_t)kXcds * k;
+  const int64_t group = block / group_size;
+  if ((group + 1) * group_size > blocks) return block;
+  const int64_t r = block - group * group_size;
+  return group * group_size + (r % kXcds) * k + r / kXcds;
+}
+
 // A 16 x 16 pixel tile of image b per 256-thread workgroup; (x, y) of this thread.
 struct TilePixel {
   int b, x, y;

@@ -870,8 +870,9 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   __shared__ float s_bound[kChunk];  // lower bound of each staged triangle's depth
 
   // Chunks run in list order, so the near slabs of every tile are (mostly) merged into the key
-  // buffer before the far ones start, and those can skip what lies behind.
-  const uint32_t work = blockIdx.x;
+  // buffer before the far ones start, and those can skip what lies behind; within groups of
+  // 512 chunks each XCD takes 64 consecutive ones (neighbouring tiles share records).
+  const uint32_t work = (uint32_t)xcd_order_grouped(blockIdx.x, gridDim.x, 64);
   const int64_t list = chunk_tile[work];
   const int64_t tile = list % ws.tiles;
   const uint32_t chunk = work - ws.chunk_offsets[list];
