@@ -147,7 +147,7 @@ def visible_at(pos, tri, height, width, b, row, col, previous=None):
     step = max(1, CHUNK_ELEMENTS // max(1, b.numel()))
     for start in range(0, tri.shape[0], step):
         idx = tri[start:start + step].long()
-        verts = pos[b[None, :], idx[:, None]]              # [n, P, 3, 4]
+        verts = pos[b[None, :, None], idx[:, None]]        # [n, P, 3, 4]
         x, y, z, w = _corner_values(verts)
         ok, depth = coverage(x, y, z, w, px, py)
         if previous is not None:

@@ -217,6 +217,24 @@ def test_depth_layers_are_ordered_and_equal_depths_go_by_index():
         previous = rast
 
 
+def test_visibility_at_listed_pixels_equals_the_full_grid():
+    # visible_at is the brute force behind the full-size checks: every pixel of a batched
+    # mesh, over three depth layers, must equal visible_triangles there.
+    gen = torch.Generator().manual_seed(4)
+    pos, tri = tiny_mesh(80, gen, 0.6, batch=2)
+    height, width = 20, 28
+    b, row, col = (t.reshape(-1) for t in torch.meshgrid(
+        torch.arange(2), torch.arange(height), torch.arange(width), indexing="ij"))
+    px, py = R.pixel_centres(height, width, pos)
+    full, listed = None, None
+    for _ in range(3):
+        full = R.visible_triangles(pos, tri, px, py, full)
+        listed = R.visible_at(pos, tri, height, width, b, row, col, listed)
+        assert torch.equal(listed[1], full[1].reshape(-1))
+        assert torch.equal(listed[0], full[0].reshape(-1))
+    assert (full[1] >= 0).any()
+
+
 def test_resolve_closed_forms_and_rast_db_finite_differences():
     pos = torch.tensor([[[-0.8, -0.6, 0.2, 1.0], [1.2, -0.9, 0.5, 2.0], [0.1, 1.5, -0.3, 1.5]]],
                        dtype=torch.float64)
