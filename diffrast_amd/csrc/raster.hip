@@ -20,19 +20,23 @@
 //    reserves each workgroup's share of a tile's list with one global atomic and fills it.
 // 4. One 256-thread workgroup per (tile, chunk of <= 256 triangles) starts from the tile's keys
 //    so far, skips triangles that lie entirely behind the farthest of them, stages the others
-//    in LDS and tests the pixels of their boxes inside the tile as one flat list of work items
-//    (every lane busy whatever the box sizes), merging into the tile's keys in LDS (64-bit
-//    min); improved keys then go to the key buffer, one atomic per pixel.
+//    in LDS with, per tile row, the span of columns their pixel centres may cover (a bound
+//    proved against the coverage test in coverage.h), and tests the pixels of those spans as
+//    one flat list of work items (every lane busy whatever the span lengths), merging into the
+//    tile's keys in LDS (64-bit min); improved keys then go to the key buffer, one atomic per
+//    pixel.
 //
 // The resolve kernels turn keys into rast / rast_db (reference.py:69-114) and carry gradients
 // back to the vertices.
 #include "common.h"
+#include "coverage.h"
 
 namespace dr {
 namespace {
 
 constexpr int kTile = 16;            // tile edge in pixels; a tile is one 256-thread workgroup
 constexpr int kChunk = 256;          // triangles per tile work item
+constexpr int kWindow = 1024;        // work items per map of the tile kernel (256 threads x 4)
 constexpr int kSmallPixels = 16;     // bounding boxes up to this many pixels skip binning
 constexpr int kScanBlock = 1024;     // elements per scan block (256 threads x 4)
 constexpr int kOrderBuckets = 4096;  // Morton buckets (12 bits of a 30-bit code)
@@ -41,7 +45,6 @@ constexpr int kTileSlots = 1024;     // LDS table of a workgroup's tiles
 constexpr int kRecord = 4;           // float4 per binned triangle record (one 64-byte line)
 constexpr int kDepthSlabs = 16;      // tile lists per tile, by the triangle's nearest depth
 constexpr int kRangeParts = 64;      // workgroups per image in the depth span reduction
-constexpr float kAreaTolerance = 2.384185791015625e-07f;  // 2 * float32 epsilon
 
 struct Workspace {
   float4* records;           // binned triangles, kRecord float4 each: the three clip-space
@@ -143,17 +146,6 @@ __device__ __forceinline__ void instance(const DrRasterGeometry& g, const uint32
   t = g.ranges[2 * b] + (int)(i - g.range_prefix[b]);
 }
 
-struct Tri {
-  float x[3], y[3], z[3], w[3];
-  float reach_x, reach_y;  // max_k |x_k| + |w_k| and likewise for y (reference.py:321-326)
-};
-
-// max_k |a_k| + |w_k|
-__device__ __forceinline__ float reach(const float* a, const float* w) {
-  return fmaxf(fmaxf(fabsf(a[0]) + fabsf(w[0]), fabsf(a[1]) + fabsf(w[1])),
-               fabsf(a[2]) + fabsf(w[2]));
-}
-
 __device__ __forceinline__ void load_tri(const DrRasterGeometry& g, int b, int t, Tri& T,
                                          int (&v)[3]) {
   const int32_t* row = g.tri + 3 * (int64_t)t;
@@ -171,47 +163,6 @@ __device__ __forceinline__ void load_tri(const DrRasterGeometry& g, int b, int t
   }
   T.reach_x = reach(T.x, T.w);
   T.reach_y = reach(T.y, T.w);
-}
-
-// Fill-rule test of one edge (reference.py:338-365).
-__device__ __forceinline__ bool inside_edge(float e, float ai, float ci, float wi, float aj,
-                                            float cj, float wj, bool positive) {
-  float q = e;
-  if (e == 0.0f) {
-    float gx = ci * wj - cj * wi;
-    float gy = aj * wi - ai * wj;
-    q = (gx == 0.0f) ? gy : gx;
-  }
-  return positive ? (q > 0.0f) : (q < 0.0f);
-}
-
-// Coverage of pixel centre (px, py) and depth there: the reference's operations in its order
-// (reference.py:301-335), one rounding each. The triangle is known to be finite.
-__device__ __forceinline__ bool covers(const float* x, const float* y, const float* z,
-                                       const float* w, float reach_x, float reach_y, float px,
-                                       float py, float& depth) {
-  const float a0 = x[0] - px * w[0];
-  const float a1 = x[1] - px * w[1];
-  const float a2 = x[2] - px * w[2];
-  const float c0 = y[0] - py * w[0];
-  const float c1 = y[1] - py * w[1];
-  const float c2 = y[2] - py * w[2];
-  const float e0 = a1 * c2 - a2 * c1;
-  const float e1 = a2 * c0 - a0 * c2;
-  const float e2 = a0 * c1 - a1 * c0;
-  const float s = e0 + e1 + e2;
-  const bool positive = s > 0.0f;
-  if (!inside_edge(e0, a1, c1, w[1], a2, c2, w[2], positive)) return false;
-  if (!inside_edge(e1, a2, c2, w[2], a0, c0, w[0], positive)) return false;
-  if (!inside_edge(e2, a0, c0, w[0], a1, c1, w[1], positive)) return false;
-  const float span_x = fabsf(a0) + fabsf(a1) + fabsf(a2);
-  const float span_y = fabsf(c0) + fabsf(c1) + fabsf(c2);
-  if (!(fabsf(s) > (reach_x * span_y + span_x * (reach_y + span_y)) * kAreaTolerance))
-    return false;
-  const float ew = e0 * w[0] + e1 * w[1] + e2 * w[2];
-  if (positive ? !(ew > 0.0f) : !(ew < 0.0f)) return false;
-  depth = (e0 * z[0] + e1 * z[1] + e2 * z[2]) / ew;
-  return depth >= -1.0f && depth <= 1.0f;
 }
 
 __device__ __forceinline__ bool finite_tri(const Tri& T) {
@@ -848,21 +799,28 @@ __global__ __launch_bounds__(256) void raster_chunk_tiles(Workspace ws, uint32_t
     chunk_list[c] = (uint32_t)l;
 }
 
-// One workgroup per (tile, chunk of up to kChunk binned triangles). The chunk's triangles and
-// the parts of their bounding boxes inside the tile are staged in LDS; the pixels of all those
-// boxes form one list of work items (triangle j owns items s_start[j] .. s_start[j + 1] - 1),
-// which the 256 threads walk in steps of 256, so every lane has a pixel to test whatever the
-// sizes of the boxes. Hits merge into the tile's keys in LDS (64-bit min); the tile then goes
-// to the key buffer with one atomic min per pixel.
+// One workgroup per (tile, chunk of up to kChunk binned triangles). The chunk's triangles are
+// staged in LDS together with, per row of the tile, the columns their pixel centres may cover
+// (row_span(); the whole row of the box for a triangle without spans). The pixels of all those
+// row spans form one list of work items, which the 256 threads walk in steps of 256, so every
+// lane has a pixel to test whatever the span lengths. The list is mapped kWindow items at a
+// time: each span writes (its first item, its triangle, its first pixel) at its first item of
+// the window, and a max-scan over the window carries that to the span's other items. Hits
+// merge into the tile's keys in LDS (64-bit min); the tile then goes to the key buffer with one
+// atomic min per improved pixel.
 __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
                                                           const uint64_t* prev, uint64_t* keys,
                                                           Workspace ws,
                                                           const uint32_t* entries,
                                                           const uint32_t* chunk_tile) {
-  // Per staged triangle: the three vertices, then (reach_x, reach_y, row bits, box bits).
+  // Per staged triangle: the three vertices, then (reach_x, reach_y, row bits, unused).
   __shared__ float4 s_tri[kChunk][4];
-  __shared__ int s_start[kChunk];
+  // Per staged triangle and tile row: first column | last column << 4 (0x0f: no pixel).
+  __shared__ uint8_t s_rows[kChunk][kTile];
+  // Work item -> (first item of its span in the window) << 20 | triangle << 12 | pixel offset.
+  __shared__ uint4 s_map[kWindow / 4];
   __shared__ int s_wave_sum[256 / DR_WAVE];
+  __shared__ uint32_t s_wave_max[256 / DR_WAVE];
   __shared__ unsigned long long s_key[kTile * kTile];
   __shared__ unsigned long long s_prev[kTile * kTile];
   __shared__ float s_px[kTile], s_py[kTile];
@@ -922,7 +880,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   const bool cull = far_key != kEmptyKey;
   const float far_depth = key_depth(far_key);
 
-  int area = 0;
+  int items = 0, row_lo = 0, row_hi = -1;
   if ((int)threadIdx.x < n) {
     const float4* rec = ws.records + (size_t)entries[first + threadIdx.x] * kRecord;
     Tri T;
@@ -935,6 +893,8 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
       T.z[k] = p.z;
       T.w[k] = p.w;
     }
+    T.reach_x = reach(T.x, T.w);
+    T.reach_y = reach(T.y, T.w);
     int x_lo, x_hi, y_lo, y_hi;
     candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
     const int bx0 = max(x_lo - tile_x0, 0), bx1 = min(x_hi - tile_x0, kTile - 1);
@@ -949,20 +909,30 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
       bound = nearest - 1e-5f * scale;
     }
     s_bound[threadIdx.x] = bound;
+    s_tri[threadIdx.x][3] = make_float4(T.reach_x, T.reach_y,
+                                        __int_as_float(__float_as_int(rec[3].y) & 0xffffff), 0.0f);
     const bool behind = cull && bound > far_depth;
-    uint32_t box = 0u;
     if (bx0 <= bx1 && by0 <= by1 && !behind) {
-      area = (bx1 - bx0 + 1) * (by1 - by0 + 1);
-      box = pack_box(bx0, bx1 - bx0 + 1, by0, by1 - by0 + 1);
+      RowSpans se;
+      const bool spans = span_setup(T.x, T.y, T.w, T.reach_x, T.reach_y, g.width, tile_x0, se);
+      row_lo = by0;
+      row_hi = by1;
+      for (int r = by0; r <= by1; ++r) {
+        int lo = bx0, hi = bx1;
+        if (spans) row_span(se, s_py[r], lo, hi);
+        uint32_t code = 0x0fu;
+        if (lo <= hi) {
+          code = (uint32_t)lo | (uint32_t)hi << 4;
+          items += hi - lo + 1;
+        }
+        s_rows[threadIdx.x][r] = (uint8_t)code;
+      }
     }
-    s_tri[threadIdx.x][3] = make_float4(reach(T.x, T.w), reach(T.y, T.w),
-                                        __int_as_float(__float_as_int(rec[3].y) & 0xffffff),
-                                        __uint_as_float(box));
   }
-  // Exclusive prefix of the areas over the workgroup.
+  // Exclusive prefix of the item counts over the workgroup.
   const int lane = lane_id();
   const int wave = threadIdx.x / DR_WAVE;
-  int incl = area;
+  int incl = items;
 #pragma unroll
   for (int d = 1; d < DR_WAVE; d <<= 1) {
     const int up = __shfl_up(incl, d);
@@ -977,33 +947,72 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     before += w < wave ? v : 0;
     total += v;
   }
-  s_start[threadIdx.x] = before + incl - area;
-  __syncthreads();
+  const int tri_first = before + incl - items;
 
-  for (int item = threadIdx.x; item < total; item += 256) {
-    // The last triangle whose first item is at or before this one (s_start[0] = 0).
-    int j = 0;
-#pragma unroll
-    for (int step = kChunk / 2; step >= 1; step >>= 1)
-      if (s_start[j + step] <= item) j += step;
-    const float4 v0 = s_tri[j][0], v1 = s_tri[j][1], v2 = s_tri[j][2], extra = s_tri[j][3];
-    const uint32_t box = __float_as_uint(extra.w);
-    const int bw = (int)((box >> 8) & 0xff) + 1;
-    int dx, dy;
-    box_cell(item - s_start[j], bw, dx, dy);
-    const int lx = (int)(box & 0xff) + dx, ly = (int)((box >> 16) & 0xff) + dy;
-    const int p = ly * kTile + lx;
-    // Early depth test: the pixel already holds a nearer key (NaN for an empty one: no skip).
-    if (s_bound[j] > key_depth(s_key[p])) continue;
-    const float X[3] = {v0.x, v1.x, v2.x}, Y[3] = {v0.y, v1.y, v2.y};
-    const float Z[3] = {v0.z, v1.z, v2.z}, Wv[3] = {v0.w, v1.w, v2.w};
-    float depth;
-    if (covers(X, Y, Z, Wv, extra.x, extra.y, s_px[lx], s_py[ly], depth)) {
-      const uint64_t key = depth_key(depth, (uint32_t)__float_as_int(extra.z));
-      if (prev == nullptr || key > s_prev[p]) atomicMin(s_key + p, (unsigned long long)key);
+  for (int base = 0; base < total; base += kWindow) {
+    s_map[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+    // Mark the first item in the window of each span that reaches into it.
+    if (items > 0 && tri_first < base + kWindow && tri_first + items > base) {
+      int at = tri_first;
+      for (int r = row_lo; r <= row_hi && at < base + kWindow; ++r) {
+        const uint32_t code = s_rows[threadIdx.x][r];
+        const int lo = (int)(code & 15u), hi = (int)(code >> 4);
+        if (lo > hi) continue;
+        const int width = hi - lo + 1;
+        if (at + width > base) {
+          const int pos = max(at, base) - base;
+          // Pixel of item i (counted from base) of this span: q - 2048 + i, q in [1025, 2319].
+          const int q = r * kTile + lo - (at - base) + 2048;
+          reinterpret_cast<uint32_t*>(s_map)[pos] =
+              (uint32_t)pos << 20 | threadIdx.x << 12 | (uint32_t)q;
+        }
+        at += width;
+      }
     }
+    __syncthreads();
+    // Inclusive max-scan of the window (each mark exceeds every mark before it).
+    uint4 m = s_map[threadIdx.x];
+    m.y = max(m.y, m.x);
+    m.z = max(m.z, m.y);
+    m.w = max(m.w, m.z);
+    uint32_t run = m.w;
+#pragma unroll
+    for (int d = 1; d < DR_WAVE; d <<= 1) {
+      const uint32_t up = __shfl_up(run, d);
+      if (lane >= d) run = max(run, up);
+    }
+    if (lane == DR_WAVE - 1) s_wave_max[wave] = run;
+    uint32_t carry = __shfl_up(run, 1);
+    if (lane == 0) carry = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < 256 / DR_WAVE; ++w) carry = w < wave ? max(carry, s_wave_max[w]) : carry;
+    m.x = max(m.x, carry);
+    m.y = max(m.y, carry);
+    m.z = max(m.z, carry);
+    m.w = max(m.w, carry);
+    s_map[threadIdx.x] = m;
+    __syncthreads();
+
+    const int count = min(total - base, kWindow);
+    for (int i = threadIdx.x; i < count; i += 256) {
+      const uint32_t v = reinterpret_cast<const uint32_t*>(s_map)[i];
+      const int j = (int)((v >> 12) & 0xffu);
+      const int p = (int)(v & 0xfffu) - 2048 + i;
+      // Early depth test: the pixel already holds a nearer key (NaN for an empty one: no skip).
+      if (s_bound[j] > key_depth(s_key[p])) continue;
+      const float4 v0 = s_tri[j][0], v1 = s_tri[j][1], v2 = s_tri[j][2], extra = s_tri[j][3];
+      const float X[3] = {v0.x, v1.x, v2.x}, Y[3] = {v0.y, v1.y, v2.y};
+      const float Z[3] = {v0.z, v1.z, v2.z}, Wv[3] = {v0.w, v1.w, v2.w};
+      float depth;
+      if (covers(X, Y, Z, Wv, extra.x, extra.y, s_px[p & (kTile - 1)], s_py[p / kTile], depth)) {
+        const uint64_t key = depth_key(depth, (uint32_t)__float_as_int(extra.z));
+        if (prev == nullptr || key > s_prev[p]) atomicMin(s_key + p, (unsigned long long)key);
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
   const uint64_t best = s_key[threadIdx.x];
   if (!inside || best >= start_key) return;
   atomicMin((unsigned long long*)(keys + pixel), (unsigned long long)best);
