@@ -94,8 +94,8 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
     call("dr_raster_visibility_begin", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),
          size.value, counts, stream)
     if counts[1]:
-        # the tile lists, then the tile of each work chunk
-        entries = torch.empty(counts[1] + counts[2], dtype=torch.int32, device=device)
+        # the tile lists, tile by tile
+        entries = torch.empty(counts[1], dtype=torch.int32, device=device)
         call("dr_raster_visibility_bin", ref(geo.struct), ptr(workspace), size.value,
              ptr(entries), counts, stream)
         call("dr_raster_visibility_tiles", ref(geo.struct), ptr(prev), ptr(keys),

@@ -112,6 +112,66 @@ __device__ __forceinline__ uint32_t row_shl(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x100 + S, 0xf, 0xf, true);
 }
 
+// Wave-wide scans with DPP moves only (no LDS permute, no lane-address registers): row_shr
+// steps within each 16-lane row, then row_bcast:15 (rows 1 and 3 take the last lane of the
+// row before) and row_bcast:31 (rows 2 and 3 take lane 31). Lanes a move does not reach get 0,
+// the identity of both sum and unsigned max.
+__device__ __forceinline__ uint32_t bcast15(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);
+}
+__device__ __forceinline__ uint32_t bcast31(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);
+}
+// The value of the previous lane of the wave (0 in lane 0): DPP wave_shr:1.
+__device__ __forceinline__ uint32_t wave_shr1(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x138, 0xf, 0xf, true);
+}
+
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
+  v += row_shr<1>(v);
+  v += row_shr<2>(v);
+  v += row_shr<4>(v);
+  v += row_shr<8>(v);
+  v += bcast15(v);
+  v += bcast31(v);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_inclusive_max(uint32_t v) {
+  v = max(v, row_shr<1>(v));
+  v = max(v, row_shr<2>(v));
+  v = max(v, row_shr<4>(v));
+  v = max(v, row_shr<8>(v));
+  v = max(v, bcast15(v));
+  v = max(v, bcast31(v));
+  return v;
+}
+
+template <int S>
+__device__ __forceinline__ uint64_t row_shr64(uint64_t v) {
+  return (uint64_t)row_shr<S>((uint32_t)(v >> 32)) << 32 | row_shr<S>((uint32_t)v);
+}
+
+// Largest value over the wave, in every lane.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  uint64_t o;
+  o = row_shr64<1>(v);
+  v = o > v ? o : v;
+  o = row_shr64<2>(v);
+  v = o > v ? o : v;
+  o = row_shr64<4>(v);
+  v = o > v ? o : v;
+  o = row_shr64<8>(v);
+  v = o > v ? o : v;
+  o = (uint64_t)bcast15((uint32_t)(v >> 32)) << 32 | bcast15((uint32_t)v);
+  v = o > v ? o : v;
+  o = (uint64_t)bcast31((uint32_t)(v >> 32)) << 32 | bcast31((uint32_t)v);
+  v = o > v ? o : v;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), DR_WAVE - 1);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)v, DR_WAVE - 1);
+  return (uint64_t)hi << 32 | lo;
+}
+
 template <int S, int N>
 __device__ __forceinline__ void run_step(float (&v)[N], bool take) {
 #pragma unroll

@@ -36,7 +36,9 @@ namespace {
 
 constexpr int kTile = 16;            // tile edge in pixels; a tile is one 256-thread workgroup
 constexpr int kChunk = 256;          // triangles per tile work item
-constexpr int kWindow = 1024;        // work items per map of the tile kernel (256 threads x 4)
+constexpr int kWorkClasses = 128;    // classes of 32 entries in the tile pass's heavy-first order
+constexpr int kWindow = 512;         // work items per map of the tile kernel (256 threads x 2)
+static_assert(kWindow == 2 * 256, "the map scan gives each thread two entries");
 constexpr int kSmallPixels = 16;     // bounding boxes up to this many pixels skip binning
 constexpr int kScanBlock = 1024;     // elements per scan block (256 threads x 4)
 constexpr int kOrderBuckets = 4096;  // Morton buckets (12 bits of a 30-bit code)
@@ -50,8 +52,9 @@ struct Workspace {
   float4* records;           // binned triangles, kRecord float4 each: the three clip-space
                              // vertices, then the bits of (image, row, tx0 | tx1 << 16,
                              // ty0 | ty1 << 16)
-  // Tile lists: list slab * tiles + tile holds the binned triangles of that tile whose nearest
-  // depth falls in depth slab `slab` of their image, so lists run near to far.
+  // Tile lists: list tile * kDepthSlabs + slab holds the binned triangles of that tile whose
+  // nearest depth falls in depth slab `slab` of their image, so a tile's entries are one range
+  // that runs near to far.
   uint32_t* list_counts;     // [lists + 1]
   uint32_t* list_offsets;    // [lists + 1] exclusive prefix of list_counts
   uint32_t* list_cursor;     // [lists + 1] fill positions of the bin pass
@@ -62,6 +65,7 @@ struct Workspace {
   uint2* block_sums;         // [scan blocks] (entries, chunks)
   uint32_t* counters;        // [1] entries, [2] chunks
   uint32_t* block_records;   // [record_blocks] binned triangles of each setup workgroup
+  uint32_t* tile_order;      // [tiles] tile pass order: heavy tiles first within each XCD's share
   float* px;                 // [width] pixel-centre x per column
   float* py;                 // [height] pixel-centre y per row
   uint32_t* order;           // [num_tri] processing order (instanced meshes only)
@@ -111,6 +115,7 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
   w.range_parts = (uint32_t*)take(sizeof(uint32_t) * 2 * kRangeParts * w.depth_ranges);
   w.block_sums = (uint2*)take(sizeof(uint2) * (w.scan_blocks + 1));
   w.block_records = (uint32_t*)take(sizeof(uint32_t) * w.record_blocks);
+  w.tile_order = (uint32_t*)take(sizeof(uint32_t) * w.tiles);
   w.px = (float*)take(sizeof(float) * g.width);
   w.py = (float*)take(sizeof(float) * g.height);
   if (w.ordered) {
@@ -635,10 +640,11 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
       out[3] = make_float4(__int_as_float(b), __int_as_float(t | (slab << 24)),
                            __uint_as_float((uint32_t)tx0 | ((uint32_t)tx1 << 16)),
                            __uint_as_float((uint32_t)ty0 | ((uint32_t)ty1 << 16)));
-      const uint32_t list_base = (uint32_t)(slab * ws.tiles) + (uint32_t)b * ws.tiles_x * ws.tiles_y;
+      const uint32_t image_tiles = (uint32_t)b * ws.tiles_x * ws.tiles_y;
       for (int ty = ty0; ty <= ty1; ++ty)
         for (int tx = tx0; tx <= tx1; ++tx) {
-          const uint32_t list = list_base + ty * ws.tiles_x + tx;
+          const uint32_t list =
+              (image_tiles + ty * ws.tiles_x + tx) * kDepthSlabs + (uint32_t)slab;
           const int slot = table.insert(list);
           if (slot >= 0)
             atomicAdd(table.count + slot, 1u);
@@ -757,7 +763,7 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
   // The records of setup workgroup blockIdx.x.
   const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
   int tx0 = 0, tx1 = -1, ty0 = 0, ty1 = -1;
-  uint32_t image_tiles = 0;
+  uint32_t image_tiles = 0, slab = 0;
   if (threadIdx.x < ws.block_records[blockIdx.x]) {
     const float4 rec = ws.records[(size_t)r * kRecord + 3];
     const uint32_t rx = __float_as_uint(rec.z), ry = __float_as_uint(rec.w);
@@ -765,13 +771,12 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
     tx1 = (int)(rx >> 16);
     ty0 = (int)(ry & 0xffffu);
     ty1 = (int)(ry >> 16);
-    const uint32_t slab = __float_as_uint(rec.y) >> 24;
-    image_tiles = (uint32_t)(slab * ws.tiles) +
-                  (uint32_t)__float_as_int(rec.x) * ws.tiles_x * ws.tiles_y;
+    slab = __float_as_uint(rec.y) >> 24;
+    image_tiles = (uint32_t)__float_as_int(rec.x) * ws.tiles_x * ws.tiles_y;
   }
   for (int ty = ty0; ty <= ty1; ++ty)
     for (int tx = tx0; tx <= tx1; ++tx) {
-      const int slot = table.insert(image_tiles + ty * ws.tiles_x + tx);
+      const int slot = table.insert((image_tiles + ty * ws.tiles_x + tx) * kDepthSlabs + slab);
       if (slot >= 0) atomicAdd(table.count + slot, 1u);
     }
   __syncthreads();
@@ -783,239 +788,263 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
   __syncthreads();
   for (int ty = ty0; ty <= ty1; ++ty)
     for (int tx = tx0; tx <= tx1; ++tx) {
-      const uint32_t tile = image_tiles + ty * ws.tiles_x + tx;
-      const int slot = table.find(tile);
+      const uint32_t list = (image_tiles + ty * ws.tiles_x + tx) * kDepthSlabs + slab;
+      const int slot = table.find(list);
       const uint32_t at = slot >= 0 ? table.base[slot] + atomicAdd(table.count + slot, 1u)
-                                    : atomicAdd(ws.list_cursor + tile, 1u);
+                                    : atomicAdd(ws.list_cursor + list, 1u);
       entries[at] = r;
     }
 }
 
-// The list of every work chunk: chunk_list[c] = l for the chunks of list l.
-__global__ __launch_bounds__(256) void raster_chunk_tiles(Workspace ws, uint32_t* chunk_list) {
-  const int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (l >= ws.lists) return;
-  for (uint32_t c = ws.chunk_offsets[l]; c < ws.chunk_offsets[l + 1]; ++c)
-    chunk_list[c] = (uint32_t)l;
+// The order in which the tile pass takes the tiles: each XCD keeps its contiguous share of
+// them (xcd_order), and within the share the tiles with the most binned triangles go first, so
+// that the longest workgroups do not start last. A counting sort by entry count in classes of
+// 32 entries; the order within a class is free (tiles are independent). One 1024-thread
+// workgroup per XCD share.
+__global__ __launch_bounds__(1024) void raster_tile_order(Workspace ws) {
+  __shared__ uint32_t s_count[kWorkClasses];
+  const int64_t tiles = ws.tiles;
+  constexpr int kXcds = 8;
+  const int64_t per = tiles / kXcds, extra = tiles % kXcds, k = blockIdx.x;
+  const int64_t start = k * per + (k < extra ? k : extra);
+  const int64_t own = tiles < kXcds ? (k < tiles ? 1 : 0) : per + (k < extra ? 1 : 0);
+  for (int c = threadIdx.x; c < kWorkClasses; c += blockDim.x) s_count[c] = 0u;
+  __syncthreads();
+  auto work_class = [&](int64_t tile) {
+    const uint32_t n = ws.list_offsets[(tile + 1) * kDepthSlabs] - ws.list_offsets[tile * kDepthSlabs];
+    return (int)min(n >> 5, (uint32_t)(kWorkClasses - 1));
+  };
+  for (int64_t i = threadIdx.x; i < own; i += blockDim.x)
+    atomicAdd(s_count + work_class(start + i), 1u);
+  __syncthreads();
+  if (threadIdx.x == 0) {  // first position of each class, heaviest class first
+    uint32_t run = 0u;
+    for (int c = kWorkClasses - 1; c >= 0; --c) {
+      const uint32_t n = s_count[c];
+      s_count[c] = run;
+      run += n;
+    }
+  }
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < own; i += blockDim.x) {
+    const uint32_t at = atomicAdd(s_count + work_class(start + i), 1u);
+    ws.tile_order[start + at] = (uint32_t)(start + i);
+  }
 }
 
-// One workgroup per (tile, chunk of up to kChunk binned triangles). The chunk's triangles are
-// staged in LDS together with, per row of the tile, the columns their pixel centres may cover
-// (row_span(); the whole row of the box for a triangle without spans). The pixels of all those
-// row spans form one list of work items, which the 256 threads walk in steps of 256, so every
-// lane has a pixel to test whatever the span lengths. The list is mapped kWindow items at a
-// time: each span writes (its first item, its triangle, its first pixel) at its first item of
-// the window, and a max-scan over the window carries that to the span's other items. Hits
-// merge into the tile's keys in LDS (64-bit min); the tile then goes to the key buffer with one
-// atomic min per improved pixel.
+// One workgroup per tile: the tile's keys stay in LDS while it walks the tile's binned
+// triangles near to far (its depth-slab lists are one range of the entry array), kChunk at a
+// time. Each chunk is staged in LDS together with, per row of the tile, the columns its pixel
+// centres may cover (row_span(); the whole row of the box for a triangle without spans). The
+// pixels of all those row spans form one list of work items, which the 256 threads walk in
+// steps of 256, so every lane has a pixel to test whatever the span lengths. The list is mapped
+// kWindow items at a time: each span writes (its first item, its triangle, its first pixel) at
+// its first item of the window, and a max-scan over the window carries that to the span's other
+// items. Hits merge into the keys in LDS (64-bit min). Before each chunk the tile's farthest key
+// bounds what can still win: triangles entirely behind it are skipped, and so are single pixels
+// that already hold a nearer key. The improved keys are stored once at the end.
 __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
                                                           const uint64_t* prev, uint64_t* keys,
                                                           Workspace ws,
-                                                          const uint32_t* entries,
-                                                          const uint32_t* chunk_tile) {
-  // Per staged triangle: the three vertices, then (reach_x, reach_y, row bits, unused).
-  __shared__ float4 s_tri[kChunk][4];
+                                                          const uint32_t* entries) {
+  // Per staged triangle: the three vertices, (reach_x, reach_y) and its row of tri.
+  __shared__ float4 s_tri[kChunk][3];
+  __shared__ float2 s_reach[kChunk];
+  __shared__ uint32_t s_row[kChunk];
   // Per staged triangle and tile row: first column | last column << 4 (0x0f: no pixel).
   __shared__ uint8_t s_rows[kChunk][kTile];
   // Work item -> (first item of its span in the window) << 20 | triangle << 12 | pixel offset.
-  __shared__ uint4 s_map[kWindow / 4];
+  __shared__ uint2 s_map[kWindow / 2];
   __shared__ int s_wave_sum[256 / DR_WAVE];
   __shared__ uint32_t s_wave_max[256 / DR_WAVE];
   __shared__ unsigned long long s_key[kTile * kTile];
-  __shared__ unsigned long long s_prev[kTile * kTile];
   __shared__ float s_px[kTile], s_py[kTile];
   __shared__ uint64_t s_far[256 / DR_WAVE];
   __shared__ float s_bound[kChunk];  // lower bound of each staged triangle's depth
 
-  // Chunks run in list order, so the near slabs of every tile are (mostly) merged into the key
-  // buffer before the far ones start, and those can skip what lies behind; within groups of
-  // 512 chunks each XCD takes 64 consecutive ones (neighbouring tiles share records).
-  const uint32_t work = (uint32_t)xcd_order_grouped(blockIdx.x, gridDim.x, 64);
-  const int64_t list = chunk_tile[work];
-  const int64_t tile = list % ws.tiles;
-  const uint32_t chunk = work - ws.chunk_offsets[list];
-  const uint32_t first = ws.list_offsets[list] + chunk * kChunk;
-  const uint32_t end = min(ws.list_offsets[list + 1], first + kChunk);
-  const int n = (int)(end - first);
+  // XCD k takes the k-th eighth of the tiles (for a batch of 8 images, one image each), so the
+  // records that neighbouring tiles share stay in one L2; heavy tiles first within it.
+  const uint32_t tile = ws.tile_order[xcd_order(blockIdx.x, gridDim.x)];
+  const uint32_t begin = ws.list_offsets[(size_t)tile * kDepthSlabs];
+  const uint32_t end = ws.list_offsets[(size_t)(tile + 1) * kDepthSlabs];
+  if (begin == end) return;  // uniform over the workgroup
+
+  // This thread's entry of the next chunk, read ahead.
+  uint32_t next = begin + threadIdx.x < end ? entries[begin + threadIdx.x] : 0u;
 
   const int per_image = ws.tiles_x * ws.tiles_y;
   const int b = (int)(tile / per_image);
-  const int tile_in_image = (int)(tile - (int64_t)b * per_image);
+  const int tile_in_image = (int)(tile - (uint32_t)b * per_image);
   const int tile_x0 = (tile_in_image % ws.tiles_x) * kTile;
   const int tile_y0 = (tile_in_image / ws.tiles_x) * kTile;
 
-  // This thread's pixel of the tile: its key so far (the small-triangle pass and other chunks
-  // of this tile have already merged theirs) and the previous layer's key.
+  // This thread's pixel of the tile and its key so far (from the small-triangle pass).
   const int x = tile_x0 + (threadIdx.x % kTile), y = tile_y0 + (threadIdx.x / kTile);
   const bool inside = x < g.width && y < g.height;
-  const int64_t pixel = ((int64_t)b * g.height + y) * g.width + x;
-  const uint64_t start_key = inside ? keys[pixel] : kEmptyKey;
-  {
-    s_key[threadIdx.x] = start_key;
-    uint64_t floor_key = 0ull;
-    if (prev != nullptr && inside) floor_key = prev[pixel];
-    s_prev[threadIdx.x] = floor_key;
-    if (threadIdx.x < kTile && tile_x0 + (int)threadIdx.x < g.width)
-      s_px[threadIdx.x] = ws.px[tile_x0 + threadIdx.x];
-    if (threadIdx.x >= 32 && threadIdx.x < 32 + kTile &&
-        tile_y0 + (int)threadIdx.x - 32 < g.height)
-      s_py[threadIdx.x - 32] = ws.py[tile_y0 + threadIdx.x - 32];
-  }
-  // The farthest key of the tile so far (pixels outside the image count as nearest). A
-  // triangle whose nearest vertex lies beyond it, by more than the rounding of the depth,
-  // cannot win any pixel of the tile and is skipped; the same bound skips single pixels that
-  // already hold a nearer key. The depth computed at a covered pixel is a convex combination
-  // of the vertex depths z_k / w_k up to a few float32 roundings (~6 * 2^-24 of the largest
-  // |z_k / w_k|; the margin is 1e-5 of it), and equal depths are never skipped.
-  uint64_t far_key = inside ? start_key : 0ull;
-#pragma unroll
-  for (int d = 1; d < DR_WAVE; d <<= 1) {
-    const uint64_t other = __shfl_xor(far_key, d);
-    far_key = other > far_key ? other : far_key;
-  }
-  if (lane_id() == 0) s_far[threadIdx.x / DR_WAVE] = far_key;
-  __syncthreads();
-#pragma unroll
-  for (int w = 0; w < 256 / DR_WAVE; ++w) far_key = s_far[w] > far_key ? s_far[w] : far_key;
-  const bool cull = far_key != kEmptyKey;
-  const float far_depth = key_depth(far_key);
-
-  int items = 0, row_lo = 0, row_hi = -1;
-  if ((int)threadIdx.x < n) {
-    const float4* rec = ws.records + (size_t)entries[first + threadIdx.x] * kRecord;
-    Tri T;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      const float4 p = rec[k];
-      s_tri[threadIdx.x][k] = p;
-      T.x[k] = p.x;
-      T.y[k] = p.y;
-      T.z[k] = p.z;
-      T.w[k] = p.w;
-    }
-    T.reach_x = reach(T.x, T.w);
-    T.reach_y = reach(T.y, T.w);
-    int x_lo, x_hi, y_lo, y_hi;
-    candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
-    const int bx0 = max(x_lo - tile_x0, 0), bx1 = min(x_hi - tile_x0, kTile - 1);
-    const int by0 = max(y_lo - tile_y0, 0), by1 = min(y_hi - tile_y0, kTile - 1);
-    // A lower bound of the triangle's depth at any pixel it covers (-inf when it crosses the
-    // camera plane).
-    float bound = -__int_as_float(0x7f800000);
-    if (T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
-      const float d0 = T.z[0] / T.w[0], d1 = T.z[1] / T.w[1], d2 = T.z[2] / T.w[2];
-      const float nearest = fminf(fminf(d0, d1), d2);
-      const float scale = fmaxf(fmaxf(fabsf(d0), fabsf(d1)), fabsf(d2));
-      bound = nearest - 1e-5f * scale;
-    }
-    s_bound[threadIdx.x] = bound;
-    s_tri[threadIdx.x][3] = make_float4(T.reach_x, T.reach_y,
-                                        __int_as_float(__float_as_int(rec[3].y) & 0xffffff), 0.0f);
-    const bool behind = cull && bound > far_depth;
-    if (bx0 <= bx1 && by0 <= by1 && !behind) {
-      RowSpans se;
-      const bool spans = span_setup(T.x, T.y, T.w, T.reach_x, T.reach_y, g.width, tile_x0, se);
-      row_lo = by0;
-      row_hi = by1;
-      for (int r = by0; r <= by1; ++r) {
-        int lo = bx0, hi = bx1;
-        if (spans) row_span(se, s_py[r], lo, hi);
-        uint32_t code = 0x0fu;
-        if (lo <= hi) {
-          code = (uint32_t)lo | (uint32_t)hi << 4;
-          items += hi - lo + 1;
-        }
-        s_rows[threadIdx.x][r] = (uint8_t)code;
-      }
-    }
-  }
-  // Exclusive prefix of the item counts over the workgroup.
+  const int64_t tile_pixel0 = ((int64_t)b * g.height + tile_y0) * g.width + tile_x0;
+  s_key[threadIdx.x] =
+      inside ? keys[tile_pixel0 + (int64_t)(threadIdx.x / kTile) * g.width + threadIdx.x % kTile]
+             : kEmptyKey;
+  if (threadIdx.x < kTile && tile_x0 + (int)threadIdx.x < g.width)
+    s_px[threadIdx.x] = ws.px[tile_x0 + threadIdx.x];
+  if (threadIdx.x >= 32 && threadIdx.x < 32 + kTile && tile_y0 + (int)threadIdx.x - 32 < g.height)
+    s_py[threadIdx.x - 32] = ws.py[tile_y0 + threadIdx.x - 32];
   const int lane = lane_id();
   const int wave = threadIdx.x / DR_WAVE;
-  int incl = items;
-#pragma unroll
-  for (int d = 1; d < DR_WAVE; d <<= 1) {
-    const int up = __shfl_up(incl, d);
-    if (lane >= d) incl += up;
-  }
-  if (lane == DR_WAVE - 1) s_wave_sum[wave] = incl;
-  __syncthreads();
-  int before = 0, total = 0;
-#pragma unroll
-  for (int w = 0; w < 256 / DR_WAVE; ++w) {
-    const int v = s_wave_sum[w];
-    before += w < wave ? v : 0;
-    total += v;
-  }
-  const int tri_first = before + incl - items;
 
-  for (int base = 0; base < total; base += kWindow) {
-    s_map[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+  for (uint32_t at = begin; at < end; at += kChunk) {
+    const int n = (int)min(end - at, (uint32_t)kChunk);
+    const bool staged = (int)threadIdx.x < n;
+    Tri T = {};
+    uint32_t tri_row = 0u;
+    if (staged) {
+      const float4* rec = ws.records + (size_t)next * kRecord;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const float4 v = rec[k];
+        T.x[k] = v.x;
+        T.y[k] = v.y;
+        T.z[k] = v.z;
+        T.w[k] = v.w;
+      }
+      tri_row = __float_as_uint(rec[3].y) & 0xffffffu;
+    }
+    if (at + kChunk + threadIdx.x < end) next = entries[at + kChunk + threadIdx.x];
+
+    // The farthest key of the tile so far (pixels outside the image count as nearest). A
+    // triangle whose nearest vertex lies beyond it, by more than the rounding of the depth,
+    // cannot win any pixel of the tile and is skipped; the same bound skips single pixels that
+    // already hold a nearer key. The depth computed at a covered pixel is a convex combination
+    // of the vertex depths z_k / w_k up to a few float32 roundings (~6 * 2^-24 of the largest
+    // |z_k / w_k|; the margin is 1e-5 of it), and equal depths are never skipped.
+    __syncthreads();  // the previous chunk's merges (and the set-up above) are done
+    uint64_t far_key = wave_max_u64(inside ? s_key[threadIdx.x] : 0ull);
+    if (lane == 0) s_far[wave] = far_key;
     __syncthreads();
-    // Mark the first item in the window of each span that reaches into it.
-    if (items > 0 && tri_first < base + kWindow && tri_first + items > base) {
-      int at = tri_first;
-      for (int r = row_lo; r <= row_hi && at < base + kWindow; ++r) {
-        const uint32_t code = s_rows[threadIdx.x][r];
-        const int lo = (int)(code & 15u), hi = (int)(code >> 4);
-        if (lo > hi) continue;
-        const int width = hi - lo + 1;
-        if (at + width > base) {
-          const int pos = max(at, base) - base;
-          // Pixel of item i (counted from base) of this span: q - 2048 + i, q in [1025, 2319].
-          const int q = r * kTile + lo - (at - base) + 2048;
-          reinterpret_cast<uint32_t*>(s_map)[pos] =
-              (uint32_t)pos << 20 | threadIdx.x << 12 | (uint32_t)q;
+#pragma unroll
+    for (int w = 0; w < 256 / DR_WAVE; ++w) far_key = s_far[w] > far_key ? s_far[w] : far_key;
+    const bool cull = far_key != kEmptyKey;
+    const float far_depth = key_depth(far_key);
+
+    int items = 0, row_lo = 0, row_hi = -1;
+    if (staged) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) s_tri[threadIdx.x][k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
+      T.reach_x = reach(T.x, T.w);
+      T.reach_y = reach(T.y, T.w);
+      int x_lo, x_hi, y_lo, y_hi;
+      candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
+      const int bx0 = max(x_lo - tile_x0, 0), bx1 = min(x_hi - tile_x0, kTile - 1);
+      const int by0 = max(y_lo - tile_y0, 0), by1 = min(y_hi - tile_y0, kTile - 1);
+      // A lower bound of the triangle's depth at any pixel it covers (-inf when it crosses the
+      // camera plane).
+      float bound = -__int_as_float(0x7f800000);
+      if (T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
+        const float d0 = T.z[0] / T.w[0], d1 = T.z[1] / T.w[1], d2 = T.z[2] / T.w[2];
+        const float nearest = fminf(fminf(d0, d1), d2);
+        const float scale = fmaxf(fmaxf(fabsf(d0), fabsf(d1)), fabsf(d2));
+        bound = nearest - 1e-5f * scale;
+      }
+      s_bound[threadIdx.x] = bound;
+      s_reach[threadIdx.x] = make_float2(T.reach_x, T.reach_y);
+      s_row[threadIdx.x] = tri_row;
+      const bool behind = cull && bound > far_depth;
+      if (bx0 <= bx1 && by0 <= by1 && !behind) {
+        RowSpans se = {};
+        const bool spans =
+            span_setup(T.x, T.y, T.w, T.reach_x, T.reach_y, g.width, tile_x0, se);
+        row_lo = by0;
+        row_hi = by1;
+        for (int r = by0; r <= by1; ++r) {
+          int lo = bx0, hi = bx1;
+          if (spans) row_span(se, s_py[r], lo, hi);
+          uint32_t code = 0x0fu;
+          if (lo <= hi) {
+            code = (uint32_t)lo | (uint32_t)hi << 4;
+            items += hi - lo + 1;
+          }
+          s_rows[threadIdx.x][r] = (uint8_t)code;
         }
-        at += width;
       }
     }
+    // Exclusive prefix of the item counts over the workgroup.
+    const int incl = (int)wave_inclusive_sum((uint32_t)items);
+    if (lane == DR_WAVE - 1) s_wave_sum[wave] = incl;
     __syncthreads();
-    // Inclusive max-scan of the window (each mark exceeds every mark before it).
-    uint4 m = s_map[threadIdx.x];
-    m.y = max(m.y, m.x);
-    m.z = max(m.z, m.y);
-    m.w = max(m.w, m.z);
-    uint32_t run = m.w;
+    int before = 0, total = 0;
 #pragma unroll
-    for (int d = 1; d < DR_WAVE; d <<= 1) {
-      const uint32_t up = __shfl_up(run, d);
-      if (lane >= d) run = max(run, up);
+    for (int w = 0; w < 256 / DR_WAVE; ++w) {
+      const int v = s_wave_sum[w];
+      before += w < wave ? v : 0;
+      total += v;
     }
-    if (lane == DR_WAVE - 1) s_wave_max[wave] = run;
-    uint32_t carry = __shfl_up(run, 1);
-    if (lane == 0) carry = 0u;
-    __syncthreads();
-#pragma unroll
-    for (int w = 0; w < 256 / DR_WAVE; ++w) carry = w < wave ? max(carry, s_wave_max[w]) : carry;
-    m.x = max(m.x, carry);
-    m.y = max(m.y, carry);
-    m.z = max(m.z, carry);
-    m.w = max(m.w, carry);
-    s_map[threadIdx.x] = m;
-    __syncthreads();
+    const int tri_first = before + incl - items;
 
-    const int count = min(total - base, kWindow);
-    for (int i = threadIdx.x; i < count; i += 256) {
-      const uint32_t v = reinterpret_cast<const uint32_t*>(s_map)[i];
-      const int j = (int)((v >> 12) & 0xffu);
-      const int p = (int)(v & 0xfffu) - 2048 + i;
-      // Early depth test: the pixel already holds a nearer key (NaN for an empty one: no skip).
-      if (s_bound[j] > key_depth(s_key[p])) continue;
-      const float4 v0 = s_tri[j][0], v1 = s_tri[j][1], v2 = s_tri[j][2], extra = s_tri[j][3];
-      const float X[3] = {v0.x, v1.x, v2.x}, Y[3] = {v0.y, v1.y, v2.y};
-      const float Z[3] = {v0.z, v1.z, v2.z}, Wv[3] = {v0.w, v1.w, v2.w};
-      float depth;
-      if (covers(X, Y, Z, Wv, extra.x, extra.y, s_px[p & (kTile - 1)], s_py[p / kTile], depth)) {
-        const uint64_t key = depth_key(depth, (uint32_t)__float_as_int(extra.z));
-        if (prev == nullptr || key > s_prev[p]) atomicMin(s_key + p, (unsigned long long)key);
+    for (int base = 0; base < total; base += kWindow) {
+      s_map[threadIdx.x] = make_uint2(0u, 0u);
+      __syncthreads();
+      // Mark the first item in the window of each span that reaches into it.
+      if (items > 0 && tri_first < base + kWindow && tri_first + items > base) {
+        int first = tri_first;
+        for (int r = row_lo; r <= row_hi && first < base + kWindow; ++r) {
+          const uint32_t code = s_rows[threadIdx.x][r];
+          const int lo = (int)(code & 15u), hi = (int)(code >> 4);
+          if (lo > hi) continue;
+          const int width = hi - lo + 1;
+          if (first + width > base) {
+            const int pos = max(first, base) - base;
+            // Pixel of item i (counted from base) of this span: q - 2048 + i, 0 < q < 4096.
+            const int q = r * kTile + lo - (first - base) + 2048;
+            reinterpret_cast<uint32_t*>(s_map)[pos] =
+                (uint32_t)pos << 20 | threadIdx.x << 12 | (uint32_t)q;
+          }
+          first += width;
+        }
       }
+      __syncthreads();
+      // Inclusive max-scan of the window (each mark exceeds every mark before it).
+      uint2 m = s_map[threadIdx.x];
+      m.y = max(m.y, m.x);
+      const uint32_t run = wave_inclusive_max(m.y);
+      if (lane == DR_WAVE - 1) s_wave_max[wave] = run;
+      uint32_t carry = wave_shr1(run);
+      __syncthreads();
+#pragma unroll
+      for (int w = 0; w < 256 / DR_WAVE; ++w)
+        carry = w < wave ? max(carry, s_wave_max[w]) : carry;
+      m.x = max(m.x, carry);
+      m.y = max(m.y, carry);
+      s_map[threadIdx.x] = m;
+      __syncthreads();
+
+      const int count = min(total - base, kWindow);
+      for (int i = threadIdx.x; i < count; i += 256) {
+        const uint32_t v = reinterpret_cast<const uint32_t*>(s_map)[i];
+        const int j = (int)((v >> 12) & 0xffu);
+        const int p = (int)(v & 0xfffu) - 2048 + i;
+        // Early depth test: the pixel already holds a nearer key (NaN for an empty one).
+        if (s_bound[j] > key_depth(s_key[p])) continue;
+        const float4 v0 = s_tri[j][0], v1 = s_tri[j][1], v2 = s_tri[j][2];
+        const float2 rc = s_reach[j];
+        const float X[3] = {v0.x, v1.x, v2.x}, Y[3] = {v0.y, v1.y, v2.y};
+        const float Z[3] = {v0.z, v1.z, v2.z}, Wv[3] = {v0.w, v1.w, v2.w};
+        const int lx = p & (kTile - 1), ly = p / kTile;
+        float depth;
+        if (covers(X, Y, Z, Wv, rc.x, rc.y, s_px[lx], s_py[ly], depth)) {
+          const uint64_t key = depth_key(depth, s_row[j]);
+          // Peeling: only keys after the previous layer's (read where a candidate needs it).
+          if (prev == nullptr || key > prev[tile_pixel0 + (int64_t)ly * g.width + lx])
+            atomicMin(s_key + p, (unsigned long long)key);
+        }
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
-  const uint64_t best = s_key[threadIdx.x];
-  if (!inside || best >= start_key) return;
-  atomicMin((unsigned long long*)(keys + pixel), (unsigned long long)best);
+  __syncthreads();
+  // This workgroup alone writes the tile's keys.
+  if (inside)
+    keys[tile_pixel0 + (int64_t)(threadIdx.x / kTile) * g.width + threadIdx.x % kTile] =
+        s_key[threadIdx.x];
 }
 
 // ---- resolve ----------------------------------------------------------------------------
@@ -1289,7 +1318,6 @@ extern "C" int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspa
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
   raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, entries);
-  raster_chunk_tiles<<<blocks_for(ws.lists, 256), 256, 0, s>>>(ws, entries + counts[1]);
   return launch_status();
 }
 
@@ -1303,8 +1331,8 @@ extern "C" int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint6
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
-  raster_tile_kernel<<<counts[2], 256, 0, s>>>(*g, prev_keys, keys, ws, entries,
-                                               entries + counts[1]);
+  raster_tile_order<<<8, 1024, 0, s>>>(ws);
+  raster_tile_kernel<<<(unsigned)ws.tiles, 256, 0, s>>>(*g, prev_keys, keys, ws, entries);
   return launch_status();
 }
 
