@@ -275,6 +275,21 @@ __device__ __forceinline__ Bilinear bilinear_setup(float s, float t, int face, i
 template <int N>
 __device__ __forceinline__ void fetch_taps(const float* __restrict__ texels, const Bilinear& L,
                                            int C, int c0, float (&t)[4][N]) {
+  if constexpr (N == 4) {
+    // Four-channel texels on a 16-byte aligned buffer: one 16-byte load per tap.
+    if (C == 4 && (reinterpret_cast<uintptr_t>(texels) & 15u) == 0) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float4 v = L.valid[k] ? *reinterpret_cast<const float4*>(texels + L.index[k] * 4)
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        t[k][0] = v.x;
+        t[k][1] = v.y;
+        t[k][2] = v.z;
+        t[k][3] = v.w;
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const float* row = texels + L.index[k] * C + c0;
@@ -504,6 +519,12 @@ __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* __
       }
       if (bad) res[c] = nan;
     }
+    if constexpr (NC == 4) {
+      if (C == 4 && (reinterpret_cast<uintptr_t>(o) & 15u) == 0) {
+        *reinterpret_cast<float4*>(o) = make_float4(res[0], res[1], res[2], res[3]);
+        continue;
+      }
+    }
 #pragma unroll
     for (int c = 0; c < NC; ++c)
       if (c0 + c < C) o[c0 + c] = res[c];
@@ -522,8 +543,20 @@ __device__ __forceinline__ void level_coordinate_grads(const Bilinear& L,
   for (int c0 = 0; c0 < C; c0 += N) {
     float t[4][N], gc[N];
     fetch_taps<N>(texels, L, C, c0, t);
+    bool loaded = false;
+    if constexpr (N == 4) {
+      if (C == 4 && (reinterpret_cast<uintptr_t>(g) & 15u) == 0) {
+        const float4 v = *reinterpret_cast<const float4*>(g);
+        gc[0] = v.x;
+        gc[1] = v.y;
+        gc[2] = v.z;
+        gc[3] = v.w;
+        loaded = true;
+      }
+    }
+    if (!loaded)
 #pragma unroll
-    for (int c = 0; c < N; ++c) gc[c] = c0 + c < C ? g[c0 + c] : 0.0f;
+      for (int c = 0; c < N; ++c) gc[c] = c0 + c < C ? g[c0 + c] : 0.0f;
 #pragma unroll
     for (int c = 0; c < N; ++c) {
       if (c0 + c >= C) continue;
