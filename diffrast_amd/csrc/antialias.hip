@@ -422,6 +422,15 @@ __device__ __forceinline__ PixelPairs pixel_pairs(const DrAntialiasArgs& a, cons
 // out = colour + |t - 0.5| of the neighbour's colour on the side of each crossing
 // (reference.py:253-264). A pixel takes (0.5 - t) of its pair partner when it is the first
 // pixel and t < 0.5, and (t - 0.5) when it is the second and t >= 0.5.
+// The four channels of a pixel (16-byte loads on an aligned buffer).
+__device__ __forceinline__ void load_px4(const float* p, float (&v)[4]) {
+  if (load_wide<4>(p, v)) return;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) v[c] = p[c];
+}
+
+// NC = 4 for four-channel colours (whole-pixel loads and stores), 0 for any channel count.
+template <int NC>
 __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const float2* pair_t,
                                                        const uchar2* pair_bits, float* out) {
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
@@ -439,6 +448,26 @@ __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const 
   }
   const float* color = a.color + tp.pixel * C;
   float* o = out + tp.pixel * C;
+  if constexpr (NC == 4) {
+    float own[4], v[4];
+    load_px4(color, own);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = own[c];
+    if (any) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        if (weight[n] == 0.0f) continue;
+        float other[4];
+        load_px4(a.color + P.other[n] * 4, other);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] += weight[n] * (other[c] - own[c]);
+      }
+    }
+    if (!store_wide<4>(o, v))
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = v[c];
+    return;
+  }
   for (int c = 0; c < C; ++c) {
     const float own = color[c];
     float v = own;
@@ -453,6 +482,7 @@ __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const 
 
 // Colour gradient (a gather over the same pairs) and position gradient of each active pair,
 // written by its first pixel through the workgroup's scatter table (rows of pos: x, y, z, w).
+template <int NC>
 __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const float2* pair_t,
                                                      const uchar2* pair_bits,
                                                      const float* grad_out, float* grad_color,
@@ -471,7 +501,31 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
   if (tp.inside) {
     const PixelPairs P = pixel_pairs(a, tp, pair_t, pair_bits);
     const float* g = grad_out + tp.pixel * C;
-    if (grad_color) {
+    if (grad_color && NC == 4) {
+      float gv[4], v[4];
+      load_px4(g, gv);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] = gv[c];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        if (!P.active[n]) continue;
+        const float t = P.t[n];
+        float g2[4];
+        load_px4(grad_out + P.other[n] * 4, g2);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (P.first[n]) {
+            v[c] += t < 0.5f ? -(0.5f - t) * gv[c] : (t - 0.5f) * g2[c];
+          } else {
+            v[c] += t < 0.5f ? (0.5f - t) * g2[c] : -(t - 0.5f) * gv[c];
+          }
+        }
+      }
+      float* gc = grad_color + tp.pixel * 4;
+      if (!store_wide<4>(gc, v))
+#pragma unroll
+        for (int c = 0; c < 4; ++c) gc[c] = v[c];
+    } else if (grad_color) {
       float* gc = grad_color + tp.pixel * C;
       for (int c = 0; c < C; ++c) {
         float v = g[c];
@@ -503,7 +557,19 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
         const float* cQ = a.color + q * C;
         const float* g2 = grad_out + q * C;
         float g_t = 0.0f;
-        if (t < 0.5f) {
+        if constexpr (NC == 4) {
+          float vP[4], vQ[4], vg[4];
+          load_px4(cP, vP);
+          load_px4(cQ, vQ);
+          load_px4(t < 0.5f ? g : g2, vg);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            if (t < 0.5f)
+              g_t -= vg[c] * (vQ[c] - vP[c]);
+            else
+              g_t += vg[c] * (vP[c] - vQ[c]);
+          }
+        } else if (t < 0.5f) {
           for (int c = 0; c < C; ++c) g_t -= g[c] * (cQ[c] - cP[c]);
         } else {
           for (int c = 0; c < C; ++c) g_t += g2[c] * (cP[c] - cQ[c]);
@@ -630,8 +696,10 @@ extern "C" int dr_antialias_forward(const DrAntialiasArgs* a, void* pairs, size_
   pair_buffers(a, pairs, t, bits);
   const int64_t blocks = tile_blocks(a->batch, a->height, a->width);
   aa_pairs_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits);
-  if (a->channels > 0)
-    aa_blend_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, out);
+  if (a->channels == 4)
+    aa_blend_kernel<4><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, out);
+  else if (a->channels > 0)
+    aa_blend_kernel<0><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, out);
   return launch_status();
 }
 
@@ -649,7 +717,12 @@ extern "C" int dr_antialias_backward(const DrAntialiasArgs* a, const void* pairs
   float2* t;
   uchar2* bits;
   pair_buffers(a, (void*)pairs, t, bits);
-  aa_bwd_kernel<<<tile_blocks(a->batch, a->height, a->width), 256, 0, (hipStream_t)stream>>>(
-      *a, t, bits, grad_out, grad_color, grad_pos);
+  const int64_t blocks = tile_blocks(a->batch, a->height, a->width);
+  if (a->channels == 4)
+    aa_bwd_kernel<4><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, grad_out, grad_color,
+                                                               grad_pos);
+  else
+    aa_bwd_kernel<0><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, grad_out, grad_color,
+                                                               grad_pos);
   return launch_status();
 }

@@ -48,6 +48,48 @@ __device__ __forceinline__ void store4(float* p, float4 v) { *reinterpret_cast<f
 // Hardware fp32 atomic add (the buffers are ordinary coarse-grained device memory).
 __device__ __forceinline__ void atomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
 
+// N consecutive floats at p with the widest loads their alignment allows (16 bytes for N a
+// multiple of 4, 8 bytes for N = 2); false, with nothing loaded, when p is not so aligned. Gathers
+// of whole rows this way cost one memory instruction per 16 bytes instead of one per channel.
+template <int N>
+__device__ __forceinline__ bool load_wide(const float* p, float (&v)[N]) {
+  if constexpr (N % 4 == 0) {
+    if (reinterpret_cast<uintptr_t>(p) & 15u) return false;
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const float4 q = reinterpret_cast<const float4*>(p)[i];
+      v[4 * i] = q.x;
+      v[4 * i + 1] = q.y;
+      v[4 * i + 2] = q.z;
+      v[4 * i + 3] = q.w;
+    }
+    return true;
+  } else if constexpr (N == 2) {
+    if (reinterpret_cast<uintptr_t>(p) & 7u) return false;
+    const float2 q = *reinterpret_cast<const float2*>(p);
+    v[0] = q.x;
+    v[1] = q.y;
+    return true;
+  }
+  return false;
+}
+
+template <int N>
+__device__ __forceinline__ bool store_wide(float* p, const float (&v)[N]) {
+  if constexpr (N % 4 == 0) {
+    if (reinterpret_cast<uintptr_t>(p) & 15u) return false;
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i)
+      reinterpret_cast<float4*>(p)[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    return true;
+  } else if constexpr (N == 2) {
+    if (reinterpret_cast<uintptr_t>(p) & 7u) return false;
+    *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+    return true;
+  }
+  return false;
+}
+
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
 // Sum of v over the lanes of the wave whose bit is set in `mask`, valid in every lane.

@@ -147,17 +147,18 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
   const uint32_t run_key = p.valid ? (uint32_t)p.t : 0xffffffffu;
   float gu = 0.f, gv = 0.f, g_dudx = 0.f, g_dudy = 0.f, g_dvdx = 0.f, g_dvdy = 0.f;
 
-  constexpr int N = 8;  // channels per pass through the table
+  constexpr int N = NC > 0 && NC < 8 ? NC : 8;  // channels per pass through the table
   for (int c0 = 0; c0 < C; c0 += N) {
     float A[3][N], G[N];
     const bool live = p.valid;
     if (live) load_rows<N>(a.attr, p, C, c0, A);
+    const bool wide = live && c0 + N <= C && load_wide<N>(g + c0, G);
 #pragma unroll
     for (int c = 0; c < N; ++c) {
       if (!live) A[0][c] = A[1][c] = A[2][c] = 0.0f;
-      G[c] = (live && c0 + c < C) ? g[c0 + c] : 0.0f;
+      if (!wide) G[c] = (live && c0 + c < C) ? g[c0 + c] : 0.0f;
     }
-    // Vertex k, channel c at v[8 k + c].
+    // Vertex k, channel c at v[N k + c].
     float v[3 * N];
 #pragma unroll
     for (int c = 0; c < N; ++c) {
