@@ -300,11 +300,11 @@ inline int64_t tile_blocks(int batch, int height, int width) {
 
 // Fixed-point scale of one accumulation pass of a workgroup. LDS float atomics are slow on
 // gfx950 (one lane per clock per CU), 64-bit integer ones an order of magnitude faster, so the
-// row table accumulates value * 2^shift as 64-bit integers. With every added value at most M
-// in magnitude, M < 2^(e + 1), shift = 50 - e keeps each value below 2^51 and any sum of up to
-// 2^11 of them below 2^62; the rounding of each value is at most 2^-51 M, far below float32
-// accumulation. A non-finite value anywhere in the pass sends the whole pass to global float
-// atomics instead.
+// row table accumulates value * 2^shift as 64-bit integers. With every value a lane gives at
+// most M in magnitude, M < 2^(e + 1), shift = 44 - e keeps each value below 2^45 and a wave's
+// sum of up to 64 of them (add_wave) below 2^51, the range of to_fixed(); any 2^11 such adds stay
+// below 2^62. The rounding of each value is at most 2^-45 M, far below float32 accumulation. A
+// non-finite value anywhere in the pass sends the whole pass to global float atomics instead.
 // Largest magnitude among n values, +inf if any is not finite.
 __device__ __forceinline__ float max_magnitude(const float* v, int n) {
   float m = 0.0f;
@@ -322,8 +322,13 @@ struct FixedPass {
   bool direct;   // no table: values go straight to global memory
 };
 
+// round(v * scale), to nearest even. |v * scale| < 2^51 here, so adding 1.5 * 2^52 leaves that
+// integer in the low bits of the double (every value of [2^52, 2^53) is an integer), and the
+// product itself is exact (scale is a power of two): one fused multiply-add and a subtraction.
 __device__ __forceinline__ long long to_fixed(float v, const FixedPass& f) {
-  return __double2ll_rn((double)v * f.scale);
+  const double magic = 6755399441055744.0;  // 1.5 * 2^52
+  const double y = __fma_rn((double)v, f.scale, magic);
+  return __double_as_longlong(y) - __double_as_longlong(magic);
 }
 
 __device__ __forceinline__ float from_fixed(long long x, const FixedPass& f) {
@@ -381,8 +386,8 @@ struct RowTable {
     f.direct = any_bad;
     int e = 0;
     if (M > 0.0f) e = ilogbf(M);
-    f.scale = ldexp(1.0, 50 - e);
-    f.inv = ldexp(1.0, e - 50);
+    f.scale = ldexp(1.0, 44 - e);
+    f.inv = ldexp(1.0, e - 44);
     return f;
   }
 
@@ -418,12 +423,10 @@ struct RowTable {
     if (f.direct) return false;
     const int slot = slot_of(key);
     if (slot < 0) return false;
-    for (int c = 0; c < n; ++c) {
-      const long long x = to_fixed(v[c], f);
-      if (x != 0)
-        atomicAdd(reinterpret_cast<unsigned long long*>(vals + slot * CH + c),
-                  (unsigned long long)x);
-    }
+    unsigned long long* row = reinterpret_cast<unsigned long long*>(vals + slot * CH);
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+      if (c < n) atomicAdd(row + c, (unsigned long long)to_fixed(v[c], f));
     return true;
   }
 

@@ -571,14 +571,17 @@ __device__ __forceinline__ void level_coordinate_grads(const Bilinear& L,
   }
 }
 
+// Table keys (texel rows of the packed buffer, 0xffffffff for none) and weights of a level's
+// taps. A tap of weight 0 (the second level when the blend factor is 0, or an axis with fraction
+// 0) adds nothing and gets no key.
 __device__ __forceinline__ void level_taps(const Bilinear& L, float level_weight,
-                                           int64_t tex_off, int64_t* index, float* weight) {
+                                           int64_t tex_off, uint32_t* key, float* weight) {
   float t0[4] = {0.f, 0.f, 0.f, 0.f}, wgt[4], dfx, dfy;
   bilinear_grad(L, t0, wgt, dfx, dfy);  // the weights do not depend on texel values
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    index[k] = L.valid[k] ? tex_off + L.index[k] : -1;
     weight[k] = level_weight * wgt[k];
+    key[k] = L.valid[k] && weight[k] != 0.0f ? (uint32_t)(tex_off + L.index[k]) : 0xffffffffu;
   }
 }
 
@@ -598,12 +601,12 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
   const float* texels = a.texels + tex_off * C;
 
   Lookup K;
-  // Texel gradient targets: taps 0-3 of the first level, 4-7 of the second (-1: none).
-  int64_t tap_index[8];
+  // Texel gradient targets: taps 0-3 of the first level, 4-7 of the second.
+  uint32_t tap_key[8];
   float tap_weight[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    tap_index[k] = -1;
+    tap_key[k] = Table::kEmpty;
     tap_weight[k] = 0.0f;
   }
   float g_s = 0.0f, g_t = 0.0f, g_lod = 0.0f;
@@ -617,7 +620,7 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     bool valid;
     const bool bad = nearest_setup(a, K, index, valid);
     if (!bad && valid) {
-      tap_index[0] = tex_off + index;
+      tap_key[0] = (uint32_t)(tex_off + index);
       tap_weight[0] = 1.0f;
     }
     live = false;  // no coordinate gradient
@@ -631,12 +634,12 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     } else {
       float fx0 = 0.f, fy0 = 0.f, fx1 = 0.f, fy1 = 0.f, v0 = 0.f, v1 = 0.f;
       level_coordinate_grads<NC>(L0, texels, g, C, K.level_weight[0], fx0, fy0, two, v0);
-      level_taps(L0, K.level_weight[0], tex_off, tap_index, tap_weight);
+      level_taps(L0, K.level_weight[0], tex_off, tap_key, tap_weight);
       if (L0.pass_x) g_s += fx0 * L0.size_x;
       if (L0.pass_y) g_t += fy0 * L0.size_y;
       if (two) {
         level_coordinate_grads<NC>(L1, texels, g, C, K.level_weight[1], fx1, fy1, true, v1);
-        level_taps(L1, K.level_weight[1], tex_off, tap_index + 4, tap_weight + 4);
+        level_taps(L1, K.level_weight[1], tex_off, tap_key + 4, tap_weight + 4);
         if (L1.pass_x) g_s += fx1 * L1.size_x;
         if (L1.pass_y) g_t += fy1 * L1.size_y;
         g_lod = K.lod_grad ? v1 - v0 : 0.0f;
@@ -671,28 +674,37 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
   }
   if (grad_texels == nullptr) return;  // uniform over the workgroup
 
-  // Texel gradients, four channels per pass through the workgroup's table.
+  // Texel gradients, four channels per pass through the workgroup's table: tap k adds
+  // g[c] * weight[k] to its texel row.
+  float w_max = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (tap_key[k] != Table::kEmpty) w_max = fmaxf(w_max, fabsf(tap_weight[k]));
   for (int c0 = 0; c0 < C; c0 += 4) {
     const int n = min(4, C - c0);
-    uint32_t keys[8];
-    float v[8][4];
-    float lane_max = 0.0f;
+    float gc[4] = {0.f, 0.f, 0.f, 0.f};
+    if (!(n == 4 && load_wide<4>(g + c0, gc)))
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      keys[k] = Table::kEmpty;
+      for (int c = 0; c < 4; ++c) gc[c] = c < n ? g[c0 + c] : 0.0f;
+    // The largest |g[c] * weight[k]| of this lane (rounding is monotone, so the product of the
+    // two largest factors is the largest product).
+    float g_max = 0.0f;
+    bool finite = true;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) v[k][c] = 0.0f;
-      // A tap of weight 0 (the second level when the blend factor is 0, or an axis with
-      // fraction 0) adds nothing: no table row.
-      if (tap_index[k] >= 0 && tap_weight[k] != 0.0f) {
-        keys[k] = (uint32_t)tap_index[k];
-        for (int c = 0; c < n; ++c) v[k][c] = g[c0 + c] * tap_weight[k];
-        lane_max = fmaxf(lane_max, max_magnitude(v[k], n));
-      }
+    for (int c = 0; c < 4; ++c) {
+      finite = finite && isfinite(gc[c]);
+      g_max = fmaxf(g_max, fabsf(gc[c]));
     }
+    if (!finite) g_max = __int_as_float(0x7f800000);
+    const float lane_max = w_max > 0.0f ? g_max * w_max : 0.0f;
     const FixedPass f = table.begin(lane_max);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) table.add_wave(keys[k], v[k], n, grad_texels + c0, C, f);
+    for (int k = 0; k < 8; ++k) {
+      float v[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] = gc[c] * tap_weight[k];
+      table.add_wave(tap_key[k], v, n, grad_texels + c0, C, f);
+    }
     __syncthreads();
     table.flush(grad_texels + c0, C, n, f);
     if (c0 + 4 < C) {
@@ -816,6 +828,8 @@ MipLevels copy_levels(int n, const int32_t* h, const int32_t* w, const int64_t* 
 
 bool valid_args(const DrTextureArgs* a) {
   if (!a || !a->texels || !a->uv || a->batch < 0 || a->height <= 0 || a->width <= 0) return false;
+  // Texel rows of the packed buffer are 32-bit keys of the backward pass's scatter table.
+  if (a->num_texels < 0 || (int64_t)a->tex_batch * a->num_texels >= 0xffffffffLL) return false;
   if (a->channels <= 0 || a->tex_batch < 1 || a->num_levels < 1 || a->num_levels > DR_MAX_LEVELS)
     return false;
   if (a->filter < 0 || a->filter > 3 || a->boundary < 0 || a->boundary > 3) return false;
