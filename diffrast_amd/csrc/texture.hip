@@ -394,8 +394,11 @@ struct Lookup {
   CubeProj P;
 };
 
+// CUBE: a.boundary is DR_BOUNDARY_CUBE (the kernels are compiled for both cases, so that the
+// 2D one carries no cube-map state).
+template <bool CUBE>
 __device__ __forceinline__ void lookup_setup(const DrTextureArgs& a, int64_t pixel, Lookup& K) {
-  const bool cube = a.boundary == DR_BOUNDARY_CUBE;
+  constexpr bool cube = CUBE;
   const bool mip = a.filter == DR_FILTER_MIP_NEAREST || a.filter == DR_FILTER_MIP_LINEAR;
   K.mip = mip;
   K.dir_invalid = false;
@@ -475,14 +478,14 @@ __device__ __forceinline__ bool nearest_setup(const DrTextureArgs& a, const Look
 
 // NC channels per pass (the channel count when it is 1-4; 4 with a loop for more). Every tap
 // of a pass is loaded before its stores.
-template <int NC>
+template <int NC, bool CUBE>
 __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* __restrict__ out) {
   const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (pixel >= (int64_t)a.batch * a.height * a.width) return;
   const int C = a.channels;
   float* o = out + pixel * C;
   Lookup K;
-  lookup_setup(a, pixel, K);
+  lookup_setup<CUBE>(a, pixel, K);
   if (K.dir_invalid) {
     for (int c = 0; c < C; ++c) o[c] = 0.0f;
     return;
@@ -585,7 +588,7 @@ __device__ __forceinline__ void level_taps(const Bilinear& L, float level_weight
   }
 }
 
-template <int NC>
+template <int NC, bool CUBE>
 __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const float* grad_out,
                                                       float* grad_texels, float* grad_uv,
                                                       float* grad_uv_da, float* grad_bias) {
@@ -595,7 +598,7 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   const int64_t pixel = tp.pixel;
   const int C = a.channels;
-  const bool cube = a.boundary == DR_BOUNDARY_CUBE;
+  constexpr bool cube = CUBE;
   const float* g = grad_out + (tp.inside ? pixel * C : 0);
   const int64_t tex_off = a.tex_batch > 1 ? (int64_t)tp.b * a.num_texels : 0;
   const float* texels = a.texels + tex_off * C;
@@ -612,7 +615,7 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
   float g_s = 0.0f, g_t = 0.0f, g_lod = 0.0f;
   bool live = false;
   if (tp.inside) {
-    lookup_setup(a, pixel, K);
+    lookup_setup<CUBE>(a, pixel, K);
     live = !K.dir_invalid;
   }
   if (live && K.levels == 0) {
@@ -698,7 +701,9 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     if (!finite) g_max = __int_as_float(0x7f800000);
     const float lane_max = w_max > 0.0f ? g_max * w_max : 0.0f;
     const FixedPass f = table.begin(lane_max);
-#pragma unroll
+    // One tap at a time (the tap index is uniform): unrolled, the taps' table updates would
+    // interleave and hold many more registers.
+#pragma unroll 1
     for (int k = 0; k < 8; ++k) {
       float v[4];
 #pragma unroll
@@ -828,8 +833,6 @@ MipLevels copy_levels(int n, const int32_t* h, const int32_t* w, const int64_t* 
 
 bool valid_args(const DrTextureArgs* a) {
   if (!a || !a->texels || !a->uv || a->batch < 0 || a->height <= 0 || a->width <= 0) return false;
-  // Texel rows of the packed buffer are 32-bit keys of the backward pass's scatter table.
-  if (a->num_texels < 0 || (int64_t)a->tex_batch * a->num_texels >= 0xffffffffLL) return false;
   if (a->channels <= 0 || a->tex_batch < 1 || a->num_levels < 1 || a->num_levels > DR_MAX_LEVELS)
     return false;
   if (a->filter < 0 || a->filter > 3 || a->boundary < 0 || a->boundary > 3) return false;
@@ -861,9 +864,13 @@ extern "C" int dr_texture_forward(const DrTextureArgs* a, float* out, void* stre
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0) return DR_OK;
   const DrTextureArgs args = *a;
+  const bool cube = args.boundary == DR_BOUNDARY_CUBE;
   return dispatch_channels(args.channels, [&](auto nc) {
-    tex_fwd_kernel<decltype(nc)::value>
-        <<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(args, out);
+    constexpr int NC = decltype(nc)::value;
+    if (cube)
+      tex_fwd_kernel<NC, true><<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(args, out);
+    else
+      tex_fwd_kernel<NC, false><<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(args, out);
     return launch_status();
   });
 }
@@ -876,11 +883,18 @@ extern "C" int dr_texture_backward(const DrTextureArgs* a, const float* grad_out
   if (pixels == 0) return DR_OK;
   if ((int64_t)a->tex_batch * a->num_texels >= 0xffffffffLL) return DR_ERR_ARGUMENT;
   const DrTextureArgs args = *a;
+  const bool cube = args.boundary == DR_BOUNDARY_CUBE;
+  const int64_t blocks = tile_blocks(args.batch, args.height, args.width);
+  float* g_da = args.uv_da ? grad_uv_da : nullptr;
+  float* g_bias = args.bias ? grad_bias : nullptr;
   return dispatch_channels(args.channels, [&](auto nc) {
-    tex_bwd_kernel<decltype(nc)::value>
-        <<<tile_blocks(args.batch, args.height, args.width), 256, 0, (hipStream_t)stream>>>(
-            args, grad_out, grad_texels, grad_uv, args.uv_da ? grad_uv_da : nullptr,
-            args.bias ? grad_bias : nullptr);
+    constexpr int NC = decltype(nc)::value;
+    if (cube)
+      tex_bwd_kernel<NC, true><<<blocks, 256, 0, (hipStream_t)stream>>>(
+          args, grad_out, grad_texels, grad_uv, g_da, g_bias);
+    else
+      tex_bwd_kernel<NC, false><<<blocks, 256, 0, (hipStream_t)stream>>>(
+          args, grad_out, grad_texels, grad_uv, g_da, g_bias);
     return launch_status();
   });
 }
