@@ -397,12 +397,22 @@ __device__ __forceinline__ uint32_t order_bucket(const Workspace& ws, int t) {
   return code >> 18;
 }
 
+// The bucket passes give each workgroup 4096 triangles (16 per thread), so that clearing and
+// flushing its LDS histogram of kOrderBuckets counts is paid once per 4096 triangles.
+constexpr int kOrderPerThread = 16;
+
 __global__ __launch_bounds__(256) void order_count(DrRasterGeometry g, Workspace ws) {
   __shared__ uint32_t hist[kOrderBuckets];
   for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x) hist[i] = 0u;
   __syncthreads();
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < g.num_tri) atomicAdd(hist + order_bucket(ws, t), 1u);
+  const int64_t first = (int64_t)blockIdx.x * blockDim.x * kOrderPerThread;
+  for (int i = 0; i < kOrderPerThread; ++i) {
+    const int64_t t = first + (int64_t)i * blockDim.x + threadIdx.x;
+    if (t >= g.num_tri) break;
+    const uint32_t bucket = order_bucket(ws, (int)t);
+    ws.centroids[t].w = __uint_as_float(bucket);  // for order_place
+    atomicAdd(hist + bucket, 1u);
+  }
   __syncthreads();
   for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x)
     if (hist[i]) atomicAdd(ws.bucket_counts + i, hist[i]);
@@ -437,16 +447,24 @@ __global__ __launch_bounds__(256) void order_place(DrRasterGeometry g, Workspace
   __shared__ uint32_t base[kOrderBuckets];
   for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x) hist[i] = 0u;
   __syncthreads();
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  const uint32_t bucket = t < g.num_tri ? order_bucket(ws, t) : 0u;
-  if (t < g.num_tri) atomicAdd(hist + bucket, 1u);
+  const int64_t first = (int64_t)blockIdx.x * blockDim.x * kOrderPerThread;
+  for (int i = 0; i < kOrderPerThread; ++i) {
+    const int64_t t = first + (int64_t)i * blockDim.x + threadIdx.x;
+    if (t >= g.num_tri) break;
+    atomicAdd(hist + __float_as_uint(ws.centroids[t].w), 1u);
+  }
   __syncthreads();
   for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x) {
     if (hist[i]) base[i] = atomicAdd(ws.bucket_cursor + i, hist[i]);
     hist[i] = 0u;
   }
   __syncthreads();
-  if (t < g.num_tri) ws.order[base[bucket] + atomicAdd(hist + bucket, 1u)] = (uint32_t)t;
+  for (int i = 0; i < kOrderPerThread; ++i) {
+    const int64_t t = first + (int64_t)i * blockDim.x + threadIdx.x;
+    if (t >= g.num_tri) break;
+    const uint32_t bucket = __float_as_uint(ws.centroids[t].w);
+    ws.order[base[bucket] + atomicAdd(hist + bucket, 1u)] = (uint32_t)t;
+  }
 }
 
 // ---- kernels: depth range ----------------------------------------------------------------
@@ -1282,9 +1300,10 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
                                                                      kOrderBuckets, 0u);
       order_centroids<<<tri_blocks, 256, 0, s>>>(*g, ws);
       order_bounds<<<1, 256, 0, s>>>(ws, tri_blocks);
-      order_count<<<tri_blocks, 256, 0, s>>>(*g, ws);
+      const int bucket_blocks = blocks_for(g->num_tri, 256 * kOrderPerThread);
+      order_count<<<bucket_blocks, 256, 0, s>>>(*g, ws);
       order_scan<<<1, 256, 0, s>>>(ws);
-      order_place<<<tri_blocks, 256, 0, s>>>(*g, ws);
+      order_place<<<bucket_blocks, 256, 0, s>>>(*g, ws);
     }
     raster_depth_range<<<ws.depth_ranges * kRangeParts, 256, 0, s>>>(*g, ws);
     raster_depth_range_merge<<<ws.depth_ranges, kRangeParts, 0, s>>>(ws);
