@@ -68,7 +68,8 @@ struct Workspace {
   uint32_t* tile_order;      // [tiles] tile pass order: heavy tiles first within each XCD's share
   float* px;                 // [width] pixel-centre x per column
   float* py;                 // [height] pixel-centre y per row
-  uint32_t* order;           // [num_tri] processing order (instanced meshes only)
+  int4* order;               // [num_tri] processing order (instanced meshes only): the vertex
+                             // rows of each triangle and its row of tri
   float4* centroids;         // [num_tri] clip-space centroids in the first view
   uint32_t* bucket_counts;   // [kOrderBuckets]
   uint32_t* bucket_cursor;   // [kOrderBuckets]
@@ -119,7 +120,7 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
   w.px = (float*)take(sizeof(float) * g.width);
   w.py = (float*)take(sizeof(float) * g.height);
   if (w.ordered) {
-    w.order = (uint32_t*)take(sizeof(uint32_t) * g.num_tri);
+    w.order = (int4*)take(sizeof(int4) * g.num_tri);
     w.centroids = (float4*)take(sizeof(float4) * g.num_tri);
     w.bucket_counts = (uint32_t*)take(sizeof(uint32_t) * kOrderBuckets);
     w.bucket_cursor = (uint32_t*)take(sizeof(uint32_t) * kOrderBuckets);
@@ -134,12 +135,10 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
 // ---- geometry helpers -------------------------------------------------------------------
 
 // (image, triangle row) of triangle instance i.
-__device__ __forceinline__ void instance(const DrRasterGeometry& g, const uint32_t* order,
-                                         int64_t i, int& b, int& t) {
+__device__ __forceinline__ void instance(const DrRasterGeometry& g, int64_t i, int& b, int& t) {
   if (g.ranges == nullptr) {
     b = (int)(i / g.num_tri);
-    const int j = (int)(i - (int64_t)b * g.num_tri);
-    t = order != nullptr ? (int)order[j] : j;
+    t = (int)(i - (int64_t)b * g.num_tri);
     return;
   }
   int lo = 0, hi = g.batch;  // largest b with range_prefix[b] <= i
@@ -151,12 +150,8 @@ __device__ __forceinline__ void instance(const DrRasterGeometry& g, const uint32
   t = g.ranges[2 * b] + (int)(i - g.range_prefix[b]);
 }
 
-__device__ __forceinline__ void load_tri(const DrRasterGeometry& g, int b, int t, Tri& T,
-                                         int (&v)[3]) {
-  const int32_t* row = g.tri + 3 * (int64_t)t;
-  v[0] = row[0];
-  v[1] = row[1];
-  v[2] = row[2];
+__device__ __forceinline__ void load_vertices(const DrRasterGeometry& g, int b, const int (&v)[3],
+                                              Tri& T) {
   const float* base = g.pos + (int64_t)b * g.pos_batch_stride;
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
@@ -168,6 +163,15 @@ __device__ __forceinline__ void load_tri(const DrRasterGeometry& g, int b, int t
   }
   T.reach_x = reach(T.x, T.w);
   T.reach_y = reach(T.y, T.w);
+}
+
+__device__ __forceinline__ void load_tri(const DrRasterGeometry& g, int b, int t, Tri& T,
+                                         int (&v)[3]) {
+  const int32_t* row = g.tri + 3 * (int64_t)t;
+  v[0] = row[0];
+  v[1] = row[1];
+  v[2] = row[2];
+  load_vertices(g, b, v, T);
 }
 
 __device__ __forceinline__ bool finite_tri(const Tri& T) {
@@ -197,6 +201,38 @@ __device__ __forceinline__ void axis_range(float n0, float n1, float n2, int siz
   hi = min((int)floorf(c), size - 1);
 }
 
+// Reciprocal of w (w > 0) through the hardware's approximate reciprocal, within 1 ulp: enough
+// for bounds that carry margins far wider than that (boxes, depth bounds and slabs); 0 when it
+// does not give a finite value, for the caller to divide instead.
+__device__ __forceinline__ float approx_rcp(float w) {
+  const float r = __builtin_amdgcn_rcpf(w);
+  return isfinite(r) ? r : 0.0f;
+}
+
+// x / w and y / w of the vertices (every w > 0), with approx_rcp where it serves.
+__device__ __forceinline__ void ndc(const Tri& T, float (&nx)[3], float (&ny)[3]) {
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const float r = approx_rcp(T.w[k]);
+    nx[k] = T.x[k] * r;
+    ny[k] = T.y[k] * r;
+    if (r == 0.0f || !isfinite(nx[k]) || !isfinite(ny[k])) {
+      nx[k] = T.x[k] / T.w[k];
+      ny[k] = T.y[k] / T.w[k];
+    }
+  }
+}
+
+// z / w of the vertices (every w > 0), likewise.
+__device__ __forceinline__ void vertex_depths(const Tri& T, float (&d)[3]) {
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const float r = approx_rcp(T.w[k]);
+    d[k] = T.z[k] * r;
+    if (r == 0.0f || !isfinite(d[k])) d[k] = T.z[k] / T.w[k];
+  }
+}
+
 // Box [x_lo, x_hi] x [y_lo, y_hi] of the pixel centres a triangle may cover; empty (lo > hi)
 // for a culled triangle. A triangle crossing the camera plane may cover any pixel.
 __device__ __forceinline__ void candidate_box(const DrRasterGeometry& g, const Tri& T, int& x_lo,
@@ -206,8 +242,10 @@ __device__ __forceinline__ void candidate_box(const DrRasterGeometry& g, const T
   const bool any_front = T.w[0] > 0.0f || T.w[1] > 0.0f || T.w[2] > 0.0f;
   if (!finite_tri(T) || !any_front) return;
   if (T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
-    axis_range(T.x[0] / T.w[0], T.x[1] / T.w[1], T.x[2] / T.w[2], g.width, x_lo, x_hi);
-    axis_range(T.y[0] / T.w[0], T.y[1] / T.w[1], T.y[2] / T.w[2], g.height, y_lo, y_hi);
+    float nx[3], ny[3];
+    ndc(T, nx, ny);
+    axis_range(nx[0], nx[1], nx[2], g.width, x_lo, x_hi);
+    axis_range(ny[0], ny[1], ny[2], g.height, y_lo, y_hi);
   } else {
     x_hi = g.width - 1;
     y_hi = g.height - 1;
@@ -463,7 +501,9 @@ __global__ __launch_bounds__(256) void order_place(DrRasterGeometry g, Workspace
     const int64_t t = first + (int64_t)i * blockDim.x + threadIdx.x;
     if (t >= g.num_tri) break;
     const uint32_t bucket = __float_as_uint(ws.centroids[t].w);
-    ws.order[base[bucket] + atomicAdd(hist + bucket, 1u)] = (uint32_t)t;
+    const int32_t* row = g.tri + 3 * t;
+    ws.order[base[bucket] + atomicAdd(hist + bucket, 1u)] =
+        make_int4(row[0], row[1], row[2], (int)t);
   }
 }
 
@@ -527,7 +567,9 @@ __global__ __launch_bounds__(kRangeParts) void raster_depth_range_merge(Workspac
 // Triangles that cross the camera plane go first (slab 0).
 __device__ __forceinline__ int depth_slab(const Workspace& ws, int range, const Tri& T) {
   if (!(T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f)) return 0;
-  const float nearest = fminf(fminf(T.z[0] / T.w[0], T.z[1] / T.w[1]), T.z[2] / T.w[2]);
+  float d[3];
+  vertex_depths(T, d);
+  const float nearest = fminf(fminf(d[0], d[1]), d[2]);
   const float lo = from_ordered_bits(ws.depth_range[2 * range]);
   const float hi = from_ordered_bits(ws.depth_range[2 * range + 1]);
   const float f = (nearest - lo) / (hi - lo) * (float)kDepthSlabs;
@@ -576,9 +618,19 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
   int b = 0, t = 0, x_lo = 0, x_hi = -1, y_lo = 0, y_hi = -1;
   Tri T;
   if (i < g.num_instances) {
-    instance(g, ws.ordered ? ws.order : nullptr, i, b, t);
     int v[3];
-    load_tri(g, b, t, T, v);
+    if (ws.ordered) {  // the ordered triangle carries its vertex rows: one load fewer in line
+      b = (int)(i / g.num_tri);
+      const int4 o = ws.order[i - (int64_t)b * g.num_tri];
+      v[0] = o.x;
+      v[1] = o.y;
+      v[2] = o.z;
+      t = o.w;
+      load_vertices(g, b, v, T);
+    } else {
+      instance(g, i, b, t);
+      load_tri(g, b, t, T, v);
+    }
     candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
     if (x_lo <= x_hi && y_lo <= y_hi) {
       const int64_t count = (int64_t)(x_hi - x_lo + 1) * (y_hi - y_lo + 1);
@@ -958,9 +1010,11 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
       // camera plane).
       float bound = -__int_as_float(0x7f800000);
       if (T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
-        const float d0 = T.z[0] / T.w[0], d1 = T.z[1] / T.w[1], d2 = T.z[2] / T.w[2];
-        const float nearest = fminf(fminf(d0, d1), d2);
-        const float scale = fmaxf(fmaxf(fabsf(d0), fabsf(d1)), fabsf(d2));
+        // approx_rcp's error (2^-22 relative) is far inside the margin.
+        float d[3];
+        vertex_depths(T, d);
+        const float nearest = fminf(fminf(d[0], d[1]), d[2]);
+        const float scale = fmaxf(fmaxf(fabsf(d[0]), fabsf(d[1])), fabsf(d[2]));
         bound = nearest - 1e-5f * scale;
       }
       s_bound[threadIdx.x] = bound;
