@@ -22,12 +22,11 @@ struct Pixel {
   float u, v;
 };
 
-// Reads rast for `pixel` of `image` and, for a covered pixel, the triangle's index row.
+// The pixel of `image` whose rast value is r and, for a covered pixel, its triangle's index row.
 // rows_per_image is 0 for attributes shared by all images.
-__device__ __forceinline__ Pixel load_pixel(const DrInterpolateArgs& a, int64_t pixel, int image,
-                                            uint32_t rows_per_image) {
+__device__ __forceinline__ Pixel pixel_of(const DrInterpolateArgs& a, const float4& r, int image,
+                                          uint32_t rows_per_image) {
   Pixel p;
-  const float4 r = load4(a.rast + 4 * pixel);
   // rast stores id + 1 as a float; ids past the end of tri are background (reference.py:128).
   const float id = rintf(r.w);
   p.valid = id >= 1.0f && id <= (float)a.num_tri;
@@ -44,10 +43,45 @@ __device__ __forceinline__ Pixel load_pixel(const DrInterpolateArgs& a, int64_t 
   return p;
 }
 
+__device__ __forceinline__ Pixel load_pixel(const DrInterpolateArgs& a, int64_t pixel, int image,
+                                            uint32_t rows_per_image) {
+  return pixel_of(a, load4(a.rast + 4 * pixel), image, rows_per_image);
+}
+
 // The three attribute rows of a pixel, channels [c0, c0 + N), in registers (0 past C).
 template <int N>
 __device__ __forceinline__ void load_rows(const float* attr, const Pixel& p, int C, int c0,
                                           float (&A)[3][N]) {
+  // Whole-row loads when every row of the pass is 16-byte aligned: a condition on the buffer
+  // and the channel count alone, the same for every lane.
+  if constexpr (N % 4 == 0) {
+    if (C % 4 == 0 && c0 + N <= C && (reinterpret_cast<uintptr_t>(attr) & 15u) == 0) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const float4* row = reinterpret_cast<const float4*>(attr + (int64_t)p.row[k] * C + c0);
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+          const float4 q = row[i];
+          A[k][4 * i] = q.x;
+          A[k][4 * i + 1] = q.y;
+          A[k][4 * i + 2] = q.z;
+          A[k][4 * i + 3] = q.w;
+        }
+      }
+      return;
+    }
+  }
+  if constexpr (N == 2) {
+    if (C == 2 && (reinterpret_cast<uintptr_t>(attr) & 7u) == 0) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const float2 q = reinterpret_cast<const float2*>(attr)[p.row[k]];
+        A[k][0] = q.x;
+        A[k][1] = q.y;
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
     const float* row = attr + (int64_t)p.row[k] * C + c0;
@@ -68,50 +102,73 @@ __device__ __forceinline__ float pick(const float (&row)[N], int c) {
 // Channels per pass of the generic kernel (any channel count).
 constexpr int kGenericChannels = 4;
 
-// One thread per pixel, in pixel order. Every load of a pixel is issued before its stores.
-template <int NC>
+// PPT pixels per thread, 256 apart (each load instruction of a wave stays coalesced). The
+// pixels' loads go out level by level -- rast, then the triangles' index rows, then the
+// attribute rows -- so that a thread waits once per level for all its pixels, not once per
+// pixel: the gathers are latency-bound.
+template <int NC, int PPT>
 __global__ __launch_bounds__(256) void interp_fwd_kernel(DrInterpolateArgs a,
                                                          float* __restrict__ out,
                                                          float* __restrict__ out_da,
                                                          uint32_t rows_per_image) {
-  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t image_pixels = (int64_t)a.height * a.width;
-  if (pixel >= (int64_t)a.batch * image_pixels) return;
-  const int image = image_pixels < 0x7fffffff && pixel < 0x7fffffff
-                        ? (int)((uint32_t)pixel / (uint32_t)image_pixels)
-                        : (int)(pixel / image_pixels);
+  const int64_t total = (int64_t)a.batch * image_pixels;
+  const int64_t first = (int64_t)blockIdx.x * blockDim.x * PPT + threadIdx.x;
   const int C = NC > 0 ? NC : a.channels;
-  const Pixel p = load_pixel(a, pixel, image, rows_per_image);
-  const float w = 1.0f - p.u - p.v;
-  float4 db = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (out_da != nullptr && p.valid) db = load4(a.rast_db + 4 * pixel);  // du/dx, du/dy, dv/dx, dv/dy
-  float* o = out + pixel * C;
   constexpr int N = NC > 0 ? NC : kGenericChannels;
+  int64_t pixel[PPT];
+  float4 r[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    pixel[j] = first + (int64_t)j * blockDim.x;
+    r[j] = pixel[j] < total ? load4(a.rast + 4 * pixel[j]) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  Pixel p[PPT];
+  float4 db[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const int image = image_pixels < 0x7fffffff && pixel[j] < 0x7fffffff
+                          ? (int)((uint32_t)pixel[j] / (uint32_t)image_pixels)
+                          : (int)(pixel[j] / image_pixels);
+    p[j] = pixel_of(a, r[j], image, rows_per_image);
+    db[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (out_da != nullptr && p[j].valid) db[j] = load4(a.rast_db + 4 * pixel[j]);  // du/dx, du/dy, dv/dx, dv/dy
+  }
   for (int c0 = 0; c0 < C; c0 += N) {
-    float A[3][N];
-    if (p.valid) {
-      load_rows<N>(a.attr, p, C, c0, A);
-    } else {
+    float A[PPT][3][N];
 #pragma unroll
-      for (int c = 0; c < N; ++c) A[0][c] = A[1][c] = A[2][c] = 0.0f;
-    }
-    float res[N];
+    for (int j = 0; j < PPT; ++j) {
+      if (p[j].valid) {
+        load_rows<N>(a.attr, p[j], C, c0, A[j]);
+      } else {
 #pragma unroll
-    for (int c = 0; c < N; ++c) res[c] = p.valid ? p.u * A[0][c] + p.v * A[1][c] + w * A[2][c] : 0.0f;
-    if (out_da != nullptr) {
-      float* od = out_da + pixel * 2 * a.num_diff;
-      for (int k = 0; k < a.num_diff; ++k) {
-        const int c = a.diff[k] - c0;
-        if (c < 0 || c >= N) continue;
-        const float da_du = pick(A[0], c) - pick(A[2], c);
-        const float da_dv = pick(A[1], c) - pick(A[2], c);
-        od[2 * k] = p.valid ? db.x * da_du + db.z * da_dv : 0.0f;
-        od[2 * k + 1] = p.valid ? db.y * da_du + db.w * da_dv : 0.0f;
+        for (int c = 0; c < N; ++c) A[j][0][c] = A[j][1][c] = A[j][2][c] = 0.0f;
       }
     }
 #pragma unroll
-    for (int c = 0; c < N; ++c)
-      if (c0 + c < C) o[c0 + c] = res[c];
+    for (int j = 0; j < PPT; ++j) {
+      if (pixel[j] >= total) continue;
+      const float u = p[j].u, v = p[j].v, w = 1.0f - u - v;
+      float res[N];
+#pragma unroll
+      for (int c = 0; c < N; ++c)
+        res[c] = p[j].valid ? u * A[j][0][c] + v * A[j][1][c] + w * A[j][2][c] : 0.0f;
+      if (out_da != nullptr) {
+        float* od = out_da + pixel[j] * 2 * a.num_diff;
+        for (int k = 0; k < a.num_diff; ++k) {
+          const int c = a.diff[k] - c0;
+          if (c < 0 || c >= N) continue;
+          const float da_du = pick(A[j][0], c) - pick(A[j][2], c);
+          const float da_dv = pick(A[j][1], c) - pick(A[j][2], c);
+          od[2 * k] = p[j].valid ? db[j].x * da_du + db[j].z * da_dv : 0.0f;
+          od[2 * k + 1] = p[j].valid ? db[j].y * da_du + db[j].w * da_dv : 0.0f;
+        }
+      }
+      float* o = out + pixel[j] * C;
+#pragma unroll
+      for (int c = 0; c < N; ++c)
+        if (c0 + c < C) o[c0 + c] = res[c];
+    }
   }
 }
 
@@ -260,9 +317,12 @@ extern "C" int dr_interpolate_forward(const DrInterpolateArgs* a, float* out, fl
   if (pixels == 0 || (a->channels == 0 && a->num_diff == 0)) return DR_OK;
   const DrInterpolateArgs args = *a;
   const uint32_t rows_per_image = image_rows(args);
+  float* da = args.num_diff > 0 ? out_da : nullptr;
   return dispatch_channels(args.channels, [&](auto nc) {
-    interp_fwd_kernel<decltype(nc)::value><<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
-        args, out, args.num_diff > 0 ? out_da : nullptr, rows_per_image);
+    constexpr int NC = decltype(nc)::value;
+    constexpr int PPT = NC > 0 ? 2 : 1;  // pixels per thread
+    interp_fwd_kernel<NC, PPT><<<blocks_for(pixels, 256 * PPT), 256, 0, (hipStream_t)stream>>>(
+        args, out, da, rows_per_image);
     return launch_status();
   });
 }
