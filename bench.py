@@ -104,10 +104,10 @@ class KernelTimer:
 
 
 # Tile rasterization, per tile list entry: the entry (4 B) and the 64-byte record it names
-# (three clip-space vertices, triangle row, tile rectangle); per work chunk: the 256 keys of its
-# tile read and merged (16 B each).
+# (three clip-space vertices, triangle row, tile rectangle); per tile with entries: its 256
+# keys read and written once (16 B each).
 TILE_ENTRY_BYTES = 4 + 64
-TILE_CHUNK_BYTES = 256 * 16
+TILE_KEY_BYTES = 256 * 16
 
 
 def _struct(arg):
@@ -143,7 +143,7 @@ class BytesModel:
 
     def raster_visibility_tiles(self, args):
         counts = args[6]
-        return counts[1] * TILE_ENTRY_BYTES + counts[2] * TILE_CHUNK_BYTES
+        return counts[1] * TILE_ENTRY_BYTES + counts[2] * TILE_KEY_BYTES
 
     def resolve_forward(self, args):
         P = self._pixels(_struct(args[0]))

@@ -63,7 +63,7 @@ struct Workspace {
                              // farthest vertex depth of an image (one when pos is shared)
   uint32_t* range_parts;     // [depth_ranges][kRangeParts][2] partial spans
   uint2* block_sums;         // [scan blocks] (entries, chunks)
-  uint32_t* counters;        // [1] entries, [2] chunks
+  uint32_t* counters;        // [1] entries, [2] list chunks (scan by-product), [3] busy tiles
   uint32_t* block_records;   // [record_blocks] binned triangles of each setup workgroup
   uint32_t* tile_order;      // [tiles] tile pass order: heavy tiles first within each XCD's share
   float* px;                 // [width] pixel-centre x per column
@@ -866,6 +866,16 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
     }
 }
 
+// Number of tiles with binned triangles (counters[3]), the workgroups of the tile pass that
+// have work. One thread per tile, one atomic per wave.
+__global__ __launch_bounds__(256) void raster_count_tiles(Workspace ws) {
+  const int64_t tile = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool busy = tile < ws.tiles && ws.list_offsets[(tile + 1) * kDepthSlabs] >
+                                           ws.list_offsets[tile * kDepthSlabs];
+  const uint64_t mask = __ballot(busy);
+  if (lane_id() == 0 && mask != 0) atomicAdd(ws.counters + 3, (uint32_t)__popcll(mask));
+}
+
 // The order in which the tile pass takes the tiles: each XCD keeps its contiguous share of
 // them (xcd_order), and within the share the tiles with the most binned triangles go first, so
 // that the longest workgroups do not start last. A counting sort by entry count in classes of
@@ -1368,6 +1378,7 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
     raster_scan_apply<<<ws.scan_blocks, 256, 0, s>>>(ws.list_counts, ws.lists, ws.block_sums,
                                                      ws.list_offsets, ws.list_cursor,
                                                      ws.chunk_offsets);
+    raster_count_tiles<<<blocks_for(ws.tiles, 256), 256, 0, s>>>(ws);
   }
   int status = launch_status();
   if (status != DR_OK) return status;
@@ -1377,7 +1388,7 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
     return DR_ERR_HIP;
   counts[0] = (uint32_t)ws.record_blocks;
   counts[1] = host[1];
-  counts[2] = host[2];
+  counts[2] = host[3];
   return DR_OK;
 }
 
@@ -1391,6 +1402,7 @@ extern "C" int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspa
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
   raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, entries);
+  raster_tile_order<<<8, 1024, 0, s>>>(ws);
   return launch_status();
 }
 
@@ -1404,7 +1416,6 @@ extern "C" int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint6
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
-  raster_tile_order<<<8, 1024, 0, s>>>(ws);
   raster_tile_kernel<<<(unsigned)ws.tiles, 256, 0, s>>>(*g, prev_keys, keys, ws, entries);
   return launch_status();
 }
