@@ -66,6 +66,9 @@ struct Workspace {
   uint32_t* counters;        // [1] entries, [2] list chunks (scan by-product), [3] busy tiles
   uint32_t* block_records;   // [record_blocks] binned triangles of each setup workgroup
   uint32_t* tile_order;      // [tiles] tile pass order: heavy tiles first within each XCD's share
+  uint8_t* tile_class;       // [tiles] work class of each tile (entries / 32, capped)
+  uint32_t* class_counts;    // [8][kWorkClasses] tiles per (XCD share, class)
+  uint32_t* class_cursor;    // [8][kWorkClasses] fill positions of the placement pass
   float* px;                 // [width] pixel-centre x per column
   float* py;                 // [height] pixel-centre y per row
   int4* order;               // [num_tri] processing order (instanced meshes only): the vertex
@@ -117,6 +120,9 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
   w.block_sums = (uint2*)take(sizeof(uint2) * (w.scan_blocks + 1));
   w.block_records = (uint32_t*)take(sizeof(uint32_t) * w.record_blocks);
   w.tile_order = (uint32_t*)take(sizeof(uint32_t) * w.tiles);
+  w.tile_class = (uint8_t*)take(w.tiles);
+  w.class_counts = (uint32_t*)take(sizeof(uint32_t) * 8 * kWorkClasses);
+  w.class_cursor = (uint32_t*)take(sizeof(uint32_t) * 8 * kWorkClasses);
   w.px = (float*)take(sizeof(float) * g.width);
   w.py = (float*)take(sizeof(float) * g.height);
   if (w.ordered) {
@@ -866,50 +872,91 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
     }
 }
 
-// Number of tiles with binned triangles (counters[3]), the workgroups of the tile pass that
-// have work. One thread per tile, one atomic per wave.
-__global__ __launch_bounds__(256) void raster_count_tiles(Workspace ws) {
-  const int64_t tile = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const bool busy = tile < ws.tiles && ws.list_offsets[(tile + 1) * kDepthSlabs] >
-                                           ws.list_offsets[tile * kDepthSlabs];
-  const uint64_t mask = __ballot(busy);
-  if (lane_id() == 0 && mask != 0) atomicAdd(ws.counters + 3, (uint32_t)__popcll(mask));
+// ---- tile order: heavy tiles first within each XCD's share -----------------------------------
+//
+// The tile pass takes tiles in this order: each XCD keeps its contiguous share of them
+// (xcd_order), and within the share the tiles with the most binned triangles go first, so that
+// the longest workgroups do not start last. A counting sort by entry count in kWorkClasses
+// classes of 32 entries, in three passes over the tiles (classes and their counts, the class
+// cursors, placement); workgroups aggregate in LDS before touching global counters. The order
+// within a class is free: tiles are independent.
+
+constexpr int kXcdShares = 8;
+
+// The XCD share of tile i under xcd_order, and the first tile of share k.
+__device__ __forceinline__ int xcd_share(int64_t i, int64_t tiles) {
+  if (tiles < kXcdShares) return (int)i;
+  const int64_t per = tiles / kXcdShares, extra = tiles % kXcdShares;
+  const int64_t big = extra * (per + 1);
+  return i < big ? (int)(i / (per + 1)) : (int)(extra + (i - big) / per);
+}
+__device__ __forceinline__ int64_t share_start(int k, int64_t tiles) {
+  if (tiles < kXcdShares) return k;
+  const int64_t per = tiles / kXcdShares, extra = tiles % kXcdShares;
+  return k * per + (k < extra ? k : extra);
 }
 
-// The order in which the tile pass takes the tiles: each XCD keeps its contiguous share of
-// them (xcd_order), and within the share the tiles with the most binned triangles go first, so
-// that the longest workgroups do not start last. A counting sort by entry count in classes of
-// 32 entries; the order within a class is free (tiles are independent). One 1024-thread
-// workgroup per XCD share.
-__global__ __launch_bounds__(1024) void raster_tile_order(Workspace ws) {
-  __shared__ uint32_t s_count[kWorkClasses];
-  const int64_t tiles = ws.tiles;
-  constexpr int kXcds = 8;
-  const int64_t per = tiles / kXcds, extra = tiles % kXcds, k = blockIdx.x;
-  const int64_t start = k * per + (k < extra ? k : extra);
-  const int64_t own = tiles < kXcds ? (k < tiles ? 1 : 0) : per + (k < extra ? 1 : 0);
-  for (int c = threadIdx.x; c < kWorkClasses; c += blockDim.x) s_count[c] = 0u;
+// Pass 1, one thread per tile: its class (kept for pass 3), the class counts of each share and
+// the number of tiles with binned triangles (counters[3], the tile pass's busy workgroups).
+__global__ __launch_bounds__(256) void raster_tile_classes(Workspace ws) {
+  __shared__ uint32_t hist[kXcdShares * kWorkClasses];
+  __shared__ uint32_t busy;
+  for (int i = threadIdx.x; i < kXcdShares * kWorkClasses; i += blockDim.x) hist[i] = 0u;
+  if (threadIdx.x == 0) busy = 0u;
   __syncthreads();
-  auto work_class = [&](int64_t tile) {
-    const uint32_t n = ws.list_offsets[(tile + 1) * kDepthSlabs] - ws.list_offsets[tile * kDepthSlabs];
-    return (int)min(n >> 5, (uint32_t)(kWorkClasses - 1));
-  };
-  for (int64_t i = threadIdx.x; i < own; i += blockDim.x)
-    atomicAdd(s_count + work_class(start + i), 1u);
+  const int64_t tile = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  bool has = false;
+  if (tile < ws.tiles) {
+    const uint32_t n =
+        ws.list_offsets[(tile + 1) * kDepthSlabs] - ws.list_offsets[tile * kDepthSlabs];
+    const int c = (int)min(n >> 5, (uint32_t)(kWorkClasses - 1));
+    ws.tile_class[tile] = (uint8_t)c;
+    atomicAdd(hist + xcd_share(tile, ws.tiles) * kWorkClasses + c, 1u);
+    has = n > 0;
+  }
+  const uint64_t mask = __ballot(has);
+  if (lane_id() == 0 && mask != 0) atomicAdd(&busy, (uint32_t)__popcll(mask));
   __syncthreads();
-  if (threadIdx.x == 0) {  // first position of each class, heaviest class first
-    uint32_t run = 0u;
+  for (int i = threadIdx.x; i < kXcdShares * kWorkClasses; i += blockDim.x)
+    if (hist[i]) atomicAdd(ws.class_counts + i, hist[i]);
+  if (threadIdx.x == 0 && busy) atomicAdd(ws.counters + 3, busy);
+}
+
+// Pass 2, one workgroup: first position of each class in its share, heaviest class first.
+__global__ __launch_bounds__(256) void raster_tile_cursors(Workspace ws) {
+  __shared__ uint32_t counts[kXcdShares * kWorkClasses];
+  for (int i = threadIdx.x; i < kXcdShares * kWorkClasses; i += blockDim.x)
+    counts[i] = ws.class_counts[i];
+  __syncthreads();
+  if (threadIdx.x < kXcdShares) {
+    const int k = threadIdx.x;
+    uint32_t run = (uint32_t)share_start(k, ws.tiles);
     for (int c = kWorkClasses - 1; c >= 0; --c) {
-      const uint32_t n = s_count[c];
-      s_count[c] = run;
-      run += n;
+      ws.class_cursor[k * kWorkClasses + c] = run;
+      run += counts[k * kWorkClasses + c];
     }
   }
+}
+
+// Pass 3, one thread per tile: its place in the order.
+__global__ __launch_bounds__(256) void raster_tile_place(Workspace ws) {
+  __shared__ uint32_t hist[kXcdShares * kWorkClasses];
+  __shared__ uint32_t base[kXcdShares * kWorkClasses];
+  for (int i = threadIdx.x; i < kXcdShares * kWorkClasses; i += blockDim.x) hist[i] = 0u;
   __syncthreads();
-  for (int64_t i = threadIdx.x; i < own; i += blockDim.x) {
-    const uint32_t at = atomicAdd(s_count + work_class(start + i), 1u);
-    ws.tile_order[start + at] = (uint32_t)(start + i);
+  const int64_t tile = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int slot = 0;
+  if (tile < ws.tiles) {
+    slot = xcd_share(tile, ws.tiles) * kWorkClasses + ws.tile_class[tile];
+    atomicAdd(hist + slot, 1u);
   }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kXcdShares * kWorkClasses; i += blockDim.x) {
+    if (hist[i]) base[i] = atomicAdd(ws.class_cursor + i, hist[i]);
+    hist[i] = 0u;
+  }
+  __syncthreads();
+  if (tile < ws.tiles) ws.tile_order[base[slot] + atomicAdd(hist + slot, 1u)] = (uint32_t)tile;
 }
 
 // One workgroup per tile: the tile's keys stay in LDS while it walks the tile's binned
@@ -1355,6 +1402,7 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
   raster_fill_u32<<<(int)std::min<int64_t>(blocks_for(ws.lists + 1, 256), 65536), 256, 0, s>>>(
       ws.list_counts, ws.lists + 1, 0u);
   raster_fill_u32<<<1, 64, 0, s>>>(ws.counters, 4, 0u);
+  raster_fill_u32<<<4, 256, 0, s>>>(ws.class_counts, 8 * kWorkClasses, 0u);
   raster_centres<<<blocks_for(std::max(g->width, g->height), 256), 256, 0, s>>>(
       ws.px, g->width, ws.py, g->height);
   if (g->num_instances > 0) {
@@ -1378,7 +1426,10 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
     raster_scan_apply<<<ws.scan_blocks, 256, 0, s>>>(ws.list_counts, ws.lists, ws.block_sums,
                                                      ws.list_offsets, ws.list_cursor,
                                                      ws.chunk_offsets);
-    raster_count_tiles<<<blocks_for(ws.tiles, 256), 256, 0, s>>>(ws);
+    const int tile_blocks = blocks_for(ws.tiles, 256);
+    raster_tile_classes<<<tile_blocks, 256, 0, s>>>(ws);
+    raster_tile_cursors<<<1, 256, 0, s>>>(ws);
+    raster_tile_place<<<tile_blocks, 256, 0, s>>>(ws);
   }
   int status = launch_status();
   if (status != DR_OK) return status;
@@ -1402,7 +1453,6 @@ extern "C" int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspa
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
   raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, entries);
-  raster_tile_order<<<8, 1024, 0, s>>>(ws);
   return launch_status();
 }
 

@@ -72,8 +72,9 @@ typedef struct DrRasterGeometry {
 int dr_raster_workspace_size(const DrRasterGeometry* g, size_t* bytes);
 
 /* Visibility, first part: clears keys, orders the triangles of a large mesh spatially,
- * rasterizes triangles with a small bounding box directly, and bins the others into 16x16
- * tiles (counts and scan). Waits for the stream and returns in counts[0..2] the number of
+ * rasterizes triangles with a small bounding box directly, bins the others into 16x16 tiles
+ * (counts and scan) and orders the tiles for the tile pass. Waits for the stream and returns
+ * in counts[0..2] the number of
  * setup workgroups (each with up to 256 binned triangles), tile entries, and tiles with at
  * least one entry (the tile pass's workgroups that have work).
  * prev_keys (nullable) is the previous depth layer. */
@@ -81,9 +82,8 @@ int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint64_t* prev_k
                                uint64_t* keys, void* workspace, size_t workspace_bytes,
                                uint32_t counts[3], void* stream);
 
-/* Visibility, second part: fills the per-tile lists and orders the tiles for the third part.
- * entries holds counts[1] uint32: the lists of all tiles, tile by tile, near to far. Nothing
- * to do when counts[1] == 0. (The reference has no binning: its visibility tests every triangle at every
+/* Visibility, second part: fills the per-tile lists. entries holds counts[1] uint32: the
+ * lists of all tiles, tile by tile, near to far. Nothing to do when counts[1] == 0. (The reference has no binning: its visibility tests every triangle at every
  * pixel, reference.py:368-397; _triton_raster.py:241-306 keeps the nearest per pixel.) */
 int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspace, size_t workspace_bytes,
                              uint32_t* entries, const uint32_t counts[3], void* stream);
