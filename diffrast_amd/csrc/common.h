@@ -348,7 +348,7 @@ struct RowTable {
   static constexpr int kProbe = 16;
   static_assert((SLOTS & (SLOTS - 1)) == 0 && CH % 2 == 0, "power-of-two slots, even CH");
   uint32_t keys[SLOTS];
-  long long vals[SLOTS * CH];
+  long long vals[CH * SLOTS];  // channel-major: lanes adding to different rows hit different banks
   uint32_t used[SLOTS];
   uint32_t count;
   float wave_max[256 / DR_WAVE];
@@ -423,10 +423,10 @@ struct RowTable {
     if (f.direct) return false;
     const int slot = slot_of(key);
     if (slot < 0) return false;
-    unsigned long long* row = reinterpret_cast<unsigned long long*>(vals + slot * CH);
+    unsigned long long* col = reinterpret_cast<unsigned long long*>(vals + slot);
 #pragma unroll
     for (int c = 0; c < CH; ++c)
-      if (c < n) atomicAdd(row + c, (unsigned long long)to_fixed(v[c], f));
+      if (c < n) atomicAdd(col + c * SLOTS, (unsigned long long)to_fixed(v[c], f));
     return true;
   }
 
@@ -465,7 +465,7 @@ struct RowTable {
       const int c = (int)(i & ((1u << shift) - 1u));
       if (c >= n) continue;
       const uint32_t slot = used[i >> shift];
-      long long* p = vals + slot * CH + c;
+      long long* p = vals + c * SLOTS + slot;
       const long long x = *p;
       if (x != 0) atomic_add(dst + (int64_t)keys[slot] * stride + c, from_fixed(x, f));
       *p = 0;
