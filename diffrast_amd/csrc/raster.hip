@@ -1216,33 +1216,57 @@ __device__ __forceinline__ void resolve_pixel(const Tri& T, float px, float py, 
   }
 }
 
+// Two pixels per thread, 256 apart; their loads go out level by level (keys, index rows,
+// vertices) so that a thread waits once per level for both.
 __global__ __launch_bounds__(256) void resolve_fwd_kernel(DrRasterGeometry g,
                                                               const uint64_t* keys, float* rast,
                                                               float* rast_db, float scale_x,
                                                               float scale_y) {
-  const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  constexpr int kPixels = 2;
   const int64_t total = (int64_t)g.batch * g.height * g.width;
-  if (pixel >= total) return;
-  const uint64_t key = keys[pixel];
-  if (key == kEmptyKey) {
-    store4(rast + 4 * pixel, make_float4(0.f, 0.f, 0.f, 0.f));
-    if (rast_db) store4(rast_db + 4 * pixel, make_float4(0.f, 0.f, 0.f, 0.f));
-    return;
+  const int64_t first = (int64_t)blockIdx.x * blockDim.x * kPixels + threadIdx.x;
+  int64_t pixel[kPixels];
+  uint64_t key[kPixels];
+#pragma unroll
+  for (int j = 0; j < kPixels; ++j) {
+    pixel[j] = first + (int64_t)j * blockDim.x;
+    key[j] = pixel[j] < total ? keys[pixel[j]] : kEmptyKey;
   }
-  const int t = (int)(uint32_t)key;
-  const int x = (int)(pixel % g.width);
-  const int64_t rest = pixel / g.width;
-  const int y = (int)(rest % g.height);
-  const int b = (int)(rest / g.height);
-  Tri T;
-  int v[3];
-  load_tri(g, b, t, T, v);
-  Resolved R;
-  resolve_pixel(T, pixel_centre(x, g.width), pixel_centre(y, g.height), R);
-  store4(rast + 4 * pixel, make_float4(R.b[0], R.b[1], R.depth, (float)(t + 1)));
-  if (rast_db)
-    store4(rast_db + 4 * pixel, make_float4(R.db_dx[0] * scale_x, R.db_dy[0] * scale_y,
-                                            R.db_dx[1] * scale_x, R.db_dy[1] * scale_y));
+  int v[kPixels][3];
+  int b[kPixels];
+#pragma unroll
+  for (int j = 0; j < kPixels; ++j) {
+    b[j] = 0;
+    v[j][0] = v[j][1] = v[j][2] = 0;
+    if (key[j] == kEmptyKey) continue;
+    const int32_t* row = g.tri + 3 * (int64_t)(uint32_t)key[j];
+    v[j][0] = row[0];
+    v[j][1] = row[1];
+    v[j][2] = row[2];
+    b[j] = (int)(pixel[j] / ((int64_t)g.height * g.width));
+  }
+  Tri T[kPixels];
+#pragma unroll
+  for (int j = 0; j < kPixels; ++j)
+    if (key[j] != kEmptyKey) load_vertices(g, b[j], v[j], T[j]);
+#pragma unroll
+  for (int j = 0; j < kPixels; ++j) {
+    if (pixel[j] >= total) continue;
+    if (key[j] == kEmptyKey) {
+      store4(rast + 4 * pixel[j], make_float4(0.f, 0.f, 0.f, 0.f));
+      if (rast_db) store4(rast_db + 4 * pixel[j], make_float4(0.f, 0.f, 0.f, 0.f));
+      continue;
+    }
+    const int t = (int)(uint32_t)key[j];
+    const int64_t in_image = pixel[j] - (int64_t)b[j] * g.height * g.width;
+    const int y = (int)(in_image / g.width), x = (int)(in_image - (int64_t)y * g.width);
+    Resolved R;
+    resolve_pixel(T[j], pixel_centre(x, g.width), pixel_centre(y, g.height), R);
+    store4(rast + 4 * pixel[j], make_float4(R.b[0], R.b[1], R.depth, (float)(t + 1)));
+    if (rast_db)
+      store4(rast_db + 4 * pixel[j], make_float4(R.db_dx[0] * scale_x, R.db_dy[0] * scale_y,
+                                                 R.db_dx[1] * scale_x, R.db_dy[1] * scale_y));
+  }
 }
 
 __device__ __forceinline__ void cross3(const float* u, const float* v, float* out) {
@@ -1483,7 +1507,7 @@ extern "C" int dr_resolve_forward(const DrRasterGeometry* g, const uint64_t* key
   if (pixels == 0) return DR_OK;
   float sx, sy;
   resolve_scales(g, sx, sy);
-  resolve_fwd_kernel<<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(
+  resolve_fwd_kernel<<<blocks_for(pixels, 512), 256, 0, (hipStream_t)stream>>>(
       *g, keys, rast, rast_db, sx, sy);
   return launch_status();
 }
