@@ -160,15 +160,11 @@ __global__ __launch_bounds__(256) void aa_mark_shown(const float* rast, int64_t 
   mask[row * num_tri + (int64_t)id - 1] = kShown;
 }
 
-// Silhouette bits of each (pos batch, triangle); with shown_only, of the marked ones only (the
-// others stay 0).
-__global__ __launch_bounds__(256) void aa_silhouette_kernel(const float* pos, int64_t stride,
-                                                            int pos_batch, const int32_t* tri,
-                                                            int num_tri, const int32_t* nbr,
-                                                            bool shown_only, uint8_t* mask) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)pos_batch * num_tri) return;
-  if (shown_only && mask[i] != kShown) return;
+// Silhouette bits of (pos batch, triangle) i: bit k when edge k has no partner or both
+// triangles lie on one side of it.
+__device__ __forceinline__ void silhouette_bits(const float* pos, int64_t stride,
+                                                const int32_t* tri, int num_tri,
+                                                const int32_t* nbr, int64_t i, uint8_t* mask) {
   const int b = (int)(i / num_tri);
   const int t = (int)(i - (int64_t)b * num_tri);
   const float* P = pos + (int64_t)b * stride;
@@ -189,6 +185,21 @@ __global__ __launch_bounds__(256) void aa_silhouette_kernel(const float* pos, in
     if (side(line, p[k]) * side(line, theirs) > 0.0f) bits |= (uint8_t)(1u << k);
   }
   mask[i] = bits;
+}
+
+// Silhouette bits of each (pos batch, triangle); with shown_only, of the marked ones only (the
+// others stay 0).
+__global__ __launch_bounds__(256) void aa_silhouette_kernel(const float* pos, int64_t stride,
+                                                            int pos_batch, const int32_t* tri,
+                                                            int num_tri, const int32_t* nbr,
+                                                            bool shown_only, uint8_t* mask) {
+  // A grid-stride loop: with shown_only most entries end at their mask byte, and one thread
+  // per entry would spend the pass launching workgroups.
+  const int64_t n = (int64_t)pos_batch * num_tri;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (!shown_only || mask[i] == kShown) silhouette_bits(pos, stride, tri, num_tri, nbr, i, mask);
+  }
 }
 
 // ---- crossings --------------------------------------------------------------------------
@@ -665,7 +676,7 @@ extern "C" int dr_silhouette_mask(const float* pos, int64_t pos_batch_stride, in
       aa_mark_shown<<<blocks_for(pixels, 256), 256, 0, s>>>(rast, image_pixels, pixels, num_tri,
                                                            pos_batch, mask);
   }
-  aa_silhouette_kernel<<<blocks_for(n, 256), 256, 0, s>>>(
+  aa_silhouette_kernel<<<(int)std::min<int64_t>(blocks_for(n, 256), 4096), 256, 0, s>>>(
       pos, pos_batch_stride, pos_batch, tri, num_tri, neighbours, rast != nullptr, mask);
   return launch_status();
 }
