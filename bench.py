@@ -421,6 +421,31 @@ def profiled_traffic(kernel: str, workload: str) -> dict | None:
         path.relative_to(ROOT))}
 
 
+# fp32 vector issue peak of the MI355X in lane operations per second: 256 CUs x 4 SIMDs x 32
+# lanes x 2.4 GHz (the published 157.3 TFLOP/s counts a fused multiply-add as two operations).
+VALU_PEAK = 256 * 4 * 32 * 2.4e9
+
+
+def profiled_valu(kernel: str, workload: str, mean_ms: float) -> dict | None:
+    """VALU utilisation of ``kernel``: its vector instructions per launch (SQ_INSTS_VALU, wave64
+    instructions, from its committed rocprofv3 counter summary) times 64 lanes, over its mean
+    duration, against VALU_PEAK."""
+    path = ROOT / "profiles" / f"{kernel}.{workload}.valu.txt"
+    if not path.exists():
+        return None
+    n = None
+    for line in path.read_text().splitlines():
+        key, sep, value = line.partition(":")
+        if sep and key.strip() == "valu_instructions":
+            n = float(value)
+    if n is None:
+        return None
+    ops = n * 64 / (mean_ms * 1e-3)
+    return {"instructions": int(n), "achieved": round(ops / 1e12, 2), "peak": VALU_PEAK / 1e12,
+            "unit": "T lane-ops/s", "frac": round(ops / VALU_PEAK, 4),
+            "source": str(path.relative_to(ROOT))}
+
+
 def copy_probe(mib: int, device) -> None:
     """One device-to-device copy of ``mib`` MiB from memory no cache holds, the calibration of
     the HBM byte counters: the source is written, then a 2 GiB fill evicts it from the L2s and
@@ -528,6 +553,8 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int)
             "traffic_source": None if traffic is None else traffic["source"],
             "algorithmic_bytes": int(dom_bytes),
             "mean_launch_ms": round(dom_ms, 4),
+            # The rasterizer's own bound: vector issue (no HBM stream limits it).
+            "valu": profiled_valu(SINGLE_KERNEL[dominant], name, dom_ms),
         },
         "cpu_baseline": baseline,
         "kernels": kernels,
