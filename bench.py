@@ -143,7 +143,7 @@ class BytesModel:
 
     def raster_visibility_tiles(self, args):
         counts = args[6]
-        return counts[1] * TILE_ENTRY_BYTES + counts[2] * TILE_KEY_BYTES
+        return counts[1] * TILE_ENTRY_BYTES + counts[3] * TILE_KEY_BYTES
 
     def resolve_forward(self, args):
         P = self._pixels(_struct(args[0]))

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent.parent / "libdiffrast_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 MAX_LEVELS = 32
 
 c_float_p = ctypes.POINTER(ctypes.c_float)

@@ -88,7 +88,7 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
     size = ctypes.c_size_t()
     call("dr_raster_workspace_size", ref(geo.struct), ctypes.byref(size))
     workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
-    counts = (ctypes.c_uint32 * 3)()
+    counts = (ctypes.c_uint32 * 4)()
     prev = None if previous is None else previous.contiguous()
     stream = _lib.stream(device)
     call("dr_raster_visibility_begin", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),

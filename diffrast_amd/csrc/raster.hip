@@ -36,7 +36,7 @@ namespace {
 
 constexpr int kTile = 16;            // tile edge in pixels; a tile is one 256-thread workgroup
 constexpr int kChunk = 256;          // triangles per tile work item
-constexpr int kWorkClasses = 128;    // classes of 32 entries in the tile pass's heavy-first order
+constexpr int kWorkClasses = 128;    // tile work classes: none, then 32 entries each (heavy-first order)
 constexpr int kWindow = 512;         // work items per map of the tile kernel (256 threads x 2)
 static_assert(kWindow == 2 * 256, "the map scan gives each thread two entries");
 constexpr int kSmallPixels = 16;     // bounding boxes up to this many pixels skip binning
@@ -63,12 +63,13 @@ struct Workspace {
                              // farthest vertex depth of an image (one when pos is shared)
   uint32_t* range_parts;     // [depth_ranges][kRangeParts][2] partial spans
   uint2* block_sums;         // [scan blocks] (entries, chunks)
-  uint32_t* counters;        // [1] entries, [2] list chunks (scan by-product), [3] busy tiles
+  uint32_t* counters;        // [1] entries, [2] tile pass workgroups, [3] busy tiles
   uint32_t* block_records;   // [record_blocks] binned triangles of each setup workgroup
   uint32_t* tile_order;      // [tiles] tile pass order: heavy tiles first within each XCD's share
   uint8_t* tile_class;       // [tiles] work class of each tile (entries / 32, capped)
   uint32_t* class_counts;    // [8][kWorkClasses] tiles per (XCD share, class)
   uint32_t* class_cursor;    // [8][kWorkClasses] fill positions of the placement pass
+  uint32_t* share_info;      // [16] busy tiles of each XCD share, then where they start in the order
   float* px;                 // [width] pixel-centre x per column
   float* py;                 // [height] pixel-centre y per row
   int4* order;               // [num_tri] processing order (instanced meshes only): the vertex
@@ -123,6 +124,7 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
   w.tile_class = (uint8_t*)take(w.tiles);
   w.class_counts = (uint32_t*)take(sizeof(uint32_t) * 8 * kWorkClasses);
   w.class_cursor = (uint32_t*)take(sizeof(uint32_t) * 8 * kWorkClasses);
+  w.share_info = (uint32_t*)take(sizeof(uint32_t) * 16);
   w.px = (float*)take(sizeof(float) * g.width);
   w.py = (float*)take(sizeof(float) * g.height);
   if (w.ordered) {
@@ -796,7 +798,6 @@ __global__ __launch_bounds__(256) void raster_scan_blocks(uint2* block_sums, int
   }
   if (threadIdx.x == 0) {
     counters[1] = carry.x;
-    counters[2] = carry.y;
   }
 }
 
@@ -874,9 +875,10 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
 
 // ---- tile order: heavy tiles first within each XCD's share -----------------------------------
 //
-// The tile pass takes tiles in this order: each XCD keeps its contiguous share of them
-// (xcd_order), and within the share the tiles with the most binned triangles go first, so that
-// the longest workgroups do not start last. A counting sort by entry count in kWorkClasses
+// The tile pass takes tiles in this order: the busy tiles in their XCD shares' order (so that
+// XCD k, which takes the k-th eighth of the workgroups under xcd_order, gets about share k),
+// within a share the tiles with the most binned triangles first, so that the longest
+// workgroups do not start last. A counting sort by entry count in kWorkClasses
 // classes of 32 entries, in three passes over the tiles (classes and their counts, the class
 // cursors, placement); workgroups aggregate in LDS before touching global counters. The order
 // within a class is free: tiles are independent.
@@ -909,7 +911,8 @@ __global__ __launch_bounds__(256) void raster_tile_classes(Workspace ws) {
   if (tile < ws.tiles) {
     const uint32_t n =
         ws.list_offsets[(tile + 1) * kDepthSlabs] - ws.list_offsets[tile * kDepthSlabs];
-    const int c = (int)min(n >> 5, (uint32_t)(kWorkClasses - 1));
+    // Class 0: no entries; then one class per 32 entries, the last one open-ended.
+    const int c = n == 0 ? 0 : (int)min((n >> 5) + 1, (uint32_t)(kWorkClasses - 1));
     ws.tile_class[tile] = (uint8_t)c;
     atomicAdd(hist + xcd_share(tile, ws.tiles) * kWorkClasses + c, 1u);
     has = n > 0;
@@ -922,19 +925,38 @@ __global__ __launch_bounds__(256) void raster_tile_classes(Workspace ws) {
   if (threadIdx.x == 0 && busy) atomicAdd(ws.counters + 3, busy);
 }
 
-// Pass 2, one workgroup: first position of each class in its share, heaviest class first.
+// Pass 2, one workgroup: first position of each class. The busy tiles come first, share by
+// share, heaviest class first within a share; the tiles without entries follow, so that the
+// tile pass launches one workgroup per busy tile.
 __global__ __launch_bounds__(256) void raster_tile_cursors(Workspace ws) {
   __shared__ uint32_t counts[kXcdShares * kWorkClasses];
+  __shared__ uint32_t busy[kXcdShares], idle[kXcdShares];
   for (int i = threadIdx.x; i < kXcdShares * kWorkClasses; i += blockDim.x)
     counts[i] = ws.class_counts[i];
   __syncthreads();
-  if (threadIdx.x < kXcdShares) {
-    const int k = threadIdx.x;
-    uint32_t run = (uint32_t)share_start(k, ws.tiles);
-    for (int c = kWorkClasses - 1; c >= 0; --c) {
+  const int k = threadIdx.x;
+  uint32_t run = 0u;
+  if (k < kXcdShares) {  // the share's classes, relative to its first busy tile
+    for (int c = kWorkClasses - 1; c >= 1; --c) {
       ws.class_cursor[k * kWorkClasses + c] = run;
       run += counts[k * kWorkClasses + c];
     }
+    busy[k] = run;
+    idle[k] = counts[k * kWorkClasses];
+  }
+  __syncthreads();
+  if (k < kXcdShares) {
+    uint32_t first = 0u, idle_first = 0u, widest = 0u;
+    for (int j = 0; j < kXcdShares; ++j) {
+      first += j < k ? busy[j] : 0u;
+      idle_first += busy[j] + (j < k ? idle[j] : 0u);
+      widest = max(widest, busy[j]);
+    }
+    for (int c = kWorkClasses - 1; c >= 1; --c) ws.class_cursor[k * kWorkClasses + c] += first;
+    ws.class_cursor[k * kWorkClasses] = idle_first;
+    ws.share_info[k] = busy[k];
+    ws.share_info[kXcdShares + k] = first;
+    if (k == 0) ws.counters[2] = kXcdShares * widest;  // the tile pass's workgroups
   }
 }
 
@@ -989,9 +1011,13 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   __shared__ uint64_t s_far[256 / DR_WAVE];
   __shared__ float s_bound[kChunk];  // lower bound of each staged triangle's depth
 
-  // XCD k takes the k-th eighth of the tiles (for a batch of 8 images, one image each), so the
-  // records that neighbouring tiles share stay in one L2; heavy tiles first within it.
-  const uint32_t tile = ws.tile_order[xcd_order(blockIdx.x, gridDim.x)];
+  // Workgroups are dispatched round-robin over the 8 XCDs: XCD k runs the busy tiles of share
+  // k (for a batch of 8 images, one image), so the records that neighbouring tiles share stay in
+  // one L2, heaviest first; the grid is 8 x the largest share, the surplus returns at once.
+  const int share = (int)(blockIdx.x % kXcdShares);
+  const uint32_t slot = blockIdx.x / kXcdShares;
+  if (slot >= ws.share_info[share]) return;  // uniform over the workgroup
+  const uint32_t tile = ws.tile_order[ws.share_info[kXcdShares + share] + slot];
   const uint32_t begin = ws.list_offsets[(size_t)tile * kDepthSlabs];
   const uint32_t end = ws.list_offsets[(size_t)(tile + 1) * kDepthSlabs];
   if (begin == end) return;  // uniform over the workgroup
@@ -1409,10 +1435,10 @@ extern "C" int dr_raster_workspace_size(const DrRasterGeometry* g, size_t* bytes
 
 extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                           uint64_t* keys, void* workspace,
-                                          size_t workspace_bytes, uint32_t counts[3],
+                                          size_t workspace_bytes, uint32_t counts[4],
                                           void* stream) {
   if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
-  counts[0] = counts[1] = counts[2] = 0;
+  counts[0] = counts[1] = counts[2] = counts[3] = 0;
   hipStream_t s = (hipStream_t)stream;
   const int64_t pixels = (int64_t)g->batch * g->height * g->width;
   if (pixels == 0) return DR_OK;
@@ -1463,13 +1489,14 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
     return DR_ERR_HIP;
   counts[0] = (uint32_t)ws.record_blocks;
   counts[1] = host[1];
-  counts[2] = host[3];
+  counts[2] = host[2];
+  counts[3] = host[3];
   return DR_OK;
 }
 
 extern "C" int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspace,
                                         size_t workspace_bytes, uint32_t* entries,
-                                        const uint32_t counts[3], void* stream) {
+                                        const uint32_t counts[4], void* stream) {
   if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
   if (counts[1] == 0) return DR_OK;
   if (!entries || counts[2] == 0) return DR_ERR_ARGUMENT;
@@ -1483,14 +1510,14 @@ extern "C" int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspa
 extern "C" int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                           uint64_t* keys, void* workspace,
                                           size_t workspace_bytes, const uint32_t* entries,
-                                          const uint32_t counts[3], void* stream) {
+                                          const uint32_t counts[4], void* stream) {
   if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
   if (counts[1] == 0) return DR_OK;
   if (!entries || !keys || counts[2] == 0) return DR_ERR_ARGUMENT;
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
-  raster_tile_kernel<<<(unsigned)ws.tiles, 256, 0, s>>>(*g, prev_keys, keys, ws, entries);
+  raster_tile_kernel<<<counts[2], 256, 0, s>>>(*g, prev_keys, keys, ws, entries);
   return launch_status();
 }
 

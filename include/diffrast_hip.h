@@ -74,25 +74,25 @@ int dr_raster_workspace_size(const DrRasterGeometry* g, size_t* bytes);
 /* Visibility, first part: clears keys, orders the triangles of a large mesh spatially,
  * rasterizes triangles with a small bounding box directly, bins the others into 16x16 tiles
  * (counts and scan) and orders the tiles for the tile pass. Waits for the stream and returns
- * in counts[0..2] the number of
- * setup workgroups (each with up to 256 binned triangles), tile entries, and tiles with at
- * least one entry (the tile pass's workgroups that have work).
+ * in counts[0..3] the number of setup workgroups (each with up to 256 binned triangles), tile
+ * entries, workgroups of the tile pass (8 x the busy tiles of the XCD share with the most), and
+ * tiles with at least one entry.
  * prev_keys (nullable) is the previous depth layer. */
 int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                uint64_t* keys, void* workspace, size_t workspace_bytes,
-                               uint32_t counts[3], void* stream);
+                               uint32_t counts[4], void* stream);
 
 /* Visibility, second part: fills the per-tile lists. entries holds counts[1] uint32: the
  * lists of all tiles, tile by tile, near to far. Nothing to do when counts[1] == 0. (The reference has no binning: its visibility tests every triangle at every
  * pixel, reference.py:368-397; _triton_raster.py:241-306 keeps the nearest per pixel.) */
 int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspace, size_t workspace_bytes,
-                             uint32_t* entries, const uint32_t counts[3], void* stream);
+                             uint32_t* entries, const uint32_t counts[4], void* stream);
 
 /* Visibility, third part: rasterizes the binned triangles tile by tile into keys, after
  * dr_raster_visibility_bin with the same entries. Nothing to do when counts[1] == 0. */
 int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                uint64_t* keys, void* workspace, size_t workspace_bytes,
-                               const uint32_t* entries, const uint32_t counts[3], void* stream);
+                               const uint32_t* entries, const uint32_t counts[4], void* stream);
 
 /* rast [batch, h, w, 4] = (u, v, z/w, id + 1) and rast_db [batch, h, w, 4] = (du/dx, du/dy,
  * dv/dx, dv/dy) from keys; zeros where a key is empty. rast_db may be NULL.

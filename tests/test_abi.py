@@ -47,7 +47,7 @@ def test_argument_checks_before_launch():
     wide = _lib.RasterGeometry(num_tri=1, batch=1, height=8, width=(1 << 20) + 32, pos=1, tri=1,
                                num_instances=1)
     assert lib.dr_raster_workspace_size(ctypes.byref(wide), ctypes.byref(size)) == 1001
-    counts = (ctypes.c_uint32 * 3)(0, 0, 0)
+    counts = (ctypes.c_uint32 * 4)(0, 0, 0, 0)
     assert lib.dr_raster_visibility_bin(ctypes.byref(g), None, 0, None, counts, None) == 0
     assert lib.dr_raster_visibility_tiles(ctypes.byref(g), None, None, None, 0, None, counts,
                                           None) == 0
