@@ -149,11 +149,17 @@ __device__ __forceinline__ void instance(const DrRasterGeometry& g, int64_t i, i
     t = (int)(i - (int64_t)b * g.num_tri);
     return;
   }
-  int lo = 0, hi = g.batch;  // largest b with range_prefix[b] <= i
+  // The item of the wave's first instance by a binary search on wave-uniform values (scalar
+  // loads), then each lane steps forward over the few items its wave spans.
+  const uint32_t first_lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)i);
+  const uint32_t first_hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(i >> 32));
+  const int64_t first = (int64_t)((uint64_t)first_hi << 32 | first_lo);  // the first active lane's
+  int lo = 0, hi = g.batch;  // largest b with range_prefix[b] <= first
   while (hi - lo > 1) {
     int mid = (lo + hi) >> 1;
-    if (g.range_prefix[mid] <= i) lo = mid; else hi = mid;
+    if (g.range_prefix[mid] <= first) lo = mid; else hi = mid;
   }
+  while (lo + 1 < g.batch && g.range_prefix[lo + 1] <= i) ++lo;
   b = lo;
   t = g.ranges[2 * b] + (int)(i - g.range_prefix[b]);
 }
