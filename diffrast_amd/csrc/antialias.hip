@@ -321,71 +321,112 @@ __device__ __forceinline__ int pixel_tri(const DrAntialiasArgs& a, int64_t pixel
   return (id >= 1.0f && id <= (float)a.num_tri) ? (int)id - 1 : -1;
 }
 
-__device__ __forceinline__ void load_triangle(const DrAntialiasArgs& a, int b, int t,
+// The vertex rows of triangle t.
+__device__ __forceinline__ void load_rows(const DrAntialiasArgs& a, int t, int (&v)[3]) {
+#pragma unroll
+  for (int k = 0; k < 3; ++k) v[k] = a.tri[3 * (int64_t)t + k];
+}
+
+// x, y and w of the vertices in rows v of image b's positions.
+__device__ __forceinline__ void load_vertices(const DrAntialiasArgs& a, int b, const int (&v)[3],
                                               Triangle& T) {
   const float* P = a.pos + (int64_t)b * a.pos_batch_stride;
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
-    T.v[k] = a.tri[3 * (int64_t)t + k];
-    const float4 p = load4(P + 4 * (int64_t)T.v[k]);
+    T.v[k] = v[k];
+    const float4 p = load4(P + 4 * (int64_t)v[k]);
     T.x[k] = p.x;
     T.y[k] = p.y;
     T.w[k] = p.w;
   }
 }
 
+__device__ __forceinline__ void load_triangle(const DrAntialiasArgs& a, int b, int t,
+                                              Triangle& T) {
+  int v[3];
+  load_rows(a, t, v);
+  load_vertices(a, b, v, T);
+}
+
 // Pair record bits: the pair is active, the first pixel's triangle owns the edge, edge index.
 constexpr uint8_t kActive = 0x8, kOwnerFirst = 0x4;
 
-// The pair (p, q), q = p + (d_row, d_col), as in reference.py:238-258: crossing t from p and
-// the record bits. ids and depths are already loaded.
-__device__ __forceinline__ uint8_t eval_pair(const DrAntialiasArgs& a, int b, int row, int col,
-                                             int d_row, int d_col, int id_p, int id_q,
-                                             float depth_p, float depth_q, float& t) {
-  t = 0.0f;
-  if (id_p == id_q) return 0;
-  const uint8_t* sil = a.silhouette + (int64_t)b * a.silhouette_batch_stride;
-  const uint8_t sil_p = id_p >= 0 ? sil[id_p] : 0, sil_q = id_q >= 0 ? sil[id_q] : 0;
-  if (sil_p == 0 && sil_q == 0) return 0;
-  const bool horizontal = d_col == 1;
-  const float px = pixel_centre(col, a.width), py = pixel_centre(row, a.height);
-  const float qx = pixel_centre(col + d_col, a.width), qy = pixel_centre(row + d_row, a.height);
-  Crossing from_p{false, 0.f, 0}, from_q{false, 0.f, 0};
-  if (sil_p != 0) {
-    Triangle T;
-    load_triangle(a, b, id_p, T);
-    from_p = crossing(T, sil_p, horizontal, a.width, a.height, px, py, qx, qy);
-  }
-  if (sil_q != 0) {
-    Triangle T;
-    load_triangle(a, b, id_q, T);
-    from_q = crossing(T, sil_q, horizontal, a.width, a.height, qx, qy, px, py);
-  }
+// Record bits and t of the pair (p, q) from the crossings found from each side
+// (reference.py:238-258): the nearer triangle owns the edge, p's on a depth tie.
+__device__ __forceinline__ uint8_t pair_record(const Crossing& from_p, const Crossing& from_q,
+                                               float depth_p, float depth_q, float& t) {
   const bool use_p = from_p.found && (!from_q.found || depth_p <= depth_q);
   const bool use_q = from_q.found && !use_p;
+  t = 0.0f;
   if (!use_p && !use_q) return 0;
   t = use_p ? from_p.t : 1.0f - from_q.t;
   return (uint8_t)(kActive | (use_p ? kOwnerFirst : 0) | (use_p ? from_p.edge : from_q.edge));
 }
 
-// Every pixel evaluates the pairs it forms with its right and lower neighbours, once.
+// Triangle index of a rast pixel from its (z, w) pair, and its depth; -1 for background.
+__device__ __forceinline__ int zw_tri(const DrAntialiasArgs& a, float2 zw, float& depth) {
+  depth = zw.x;
+  const float id = rintf(zw.y);
+  // Ids past the end of tri are background (reference.py:228-230).
+  return (id >= 1.0f && id <= (float)a.num_tri) ? (int)id - 1 : -1;
+}
+
+// Every pixel evaluates the pairs it forms with its right and lower neighbours, once. The
+// loads go level by level over the (at most three) triangles involved -- ids, silhouette bits,
+// index rows, vertices -- so that each level's loads are in flight together: a wave where any
+// pixel needs a triangle reads all three for every lane, lanes that need fewer reading
+// triangle 0 in their place (one cached line). A pair of pixels showing one triangle, or two
+// triangles without silhouette edges, is inactive.
 __global__ __launch_bounds__(256) void aa_pairs_kernel(DrAntialiasArgs a, float2* pair_t,
                                                        uchar2* pair_bits) {
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   if (!tp.inside) return;
-  float depth;
-  const int id = pixel_tri(a, tp.pixel, depth);
+  const bool has_right = tp.x + 1 < a.width, has_down = tp.y + 1 < a.height;
+  const float* zw = a.rast + 4 * tp.pixel + 2;
+  const float2 zw_p = *reinterpret_cast<const float2*>(zw);
+  const float2 zw_r = *reinterpret_cast<const float2*>(zw + (has_right ? 4 : 0));
+  const float2 zw_d = *reinterpret_cast<const float2*>(zw + (has_down ? 4 * (int64_t)a.width : 0));
+  float depth, depth_r, depth_d;
+  const int id = zw_tri(a, zw_p, depth);
+  const int id_r = zw_tri(a, zw_r, depth_r);
+  const int id_d = zw_tri(a, zw_d, depth_d);
+  const bool live_r = id != id_r, live_d = id != id_d;
+  const uint8_t* sil = a.silhouette + (int64_t)tp.b * a.silhouette_batch_stride;
+  const uint8_t sil_p = (live_r || live_d) && id >= 0 ? sil[id] : 0;
+  const uint8_t sil_r = live_r && id_r >= 0 ? sil[id_r] : 0;
+  const uint8_t sil_d = live_d && id_d >= 0 ? sil[id_d] : 0;
+  // A triangle is read where it has silhouette edges and its pixel is in a live pair.
+  const bool need_p = sil_p != 0, need_r = sil_r != 0, need_d = sil_d != 0;
   float t_right = 0.f, t_down = 0.f;
   uint8_t right = 0, down = 0;
-  if (tp.x + 1 < a.width) {
-    float d2;
-    const int id2 = pixel_tri(a, tp.pixel + 1, d2);
-    right = eval_pair(a, tp.b, tp.y, tp.x, 0, 1, id, id2, depth, d2, t_right);
-  }
-  if (tp.y + 1 < a.height) {
-    float d2;
-    const int id2 = pixel_tri(a, tp.pixel + a.width, d2);
-    down = eval_pair(a, tp.b, tp.y, tp.x, 1, 0, id, id2, depth, d2, t_down);
+  if (__any(need_p || need_r || need_d)) {  // then num_tri >= 1: triangle 0 exists
+    int rows_p[3], rows_r[3], rows_d[3];
+    load_rows(a, need_p ? id : 0, rows_p);
+    load_rows(a, need_r ? id_r : 0, rows_r);
+    load_rows(a, need_d ? id_d : 0, rows_d);
+    Triangle Tp, Tr, Td;
+    load_vertices(a, tp.b, rows_p, Tp);
+    load_vertices(a, tp.b, rows_r, Tr);
+    load_vertices(a, tp.b, rows_d, Td);
+    const float px = pixel_centre(tp.x, a.width), py = pixel_centre(tp.y, a.height);
+    if (live_r && (need_p || need_r)) {
+      const float qx = pixel_centre(tp.x + 1, a.width);
+      const Crossing none{false, 0.f, 0};
+      const Crossing from_p =
+          need_p ? crossing(Tp, sil_p, true, a.width, a.height, px, py, qx, py) : none;
+      const Crossing from_q =
+          need_r ? crossing(Tr, sil_r, true, a.width, a.height, qx, py, px, py) : none;
+      right = pair_record(from_p, from_q, depth, depth_r, t_right);
+    }
+    if (live_d && (need_p || need_d)) {
+      const float qy = pixel_centre(tp.y + 1, a.height);
+      const Crossing none{false, 0.f, 0};
+      const Crossing from_p =
+          need_p ? crossing(Tp, sil_p, false, a.width, a.height, px, py, px, qy) : none;
+      const Crossing from_q =
+          need_d ? crossing(Td, sil_d, false, a.width, a.height, px, qy, px, py) : none;
+      down = pair_record(from_p, from_q, depth, depth_d, t_down);
+    }
   }
   pair_t[tp.pixel] = make_float2(t_right, t_down);
   pair_bits[tp.pixel] = make_uchar2(right, down);
