@@ -702,13 +702,22 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     const float lane_max = w_max > 0.0f ? g_max * w_max : 0.0f;
     const FixedPass f = table.begin(lane_max);
     // One tap at a time (the tap index is uniform): unrolled, the taps' table updates would
-    // interleave and hold many more registers.
+    // interleave and hold many more registers. In 2D, neighbouring pixels of a tile row whose
+    // tap falls on the same texel sum first, and the last of them adds the sum (cube faces
+    // give fewer such runs than the summing costs).
 #pragma unroll 1
     for (int k = 0; k < 8; ++k) {
+      const uint32_t key = tap_key[k];
       float v[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) v[c] = gc[c] * tap_weight[k];
-      table.add_wave(tap_key[k], v, n, grad_texels + c0, C, f);
+      if constexpr (CUBE) {
+        table.add_wave(key, v, n, grad_texels + c0, C, f);
+      } else {
+        if (__ballot(key != Table::kEmpty) == 0) continue;  // uniform
+        const bool last = row_run_sums(key, v);
+        if (last && key != Table::kEmpty) table.add_or_global(key, v, n, grad_texels + c0, C, f);
+      }
     }
     __syncthreads();
     table.flush(grad_texels + c0, C, n, f);
