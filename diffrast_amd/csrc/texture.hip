@@ -821,6 +821,178 @@ __global__ __launch_bounds__(256) void mip_up(float* grad, int C, int64_t num_te
   src[((int64_t)i * w + j) * C + c] += sum;
 }
 
+// ---- mip chain in tile stages ------------------------------------------------------------
+//
+// Where a level's sizes are divisible by 2^G (G >= 2), the next G levels halve exactly and each
+// texel has exactly one parent: a workgroup then takes a tile of 2^G x 2^G texels of the bottom
+// level through all G levels, keeping the levels in between in LDS, instead of one launch (and
+// one pass over memory) per level. The arithmetic is mip_down's and mip_up's for even sizes:
+// a texel is ((a / 4 + b / 4) + c / 4) + d / 4 of its children in row-major order, and in the
+// adjoint a child adds a quarter of its parent's total.
+
+constexpr int kMipStageLevels = 6;  // at most 64 x 64 bottom texels per tile: 32 x 32 above
+
+// Up to four channels of texel p (n valid; vec: four channels on a 16-byte aligned buffer).
+__device__ __forceinline__ float4 load_texel(const float* p, int n, bool vec) {
+  if (vec) return *reinterpret_cast<const float4*>(p);
+  return make_float4(p[0], n > 1 ? p[1] : 0.f, n > 2 ? p[2] : 0.f, n > 3 ? p[3] : 0.f);
+}
+
+__device__ __forceinline__ void store_texel(float* p, float4 v, int n, bool vec) {
+  if (vec) {
+    *reinterpret_cast<float4*>(p) = v;
+    return;
+  }
+  p[0] = v.x;
+  if (n > 1) p[1] = v.y;
+  if (n > 2) p[2] = v.z;
+  if (n > 3) p[3] = v.w;
+}
+
+__device__ __forceinline__ float4 quad_mean(float4 a, float4 b, float4 c, float4 d) {
+  auto mean = [](float a, float b, float c, float d) {
+    return ((0.25f * a + 0.25f * b) + 0.25f * c) + 0.25f * d;
+  };
+  return make_float4(mean(a.x, b.x, c.x, d.x), mean(a.y, b.y, c.y, d.y),
+                     mean(a.z, b.z, c.z, d.z), mean(a.w, b.w, c.w, d.w));
+}
+
+__device__ __forceinline__ float4 add_quarter(float4 own, float4 parent) {
+  return make_float4(own.x + 0.25f * parent.x, own.y + 0.25f * parent.y,
+                     own.z + 0.25f * parent.z, own.w + 0.25f * parent.w);
+}
+
+// The tile of this workgroup: (image, face) and tile coordinates in units of 2^G bottom texels.
+struct MipTile {
+  int64_t image;
+  int face, tx, ty;
+};
+
+__device__ __forceinline__ MipTile mip_tile(const MipLevels& L, int k, int G, int faces) {
+  const int tiles_x = L.w[k] >> G, tiles_y = L.h[k] >> G;
+  int64_t b = blockIdx.x;
+  MipTile T;
+  T.tx = (int)(b % tiles_x);
+  b /= tiles_x;
+  T.ty = (int)(b % tiles_y);
+  b /= tiles_y;
+  T.face = (int)(b % faces);
+  T.image = b / faces;
+  return T;
+}
+
+__device__ __forceinline__ float* mip_level(float* texels, int64_t num_texels, int C,
+                                            const MipLevels& L, const MipTile& T, int lvl) {
+  return texels + T.image * num_texels * C + (L.off[lvl] + (int64_t)T.face * L.h[lvl] * L.w[lvl]) * C;
+}
+
+// Levels k + 1 .. k + G from level k, one tile per workgroup.
+__global__ __launch_bounds__(256) void mip_down_stage(float* texels, int C, int64_t num_texels,
+                                                      int faces, MipLevels L, int k, int G) {
+  __shared__ float4 s_buf[2][1 << (2 * kMipStageLevels - 2)];
+  const MipTile T = mip_tile(L, k, G, faces);
+  const bool vec = C == 4 && (reinterpret_cast<uintptr_t>(texels) & 15u) == 0;
+  for (int c0 = 0; c0 < C; c0 += 4) {
+    const int n = min(4, C - c0);
+    int side = 1 << (G - 1);  // the tile's side at level k + 1
+    {
+      const float* src = mip_level(texels, num_texels, C, L, T, k) + c0;
+      float* dst = mip_level(texels, num_texels, C, L, T, k + 1) + c0;
+      const int64_t w = L.w[k], w1 = L.w[k + 1];
+      for (int i = threadIdx.x; i < side * side; i += blockDim.x) {
+        const int r = T.ty * side + i / side, c = T.tx * side + i % side;
+        const float* p = src + ((int64_t)(2 * r) * w + 2 * c) * C;
+        const float4 a = load_texel(p, n, vec), b = load_texel(p + C, n, vec);
+        const float4 cc = load_texel(p + w * C, n, vec), d = load_texel(p + w * C + C, n, vec);
+        const float4 o = quad_mean(a, b, cc, d);
+        store_texel(dst + ((int64_t)r * w1 + c) * C, o, n, vec);
+        s_buf[0][i] = o;
+      }
+    }
+    int cur = 0;
+    for (int lvl = k + 2; lvl <= k + G; ++lvl) {
+      __syncthreads();
+      const int below = side;
+      side >>= 1;
+      float* dst = mip_level(texels, num_texels, C, L, T, lvl) + c0;
+      const int64_t wl = L.w[lvl];
+      const float4* s = s_buf[cur];
+      for (int i = threadIdx.x; i < side * side; i += blockDim.x) {
+        const int r = i / side, c = i % side;
+        const float4* q = s + 2 * r * below + 2 * c;
+        const float4 o = quad_mean(q[0], q[1], q[below], q[below + 1]);
+        store_texel(dst + ((int64_t)(T.ty * side + r) * wl + T.tx * side + c) * C, o, n, vec);
+        s_buf[cur ^ 1][i] = o;
+      }
+      cur ^= 1;
+    }
+    __syncthreads();  // the next channel group reuses the LDS
+  }
+}
+
+// Adjoint of mip_down_stage: the totals of level k + G (final: the stages above ran first) fold
+// down through levels k + G - 1 .. k of the tile, each texel adding a quarter of its parent's
+// total to its own gradient, which becomes its total.
+__global__ __launch_bounds__(256) void mip_up_stage(float* grad, int C, int64_t num_texels,
+                                                    int faces, MipLevels L, int k, int G) {
+  __shared__ float4 s_buf[2][1 << (2 * kMipStageLevels - 2)];
+  const MipTile T = mip_tile(L, k, G, faces);
+  const bool vec = C == 4 && (reinterpret_cast<uintptr_t>(grad) & 15u) == 0;
+  for (int c0 = 0; c0 < C; c0 += 4) {
+    const int n = min(4, C - c0);
+    int cur = 0;
+    if (threadIdx.x == 0) {
+      const float* top = mip_level(grad, num_texels, C, L, T, k + G) + c0;
+      s_buf[0][0] = load_texel(top + ((int64_t)T.ty * L.w[k + G] + T.tx) * C, n, vec);
+    }
+    int side = 1;  // the tile's side at the level in s_buf[cur]
+    for (int lvl = k + G - 1; lvl >= k; --lvl) {
+      __syncthreads();
+      const int above = side;
+      side <<= 1;
+      float* g = mip_level(grad, num_texels, C, L, T, lvl) + c0;
+      const int64_t wl = L.w[lvl];
+      const float4* s = s_buf[cur];
+      for (int i = threadIdx.x; i < side * side; i += blockDim.x) {
+        const int r = i / side, c = i % side;
+        float* p = g + ((int64_t)(T.ty * side + r) * wl + T.tx * side + c) * C;
+        const float4 o = add_quarter(load_texel(p, n, vec), s[(r >> 1) * above + (c >> 1)]);
+        store_texel(p, o, n, vec);
+        if (lvl > k) s_buf[cur ^ 1][i] = o;
+      }
+      cur ^= 1;
+    }
+    __syncthreads();  // the next channel group reuses the LDS
+  }
+}
+
+// Tile stages and single levels of a chain: stage (k, G) builds levels k + 1 .. k + G, in one
+// tile-stage launch when G >= 2, else (G == 1) with mip_down.
+struct MipPlan {
+  int count;
+  int k[DR_MAX_LEVELS], G[DR_MAX_LEVELS];
+};
+
+MipPlan mip_plan(const MipLevels& L, int num_levels) {
+  MipPlan P{};
+  for (int k = 0; k + 1 < num_levels;) {
+    int G = 0;
+    while (G < kMipStageLevels && k + G + 1 < num_levels && L.h[k] % (2 << G) == 0 &&
+           L.w[k] % (2 << G) == 0)
+      ++G;
+    if (G < 2) G = 1;
+    P.k[P.count] = k;
+    P.G[P.count] = G;
+    ++P.count;
+    k += G;
+  }
+  return P;
+}
+
+int64_t stage_tiles(const MipLevels& L, int k, int G, int64_t images) {
+  return images * (int64_t)(L.h[k] >> G) * (L.w[k] >> G);
+}
+
 bool valid_levels(int num_levels, const int32_t* h, const int32_t* w, const int64_t* off) {
   if (num_levels < 1 || num_levels > DR_MAX_LEVELS || !h || !w || !off) return false;
   for (int k = 0; k < num_levels; ++k)
@@ -916,8 +1088,16 @@ extern "C" int dr_mip_build(float* texels, int32_t tex_batch, int32_t channels,
       !valid_levels(num_levels, level_height, level_width, level_offset))
     return DR_ERR_ARGUMENT;
   const MipLevels L = copy_levels(num_levels, level_height, level_width, level_offset);
-  for (int k = 0; k + 1 < num_levels; ++k) {
-    const int64_t count = (int64_t)tex_batch * faces * L.h[k + 1] * L.w[k + 1] * channels;
+  const MipPlan P = mip_plan(L, num_levels);
+  const int64_t images = (int64_t)tex_batch * faces;
+  for (int s = 0; s < P.count; ++s) {
+    const int k = P.k[s], G = P.G[s];
+    if (G >= 2) {
+      mip_down_stage<<<(unsigned)stage_tiles(L, k, G, images), 256, 0, (hipStream_t)stream>>>(
+          texels, channels, num_texels, faces, L, k, G);
+      continue;
+    }
+    const int64_t count = images * L.h[k + 1] * L.w[k + 1] * channels;
     mip_down<<<blocks_for(count, 256), 256, 0, (hipStream_t)stream>>>(
         texels, channels, num_texels, faces, L, k, count);
   }
@@ -932,8 +1112,16 @@ extern "C" int dr_mip_build_backward(float* grad_texels, int32_t tex_batch, int3
       !valid_levels(num_levels, level_height, level_width, level_offset))
     return DR_ERR_ARGUMENT;
   const MipLevels L = copy_levels(num_levels, level_height, level_width, level_offset);
-  for (int k = num_levels - 2; k >= 0; --k) {
-    const int64_t count = (int64_t)tex_batch * faces * L.h[k] * L.w[k] * channels;
+  const MipPlan P = mip_plan(L, num_levels);
+  const int64_t images = (int64_t)tex_batch * faces;
+  for (int s = P.count - 1; s >= 0; --s) {
+    const int k = P.k[s], G = P.G[s];
+    if (G >= 2) {
+      mip_up_stage<<<(unsigned)stage_tiles(L, k, G, images), 256, 0, (hipStream_t)stream>>>(
+          grad_texels, channels, num_texels, faces, L, k, G);
+      continue;
+    }
+    const int64_t count = images * L.h[k] * L.w[k] * channels;
     mip_up<<<blocks_for(count, 256), 256, 0, (hipStream_t)stream>>>(
         grad_texels, channels, num_texels, faces, L, k, count);
   }

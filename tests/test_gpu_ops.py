@@ -237,6 +237,29 @@ def test_mip_chain_matches_oracle(size):
     torch.testing.assert_close(grads[0], grads[1], atol=1e-5, rtol=1e-5)
 
 
+@pytest.mark.parametrize("shape", [(2, 64, 128, 4), (1, 96, 160, 8), (1, 6, 32, 32, 3),
+                                   (1, 256, 256, 4)])
+def test_mip_chain_tile_stages(shape):
+    """Sizes divisible by 2^G go through tile stages of up to six levels, the rest level by
+    level: 64x128 ends in 1x2 -> 1x1, 96x160 leaves 3x5 after five halvings, a cube map
+    stages each face, 256x256 runs a full six-level stage then two more."""
+    tex = torch.randn(*shape, generator=torch.Generator().manual_seed(5))
+    ref = R.texture_construct_mip(tex, None)
+    ours = hip.texture_construct_mip(tex.cuda(), None)
+    assert len(ours) == len(ref)
+    for a, b in zip(ours, ref):
+        assert a.shape == b.shape
+        assert rel_error(a.cpu(), b) < VALUE_TOL
+    weights = [torch.randn(l.shape, generator=torch.Generator().manual_seed(i))
+               for i, l in enumerate(ref)]
+    grads = []
+    for fn, device in ((hip.texture_construct_mip, "cuda"), (R.texture_construct_mip, "cpu")):
+        t = tex.clone().to(device).requires_grad_(True)
+        sum((l * w.to(device)).sum() for l, w in zip(fn(t, None), weights)).backward()
+        grads.append(t.grad.cpu())
+    torch.testing.assert_close(grads[0], grads[1], atol=1e-5, rtol=1e-5)
+
+
 def test_texture_through_public_api_with_mip_stack():
     tex, uv, uv_da = tex_scene(tex_batch=1, channels=3, seed=7)
     stack = dr.texture_construct_mip(tex.cuda())
