@@ -1066,7 +1066,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
         T.z[k] = v.z;
         T.w[k] = v.w;
       }
-      tri_row = __float_as_uint(rec[3].y) & 0xffffffu;
+      tri_row = __float_as_uint(rec[3].y);  // masked where it is stored, not waited for here
     }
     if (at + kChunk + threadIdx.x < end) next = entries[at + kChunk + threadIdx.x];
 
@@ -1108,7 +1108,8 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
       }
       s_bound[threadIdx.x] = bound;
       s_reach[threadIdx.x] = make_float2(T.reach_x, T.reach_y);
-      s_row[threadIdx.x] = tri_row;
+      asm volatile("" : "+v"(tri_row));  // keeps the mask (and the wait for the load) here
+      s_row[threadIdx.x] = tri_row & 0xffffffu;
       const bool behind = cull && bound > far_depth;
       if (bx0 <= bx1 && by0 <= by1 && !behind) {
         RowSpans se = {};
