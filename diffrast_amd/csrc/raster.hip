@@ -577,15 +577,16 @@ __global__ __launch_bounds__(kRangeParts) void raster_depth_range_merge(Workspac
   }
 }
 
-// Depth slab of a binned triangle: its nearest vertex depth's place in the image's depth span.
-// Triangles that cross the camera plane go first (slab 0).
-__device__ __forceinline__ int depth_slab(const Workspace& ws, int range, const Tri& T) {
+// Depth slab of a binned triangle: its nearest vertex depth's place in the image's depth span
+// (order-preserving bits of its nearest and farthest depth, from ws.depth_range). Triangles that
+// cross the camera plane go first (slab 0).
+__device__ __forceinline__ int depth_slab(uint2 span, const Tri& T) {
   if (!(T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f)) return 0;
   float d[3];
   vertex_depths(T, d);
   const float nearest = fminf(fminf(d[0], d[1]), d[2]);
-  const float lo = from_ordered_bits(ws.depth_range[2 * range]);
-  const float hi = from_ordered_bits(ws.depth_range[2 * range + 1]);
+  const float lo = from_ordered_bits(span.x);
+  const float hi = from_ordered_bits(span.y);
   const float f = (nearest - lo) / (hi - lo) * (float)kDepthSlabs;
   if (!(hi > lo) || !isfinite(f)) return 0;
   return min(max((int)f, 0), kDepthSlabs - 1);
@@ -629,6 +630,7 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
   const int64_t i = block * blockDim.x + threadIdx.x;
   bool binned = false;
   int area = 0;
+  uint2 span = make_uint2(0u, 0u);  // the image's depth span, for a binned triangle's slab
   int b = 0, t = 0, x_lo = 0, x_hi = -1, y_lo = 0, y_hi = -1;
   Tri T;
   if (i < g.num_instances) {
@@ -645,6 +647,8 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
       instance(g, i, b, t);
       load_tri(g, b, t, T, v);
     }
+    // Loaded now and used after the small triangles' work, which hides the load's latency.
+    span = reinterpret_cast<const uint2*>(ws.depth_range)[ws.depth_ranges > 1 ? b : 0];
     candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
     if (x_lo <= x_hi && y_lo <= y_hi) {
       const int64_t count = (int64_t)(x_hi - x_lo + 1) * (y_hi - y_lo + 1);
@@ -717,7 +721,7 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
       const uint32_t rec = (uint32_t)(block * 256 + before) +
                            (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
       const int tx0 = x_lo / kTile, tx1 = x_hi / kTile, ty0 = y_lo / kTile, ty1 = y_hi / kTile;
-      const int slab = depth_slab(ws, ws.depth_ranges > 1 ? b : 0, T);
+      const int slab = depth_slab(span, T);
       float4* out = ws.records + (size_t)rec * kRecord;
 #pragma unroll
       for (int k = 0; k < 3; ++k) out[k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
