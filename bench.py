@@ -73,11 +73,16 @@ class KernelTimer:
         self.bytes = defaultdict(float)
         self.bytes_of = bytes_of
         self.active = False
+        self.only = None  # entry point names to time (None: every one)
         self._call = hip.call
+
+    def reset(self):
+        self.events = defaultdict(list)
+        self.bytes = defaultdict(float)
 
     def install(self):
         def timed(name, *args):
-            if not self.active:
+            if not self.active or (self.only is not None and name not in self.only):
                 return self._call(name, *args)
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
@@ -477,15 +482,33 @@ WORKLOADS = {
 }
 
 
+def dominant_entry(per_kernel: dict, timed_bytes: dict) -> str:
+    """The longest-running entry point that launches a single kernel (so that its event time is
+    that kernel's time) and has a byte model."""
+    return max((n for n in per_kernel if n in SINGLE_KERNEL and n in timed_bytes),
+               key=lambda n: per_kernel[n][0])
+
+
 def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int) -> dict:
+    """Warm-up steps (timed per entry point after the first, to find the dominant kernel), then
+    exactly `steps` timed steps in which only the dominant entry point carries HIP events (the
+    roofline's live launch time; events around every call would add ~0.13 ms per step), then a
+    few more steps with every entry point timed, for the per-kernel table."""
     w = workloads.build(name)
     step = make_step(w, device)
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-
     timer = KernelTimer(BytesModel(w))
     timer.install()
+    for i in range(warmup):
+        timer.active = i > 0 or warmup == 1
+        step()
+    timer.active = False
+    torch.cuda.synchronize()
+    dominant = None
+    if timer.events:
+        dominant = dominant_entry(timer.summary(), timer.bytes)
+    timer.reset()
+    timer.only = None if dominant is None else {dominant}
+
     timer.active = True
     torch.cuda.synchronize()
     start = time.perf_counter()
@@ -494,25 +517,35 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
     timer.active = False
-    timer.uninstall()
     ms_per_step = elapsed * 1e3 / steps
+    live = timer.summary()
+    if dominant is None:  # no warm-up: every entry point was timed in the timed steps
+        dominant = dominant_entry(live, timer.bytes)
+    dom_total, dom_count = live[dominant]
+    dom_ms = dom_total / dom_count
+    dom_bytes = timer.bytes[dominant] / dom_count
 
+    # The per-kernel table, from its own steps after the timed ones.
+    table_steps = min(steps, 5)
+    timer.reset()
+    timer.only = None
+    timer.active = True
+    for _ in range(table_steps):
+        step()
+    torch.cuda.synchronize()
+    timer.active = False
+    timer.uninstall()
     per_kernel = timer.summary()
     kernels = {}
     for kname, (total_ms, count) in per_kernel.items():
         mean_ms = total_ms / count
-        entry = {"ms_per_step": round(total_ms / steps, 4), "launches_per_step":
-                 count // steps, "mean_launch_ms": round(mean_ms, 4)}
+        entry = {"ms_per_step": round(total_ms / table_steps, 4), "launches_per_step":
+                 count // table_steps, "mean_launch_ms": round(mean_ms, 4)}
         if kname in timer.bytes:
             gbs = timer.bytes[kname] / count / (mean_ms * 1e-3) / 1e9
             entry["GB/s"] = round(gbs, 1)
             entry["frac"] = round(gbs * 1e9 / HBM_PEAK, 4)
         kernels[kname] = entry
-    dominant = max((n for n in per_kernel if n in SINGLE_KERNEL and n in timer.bytes),
-                   key=lambda n: per_kernel[n][0])
-    dom_total, dom_count = per_kernel[dominant]
-    dom_ms = dom_total / dom_count
-    dom_bytes = timer.bytes[dominant] / dom_count
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     traffic = profiled_traffic(SINGLE_KERNEL[dominant], name)
 

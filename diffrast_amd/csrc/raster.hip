@@ -1494,8 +1494,15 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
   }
   int status = launch_status();
   if (status != DR_OK) return status;
-  uint32_t host[4] = {0, 0, 0, 0};
-  if (hipMemcpyAsync(host, ws.counters, sizeof(host), hipMemcpyDeviceToHost, s) != hipSuccess ||
+  // The counts come back through pinned host memory (one small buffer per host thread, kept
+  // for the life of the process): a copy into pageable memory is staged and slower to return.
+  static thread_local uint32_t* host = nullptr;
+  if (host == nullptr && hipHostMalloc((void**)&host, 4 * sizeof(uint32_t)) != hipSuccess) {
+    host = nullptr;
+    return DR_ERR_HIP;
+  }
+  if (hipMemcpyAsync(host, ws.counters, 4 * sizeof(uint32_t), hipMemcpyDeviceToHost, s) !=
+          hipSuccess ||
       hipStreamSynchronize(s) != hipSuccess)
     return DR_ERR_HIP;
   counts[0] = (uint32_t)ws.record_blocks;
