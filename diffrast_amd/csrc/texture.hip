@@ -458,10 +458,28 @@ __device__ __forceinline__ void lookup_setup(const DrTextureArgs& a, int64_t pix
   }
 }
 
-__device__ __forceinline__ Bilinear level_setup(const DrTextureArgs& a, const Lookup& K, int l) {
-  const int k = K.level[l];
-  return bilinear_setup(K.s, K.t, K.face, a.level_height[k], a.level_width[k],
-                        a.level_offset[k], a.boundary);
+// Sizes and packed offset of the two levels a lookup may use. The level index differs per lane,
+// so these are memory reads: both levels' are issued together, before either is used.
+struct LevelDims {
+  int h[2], w[2];
+  int64_t off[2];
+};
+
+__device__ __forceinline__ LevelDims lookup_levels(const DrTextureArgs& a, const Lookup& K) {
+  LevelDims D;
+#pragma unroll
+  for (int l = 0; l < 2; ++l) {
+    const int k = K.level[l];
+    D.h[l] = a.level_height[k];
+    D.w[l] = a.level_width[k];
+    D.off[l] = a.level_offset[k];
+  }
+  return D;
+}
+
+__device__ __forceinline__ Bilinear level_setup(const DrTextureArgs& a, const Lookup& K,
+                                                const LevelDims& D, int l) {
+  return bilinear_setup(K.s, K.t, K.face, D.h[l], D.w[l], D.off[l], a.boundary);
 }
 
 // Nearest: the texel containing the coordinate (reference.py:555-573).
@@ -500,9 +518,10 @@ __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* __
     for (int c = 0; c < C; ++c) o[c] = bad ? nan : (valid ? texels[index * C + c] : 0.0f);
     return;
   }
-  const Bilinear L0 = level_setup(a, K, 0);
+  const LevelDims D = lookup_levels(a, K);
+  const Bilinear L0 = level_setup(a, K, D, 0);
   const bool two = K.levels == 2;
-  const Bilinear L1 = two ? level_setup(a, K, 1) : L0;
+  const Bilinear L1 = two ? level_setup(a, K, D, 1) : L0;
   const bool bad = K.bad || L0.bad || (two && L1.bad);
   const float frac = K.level_weight[1];
   for (int c0 = 0; c0 < C; c0 += NC) {
@@ -628,10 +647,11 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     }
     live = false;  // no coordinate gradient
   } else if (live) {
-    const Bilinear L0 = level_setup(a, K, 0);
+    const LevelDims D = lookup_levels(a, K);
+    const Bilinear L0 = level_setup(a, K, D, 0);
     Bilinear L1 = L0;
     const bool two = K.levels == 2;
-    if (two) L1 = level_setup(a, K, 1);
+    if (two) L1 = level_setup(a, K, D, 1);
     if (K.bad || L0.bad || (two && L1.bad)) {
       live = false;
     } else {
