@@ -454,18 +454,18 @@ __device__ __forceinline__ PixelPairs pixel_pairs(const DrAntialiasArgs& a, cons
   P.t[1] = own_t.y;
   P.other[1] = tp.pixel + a.width;
   P.first[1] = true;
-  P.active[2] = false;
-  P.active[3] = false;
-  if (tp.x > 0) {
-    P.active[2] = pair_bits[tp.pixel - 1].x & kActive;
-    P.t[2] = pair_t[tp.pixel - 1].x;
-  }
+  // The left and upper neighbours' records, read with the pixel's own (a pixel on the first
+  // column or row reads its own record there and ignores it): no branch between the loads.
+  const int64_t left = tp.x > 0 ? tp.pixel - 1 : tp.pixel;
+  const int64_t up = tp.y > 0 ? tp.pixel - a.width : tp.pixel;
+  const uchar2 left_b = pair_bits[left], up_b = pair_bits[up];
+  const float2 left_t = pair_t[left], up_t = pair_t[up];
+  P.active[2] = tp.x > 0 && (left_b.x & kActive);
+  P.t[2] = left_t.x;
   P.other[2] = tp.pixel - 1;
   P.first[2] = false;
-  if (tp.y > 0) {
-    P.active[3] = pair_bits[tp.pixel - a.width].y & kActive;
-    P.t[3] = pair_t[tp.pixel - a.width].y;
-  }
+  P.active[3] = tp.y > 0 && (up_b.y & kActive);
+  P.t[3] = up_t.y;
   P.other[3] = tp.pixel - a.width;
   P.first[3] = false;
   return P;
@@ -506,13 +506,22 @@ __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const 
 #pragma unroll
     for (int c = 0; c < 4; ++c) v[c] = own[c];
     if (any) {
+      // Every neighbour that lends colour is read before any is used.
+      float other[4][4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        if (weight[n] != 0.0f) {
+          load_px4(a.color + P.other[n] * 4, other[n]);
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) other[n][c] = own[c];
+        }
+      }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         if (weight[n] == 0.0f) continue;
-        float other[4];
-        load_px4(a.color + P.other[n] * 4, other);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[c] += weight[n] * (other[c] - own[c]);
+        for (int c = 0; c < 4; ++c) v[c] += weight[n] * (other[n][c] - own[c]);
       }
     }
     if (!store_wide<4>(o, v))
@@ -558,12 +567,22 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
       load_px4(g, gv);
 #pragma unroll
       for (int c = 0; c < 4; ++c) v[c] = gv[c];
+      // Every active neighbour's gradient is read before any is used.
+      float g2s[4][4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        if (P.active[n]) {
+          load_px4(grad_out + P.other[n] * 4, g2s[n]);
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) g2s[n][c] = 0.0f;
+        }
+      }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         if (!P.active[n]) continue;
         const float t = P.t[n];
-        float g2[4];
-        load_px4(grad_out + P.other[n] * 4, g2);
+        const float (&g2)[4] = g2s[n];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           if (P.first[n]) {
