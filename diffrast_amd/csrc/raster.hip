@@ -1269,23 +1269,35 @@ __global__ __launch_bounds__(256) void resolve_fwd_kernel(DrRasterGeometry g,
     pixel[j] = first + (int64_t)j * blockDim.x;
     key[j] = pixel[j] < total ? keys[pixel[j]] : kEmptyKey;
   }
+  // The pixels' index rows, then their vertices, each level's loads issued together: in a wave
+  // with any covered pixel every lane reads (triangle 0 of image 0 for an empty one), with no
+  // branch between the pixels.
   int v[kPixels][3];
   int b[kPixels];
+  bool covered = false;
 #pragma unroll
   for (int j = 0; j < kPixels; ++j) {
-    b[j] = 0;
+    const bool hit = key[j] != kEmptyKey;
+    covered = covered || hit;
+    const int64_t image_pixels = (int64_t)g.height * g.width;
+    const int image = pixel[j] < 0xffffffffLL && image_pixels < 0xffffffffLL
+                          ? (int)((uint32_t)pixel[j] / (uint32_t)image_pixels)
+                          : (int)(pixel[j] / image_pixels);
+    b[j] = hit ? image : 0;
     v[j][0] = v[j][1] = v[j][2] = 0;
-    if (key[j] == kEmptyKey) continue;
-    const int32_t* row = g.tri + 3 * (int64_t)(uint32_t)key[j];
-    v[j][0] = row[0];
-    v[j][1] = row[1];
-    v[j][2] = row[2];
-    b[j] = (int)(pixel[j] / ((int64_t)g.height * g.width));
   }
   Tri T[kPixels];
+  if (__any(covered)) {  // then tri has rows
 #pragma unroll
-  for (int j = 0; j < kPixels; ++j)
-    if (key[j] != kEmptyKey) load_vertices(g, b[j], v[j], T[j]);
+    for (int j = 0; j < kPixels; ++j) {
+      const int32_t* row = g.tri + 3 * (int64_t)(key[j] != kEmptyKey ? (uint32_t)key[j] : 0u);
+      v[j][0] = row[0];
+      v[j][1] = row[1];
+      v[j][2] = row[2];
+    }
+#pragma unroll
+    for (int j = 0; j < kPixels; ++j) load_vertices(g, b[j], v[j], T[j]);
+  }
 #pragma unroll
   for (int j = 0; j < kPixels; ++j) {
     if (pixel[j] >= total) continue;
