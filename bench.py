@@ -240,6 +240,21 @@ def _mse(x, target):
     return torch.nn.functional.mse_loss(x, target)
 
 
+class _Shade(torch.autograd.Function):
+    """col + 0.1 * (f[..., :4] + f[..., 4:]) for 8-channel features. The same values and
+    gradients as autograd through the expression (bit for bit); its backward repeats the
+    gradient into both halves in one copy, where autograd's view/sum backward makes a strided
+    copy of the expanded gradient (~0.11 ms at 8 x 1024^2)."""
+
+    @staticmethod
+    def forward(ctx, col, f):
+        return col + 0.1 * (f[..., :4] + f[..., 4:])
+
+    @staticmethod
+    def backward(ctx, g):
+        return g, (0.1 * g).repeat(*([1] * (g.dim() - 1)), 2)
+
+
 def make_step(w, device):
     """One forward+backward step of workload ``w`` on the GPU (inputs copied to ``device``)."""
     t = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in w.tensors.items()}
@@ -281,7 +296,7 @@ def make_step(w, device):
             st, st_da = dr.interpolate(uv_attr, rast, tri, rast_db, diff_attrs="all")
             col = dr.texture(tex, st, st_da, filter_mode="linear-mipmap-linear",
                              boundary_mode="wrap")
-            shaded = col + 0.1 * f.view(*f.shape[:-1], 2, 4).sum(-2)  # f[..., :4] + f[..., 4:]
+            shaded = _Shade.apply(col, f)  # col + 0.1 * (f[..., :4] + f[..., 4:])
             return _mse(dr.antialias(shaded, rast, pos, tri), target)
     elif w.name == "cubemap":
         pos, cube = leaf("pos"), leaf("cube")
