@@ -432,9 +432,8 @@ __device__ __forceinline__ uint32_t spread10(uint32_t v) {
   return v;
 }
 
-// Morton bucket (top 12 bits of a 30-bit code) of a triangle's centroid.
-__device__ __forceinline__ uint32_t order_bucket(const Workspace& ws, int t) {
-  const float4 c = ws.centroids[t];
+// Morton bucket (top 12 bits of a 30-bit code) of a triangle's centroid c.
+__device__ __forceinline__ uint32_t order_bucket(const Workspace& ws, float4 c) {
   const float cc[3] = {c.x, c.y, c.z};
   uint32_t q[3];
 #pragma unroll
@@ -457,11 +456,20 @@ __global__ __launch_bounds__(256) void order_count(DrRasterGeometry g, Workspace
   __shared__ uint32_t hist[kOrderBuckets];
   for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x) hist[i] = 0u;
   __syncthreads();
+  // The thread's centroids are all loaded before the first is used (a clamped index past the
+  // end, not a branch, so nothing separates the loads).
   const int64_t first = (int64_t)blockIdx.x * blockDim.x * kOrderPerThread;
+  float4 c[kOrderPerThread];
+#pragma unroll
   for (int i = 0; i < kOrderPerThread; ++i) {
     const int64_t t = first + (int64_t)i * blockDim.x + threadIdx.x;
-    if (t >= g.num_tri) break;
-    const uint32_t bucket = order_bucket(ws, (int)t);
+    c[i] = ws.centroids[t < g.num_tri ? t : g.num_tri - 1];
+  }
+#pragma unroll
+  for (int i = 0; i < kOrderPerThread; ++i) {
+    const int64_t t = first + (int64_t)i * blockDim.x + threadIdx.x;
+    if (t >= g.num_tri) continue;
+    const uint32_t bucket = order_bucket(ws, c[i]);
     ws.centroids[t].w = __uint_as_float(bucket);  // for order_place
     atomicAdd(hist + bucket, 1u);
   }
@@ -499,25 +507,56 @@ __global__ __launch_bounds__(256) void order_place(DrRasterGeometry g, Workspace
   __shared__ uint32_t base[kOrderBuckets];
   for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x) hist[i] = 0u;
   __syncthreads();
+  // The thread's buckets, all loaded before the first is used (clamped index past the end).
   const int64_t first = (int64_t)blockIdx.x * blockDim.x * kOrderPerThread;
+  uint32_t bucket[kOrderPerThread];
+#pragma unroll
   for (int i = 0; i < kOrderPerThread; ++i) {
     const int64_t t = first + (int64_t)i * blockDim.x + threadIdx.x;
-    if (t >= g.num_tri) break;
-    atomicAdd(hist + __float_as_uint(ws.centroids[t].w), 1u);
+    bucket[i] = __float_as_uint(ws.centroids[t < g.num_tri ? t : g.num_tri - 1].w);
+  }
+#pragma unroll
+  for (int i = 0; i < kOrderPerThread; ++i) {
+    const int64_t t = first + (int64_t)i * blockDim.x + threadIdx.x;
+    if (t < g.num_tri) atomicAdd(hist + bucket[i], 1u);
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x) {
-    if (hist[i]) base[i] = atomicAdd(ws.bucket_cursor + i, hist[i]);
+  // The reservations: each thread's buckets' atomics are all issued before it waits for any.
+  constexpr int kBucketsPerThread = kOrderBuckets / 256;
+  uint32_t reserved[kBucketsPerThread];
+#pragma unroll
+  for (int k = 0; k < kBucketsPerThread; ++k) {
+    const int i = threadIdx.x + k * 256;
+    reserved[k] = hist[i] ? atomicAdd(ws.bucket_cursor + i, hist[i]) : 0u;
+  }
+#pragma unroll
+  for (int k = 0; k < kBucketsPerThread; ++k) {
+    const int i = threadIdx.x + k * 256;
+    base[i] = reserved[k];
     hist[i] = 0u;
   }
   __syncthreads();
-  for (int i = 0; i < kOrderPerThread; ++i) {
-    const int64_t t = first + (int64_t)i * blockDim.x + threadIdx.x;
-    if (t >= g.num_tri) break;
-    const uint32_t bucket = __float_as_uint(ws.centroids[t].w);
-    const int32_t* row = g.tri + 3 * t;
-    ws.order[base[bucket] + atomicAdd(hist + bucket, 1u)] =
-        make_int4(row[0], row[1], row[2], (int)t);
+  // The index rows, a quarter of the thread's triangles at a time, loaded before their use.
+  constexpr int kQuarter = kOrderPerThread / 4;
+#pragma unroll
+  for (int q = 0; q < kOrderPerThread; q += kQuarter) {
+    int32_t rows[kQuarter][3];
+#pragma unroll
+    for (int i = 0; i < kQuarter; ++i) {
+      const int64_t t = first + (int64_t)(q + i) * blockDim.x + threadIdx.x;
+      const int32_t* row = g.tri + 3 * (t < g.num_tri ? t : g.num_tri - 1);
+      rows[i][0] = row[0];
+      rows[i][1] = row[1];
+      rows[i][2] = row[2];
+    }
+#pragma unroll
+    for (int i = 0; i < kQuarter; ++i) {
+      const int64_t t = first + (int64_t)(q + i) * blockDim.x + threadIdx.x;
+      if (t >= g.num_tri) continue;
+      const uint32_t b = bucket[q + i];
+      ws.order[base[b] + atomicAdd(hist + b, 1u)] =
+          make_int4(rows[i][0], rows[i][1], rows[i][2], (int)t);
+    }
   }
 }
 
@@ -867,9 +906,20 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
       if (slot >= 0) atomicAdd(table.count + slot, 1u);
     }
   __syncthreads();
-  for (int s = threadIdx.x; s < kTileSlots; s += blockDim.x) {
+  // The reservations: each thread's slots' atomics are all issued before it waits for any.
+  constexpr int kSlotsPerThread = kTileSlots / 256;
+  uint32_t reserved[kSlotsPerThread];
+#pragma unroll
+  for (int k = 0; k < kSlotsPerThread; ++k) {
+    const int s = threadIdx.x + k * 256;
+    reserved[k] = 0u;
     if (table.key[s] != TileTable::kEmpty)
-      table.base[s] = atomicAdd(ws.list_cursor + table.key[s], table.count[s]);
+      reserved[k] = atomicAdd(ws.list_cursor + table.key[s], table.count[s]);
+  }
+#pragma unroll
+  for (int k = 0; k < kSlotsPerThread; ++k) {
+    const int s = threadIdx.x + k * 256;
+    table.base[s] = reserved[k];
     table.count[s] = 0u;
   }
   __syncthreads();
@@ -983,8 +1033,17 @@ __global__ __launch_bounds__(256) void raster_tile_place(Workspace ws) {
     atomicAdd(hist + slot, 1u);
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < kXcdShares * kWorkClasses; i += blockDim.x) {
-    if (hist[i]) base[i] = atomicAdd(ws.class_cursor + i, hist[i]);
+  constexpr int kClassesPerThread = kXcdShares * kWorkClasses / 256;
+  uint32_t reserved[kClassesPerThread];
+#pragma unroll
+  for (int k = 0; k < kClassesPerThread; ++k) {
+    const int i = threadIdx.x + k * 256;
+    reserved[k] = hist[i] ? atomicAdd(ws.class_cursor + i, hist[i]) : 0u;
+  }
+#pragma unroll
+  for (int k = 0; k < kClassesPerThread; ++k) {
+    const int i = threadIdx.x + k * 256;
+    base[i] = reserved[k];
     hist[i] = 0u;
   }
   __syncthreads();
