@@ -53,8 +53,16 @@ def get_backend(device: torch.device | str, op: str) -> ModuleType:
     return _load(get_backend_name(device, op))
 
 
+_loaded: dict[str, ModuleType] = {}
+
+
 def _load(name: str) -> ModuleType:
-    return importlib.import_module(f"diffrast_amd.backends.{ALIASES.get(name, name)}")
+    # Cached: import_module takes the import lock on every call (~13 us), once per op call.
+    module = _loaded.get(name)
+    if module is None:
+        module = importlib.import_module(f"diffrast_amd.backends.{ALIASES.get(name, name)}")
+        _loaded[name] = module
+    return module
 
 
 def _check_name(name: str) -> None:
