@@ -144,9 +144,17 @@ __device__ __forceinline__ float side(const float (&line)[3], const XYW& p) {
 // Marks the triangles that rast shows (only their silhouette bits are ever read).
 constexpr uint8_t kShown = 0x80;
 
+// Zeroes n bytes: 16-byte stores over the aligned body, single bytes before and after it.
 __global__ void aa_clear_mask(uint8_t* mask, int64_t n) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (; i < n; i += (int64_t)gridDim.x * blockDim.x) mask[i] = 0;
+  const int64_t head = std::min<int64_t>(n, (int64_t)((16u - ((uintptr_t)mask & 15u)) & 15u));
+  const int64_t body = (n - head) / 16;
+  const int64_t tail = head + body * 16;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < head) mask[t] = 0;
+  if (t < n - tail) mask[tail + t] = 0;
+  uint4* wide = reinterpret_cast<uint4*>(mask + head);
+  for (int64_t i = t; i < body; i += (int64_t)gridDim.x * blockDim.x)
+    wide[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
 __global__ __launch_bounds__(256) void aa_mark_shown(const float* rast, int64_t image_pixels,
@@ -731,7 +739,8 @@ extern "C" int dr_silhouette_mask(const float* pos, int64_t pos_batch_stride, in
     if (batch < 0 || height <= 0 || width <= 0) return DR_ERR_ARGUMENT;
     if (pos_batch > 1 && pos_batch != batch) return DR_ERR_ARGUMENT;
     const int64_t image_pixels = (int64_t)height * width, pixels = image_pixels * batch;
-    aa_clear_mask<<<(int)std::min<int64_t>(blocks_for(n, 256), 65536), 256, 0, s>>>(mask, n);
+    aa_clear_mask<<<(int)std::min<int64_t>(blocks_for(n / 16 + 16, 256), 65536), 256, 0, s>>>(
+        mask, n);
     if (pixels > 0)
       aa_mark_shown<<<blocks_for(pixels, 256), 256, 0, s>>>(rast, image_pixels, pixels, num_tri,
                                                            pos_batch, mask);
