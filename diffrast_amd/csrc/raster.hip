@@ -47,6 +47,7 @@ constexpr int kTileSlots = 1024;     // LDS table of a workgroup's tiles
 constexpr int kRecord = 4;           // float4 per binned triangle record (one 64-byte line)
 constexpr int kDepthSlabs = 16;      // tile lists per tile, by the triangle's nearest depth
 constexpr int kRangeParts = 64;      // workgroups per image in the depth span reduction
+constexpr int kXcdShares = 8;        // XCDs of an MI355X: workgroup b runs on XCD b mod 8
 
 struct Workspace {
   float4* records;           // binned triangles, kRecord float4 each: the three clip-space
@@ -327,20 +328,20 @@ struct TileTable {
 
 // ---- kernels: fills and pixel centres -----------------------------------------------------
 
-__global__ void raster_fill_keys(uint64_t* keys, int64_t n) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (; i < n; i += (int64_t)gridDim.x * blockDim.x) keys[i] = kEmptyKey;
-}
-
-__global__ void raster_fill_u32(uint32_t* p, int64_t n, uint32_t value) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = value;
-}
-
-__global__ void raster_centres(float* px, int width, float* py, int height) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < width) px[i] = pixel_centre(i, width);
-  if (i < height) py[i] = pixel_centre(i, height);
+// Everything a visibility call starts from, in one launch: the key buffer emptied, the list
+// counts, counters and class (and bucket) counts zeroed, the pixel centres tabulated.
+__global__ void raster_prepare(uint64_t* keys, int64_t pixels, Workspace ws, int width,
+                               int height) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t i = t; i < pixels; i += stride) keys[i] = kEmptyKey;
+  for (int64_t i = t; i < ws.lists + 1; i += stride) ws.list_counts[i] = 0u;
+  for (int64_t i = t; i < kXcdShares * kWorkClasses; i += stride) ws.class_counts[i] = 0u;
+  if (ws.ordered)
+    for (int64_t i = t; i < kOrderBuckets; i += stride) ws.bucket_counts[i] = 0u;
+  if (t < 4) ws.counters[t] = 0u;
+  for (int64_t i = t; i < width; i += stride) ws.px[i] = pixel_centre((int)i, width);
+  for (int64_t i = t; i < height; i += stride) ws.py[i] = pixel_centre((int)i, height);
 }
 
 // ---- kernels: triangle order --------------------------------------------------------------
@@ -943,8 +944,6 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
 // cursors, placement); workgroups aggregate in LDS before touching global counters. The order
 // within a class is free: tiles are independent.
 
-constexpr int kXcdShares = 8;
-
 // The XCD share of tile i under xcd_order, and the first tile of share k.
 __device__ __forceinline__ int xcd_share(int64_t i, int64_t tiles) {
   if (tiles < kXcdShares) return (int)i;
@@ -1529,19 +1528,12 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
   // Record slots (256 per setup workgroup) and tiles are indexed with 32 bits.
   if (g->num_instances > ((int64_t)1 << 32) - 512 || ws.lists >= ((int64_t)1 << 32) - 1)
     return DR_ERR_ARGUMENT;
-  const int fill_blocks = (int)std::min<int64_t>(blocks_for(pixels, 256), 65536);
-  raster_fill_keys<<<fill_blocks, 256, 0, s>>>(keys, pixels);
-  raster_fill_u32<<<(int)std::min<int64_t>(blocks_for(ws.lists + 1, 256), 65536), 256, 0, s>>>(
-      ws.list_counts, ws.lists + 1, 0u);
-  raster_fill_u32<<<1, 64, 0, s>>>(ws.counters, 4, 0u);
-  raster_fill_u32<<<4, 256, 0, s>>>(ws.class_counts, 8 * kWorkClasses, 0u);
-  raster_centres<<<blocks_for(std::max(g->width, g->height), 256), 256, 0, s>>>(
-      ws.px, g->width, ws.py, g->height);
+  const int64_t fill_items = std::max<int64_t>(pixels, ws.lists + 1);
+  raster_prepare<<<(int)std::min<int64_t>(blocks_for(fill_items, 256), 65536), 256, 0, s>>>(
+      keys, pixels, ws, g->width, g->height);
   if (g->num_instances > 0) {
     if (ws.ordered) {
       const int tri_blocks = blocks_for(g->num_tri, 256);
-      raster_fill_u32<<<blocks_for(kOrderBuckets, 256), 256, 0, s>>>(ws.bucket_counts,
-                                                                     kOrderBuckets, 0u);
       order_centroids<<<tri_blocks, 256, 0, s>>>(*g, ws);
       order_bounds<<<1, 256, 0, s>>>(ws, tri_blocks);
       const int bucket_blocks = blocks_for(g->num_tri, 256 * kOrderPerThread);
