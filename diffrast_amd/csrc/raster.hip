@@ -16,15 +16,18 @@
 //    kSmallPixels pixel centres are rasterized right away (64-bit atomic min per covered
 //    pixel); the others are binned into 16x16 tiles. Per-tile counts gather in an LDS table of
 //    the workgroup before one global atomic per distinct tile.
-// 3. A three-phase scan turns tile counts into list offsets and work chunks; the bin pass
-//    reserves each workgroup's share of a tile's list with one global atomic and fills it.
-// 4. One 256-thread workgroup per (tile, chunk of <= 256 triangles) starts from the tile's keys
-//    so far, skips triangles that lie entirely behind the farthest of them, stages the others
-//    in LDS with, per tile row, the span of columns their pixel centres may cover (a bound
-//    proved against the coverage test in coverage.h), and tests the pixels of those spans as
-//    one flat list of work items (every lane busy whatever the span lengths), merging into the
-//    tile's keys in LDS (64-bit min); improved keys then go to the key buffer, one atomic per
-//    pixel.
+// 3. A three-phase scan turns tile counts into list offsets; the bin pass reserves each
+//    workgroup's share of a tile's list with one global atomic and fills it. Each tile has one
+//    list per depth slab (the triangle's nearest vertex within the image's depth span), so a
+//    tile's entries run near to far.
+// 4. One 256-thread workgroup per tile with entries (heavy tiles first, each XCD on its own
+//    share of the tiles) holds the tile's keys in LDS and walks its entries 256 at a time:
+//    triangles entirely behind the tile's farthest key are skipped; the others are staged in
+//    LDS with, per tile row, the span of columns their pixel centres may cover (a bound proved
+//    against the coverage test in coverage.h), and the pixels of those spans are tested as one
+//    flat list of work items (every lane busy whatever the span lengths), merging into the
+//    tile's keys (64-bit min). The workgroup alone owns the tile: one plain store per pixel at
+//    the end.
 //
 // The resolve kernels turn keys into rast / rast_db (reference.py:69-114) and carry gradients
 // back to the vertices.
