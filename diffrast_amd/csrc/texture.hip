@@ -9,9 +9,12 @@
 // buffer [tex_batch, texels, channels], so a mipmapped lookup is two bilinear lookups
 // wherever the pixel's levels are.
 //
-// The backward pass writes the coordinate, derivative and bias gradients per pixel and adds
-// texel gradients with fp32 atomics. The mip chain is built level by level with exact area
-// weights (reference.py:449-488), and its adjoint is a gather, so it needs no atomics.
+// The backward pass writes the coordinate, derivative and bias gradients per pixel; texel
+// gradients are summed per workgroup in an LDS table (fixed point, after runs of neighbouring
+// pixels on one texel have summed) and reach global memory with one fp32 atomic per row and
+// channel. The mip chain uses exact area weights (reference.py:449-488): where sizes halve
+// exactly, a workgroup takes a 64 x 64 tile through six levels in LDS; odd sizes go level by
+// level. Its adjoint is a gather, so it needs no atomics.
 #include <type_traits>
 
 #include "common.h"
