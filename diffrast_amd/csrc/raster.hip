@@ -574,15 +574,25 @@ __global__ __launch_bounds__(256) void raster_depth_range(DrRasterGeometry g, Wo
   __shared__ uint32_t s_lo[256 / DR_WAVE], s_hi[256 / DR_WAVE];
   const int image = blockIdx.x / kRangeParts, part = blockIdx.x % kRangeParts;
   const float* P = g.pos + (int64_t)image * g.pos_batch_stride;
+  // Four vertices per thread and step, loaded before any is used; the span only places
+  // triangles in depth slabs (an ordering), so the hardware reciprocal serves for z / w.
   uint32_t lo = 0xffffffffu, hi = 0u;
-  for (int v = part * blockDim.x + threadIdx.x; v < g.num_vertices;
-       v += kRangeParts * blockDim.x) {
-    const float4 p = load4(P + 4 * (int64_t)v);
-    const float d = p.z / p.w;
-    if (p.w > 0.0f && isfinite(d)) {
-      const uint32_t bits = ordered_bits(fminf(fmaxf(d, -1.0f), 1.0f));
-      lo = min(lo, bits);
-      hi = max(hi, bits);
+  const int step = kRangeParts * blockDim.x;
+  for (int v0 = part * blockDim.x + threadIdx.x; v0 < g.num_vertices; v0 += 4 * step) {
+    float4 p[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int v = v0 + u * step;
+      p[u] = v < g.num_vertices ? load4(P + 4 * (int64_t)v) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float d = p[u].z * __builtin_amdgcn_rcpf(p[u].w);
+      if (p[u].w > 0.0f && isfinite(d)) {
+        const uint32_t bits = ordered_bits(fminf(fmaxf(d, -1.0f), 1.0f));
+        lo = min(lo, bits);
+        hi = max(hi, bits);
+      }
     }
   }
 #pragma unroll
