@@ -71,6 +71,7 @@ class KernelTimer:
     def __init__(self, bytes_of):
         self.events = defaultdict(list)
         self.bytes = defaultdict(float)
+        self.pending = defaultdict(list)
         self.bytes_of = bytes_of
         self.active = False
         self.only = None  # entry point names to time (None: every one)
@@ -79,6 +80,14 @@ class KernelTimer:
     def reset(self):
         self.events = defaultdict(list)
         self.bytes = defaultdict(float)
+        self.pending = defaultdict(list)
+
+    def resolve(self):
+        """Bytes of the timed calls; a model may return a function of counts that are known
+        only after the call (the tile pass queued before its list sizes arrive)."""
+        for name, amounts in self.pending.items():
+            self.bytes[name] += sum(a() if callable(a) else a for a in amounts)
+        self.pending = defaultdict(list)
 
     def install(self):
         def timed(name, *args):
@@ -92,7 +101,7 @@ class KernelTimer:
             self.events[name].append((start, end))
             amount = self.bytes_of(name, args)
             if amount is not None:
-                self.bytes[name] += amount
+                self.pending[name].append(amount)
 
         hip.call = timed
 
@@ -101,6 +110,7 @@ class KernelTimer:
 
     def summary(self):
         torch.cuda.synchronize()
+        self.resolve()
         out = {}
         for name, pairs in self.events.items():
             times = [s.elapsed_time(e) for s, e in pairs]
@@ -142,13 +152,15 @@ class BytesModel:
     def _pixels(g):
         return g.batch * g.height * g.width
 
-    def raster_visibility_begin(self, args):
+    def raster_visibility_start(self, args):
         g = _struct(args[0])
         return self.pos_bytes(self.pos_images) + self.tri * 12 + self._pixels(g) * 8
 
     def raster_visibility_tiles(self, args):
+        # The counts array holds the list sizes once the caller has them (after the call when
+        # the pass was queued before they arrived).
         counts = args[6]
-        return counts[1] * TILE_ENTRY_BYTES + counts[3] * TILE_KEY_BYTES
+        return lambda: counts[1] * TILE_ENTRY_BYTES + counts[3] * TILE_KEY_BYTES
 
     def resolve_forward(self, args):
         P = self._pixels(_struct(args[0]))

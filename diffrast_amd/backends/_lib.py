@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent.parent / "libdiffrast_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 MAX_LEVELS = 32
 
 c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -107,6 +107,7 @@ _SIGNATURES = {
     "dr_raster_workspace_size": ([_P, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "dr_raster_visibility_begin": (
         [_P, _P, _P, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_uint32), _P], ctypes.c_int),
+    "dr_raster_visibility_start": ([_P, _P, _P, _P, ctypes.c_size_t, _P, _P], ctypes.c_int),
     "dr_raster_visibility_bin": (
         [_P, _P, ctypes.c_size_t, _P, ctypes.POINTER(ctypes.c_uint32), _P], ctypes.c_int),
     "dr_raster_visibility_tiles": (

@@ -17,6 +17,7 @@ are kernels and cannot be differentiated again (``first_order``).
 from __future__ import annotations
 
 import ctypes
+import threading
 from collections.abc import Sequence
 
 import torch
@@ -81,6 +82,32 @@ class _Geometry:
         self.shape = (self.batch, int(height), int(width))
 
 
+# Tile entries seen last for a geometry shape: the next call with that shape queues binning
+# and the tile pass with a buffer this large (plus a margin) before the count reaches the host,
+# so that the device does not wait for the host, and bins again with a buffer of the exact
+# size only when the lists outgrow it.
+_ENTRY_HINTS: dict[tuple, int] = {}
+_ENTRY_HINTS_KEPT = 64
+_host = threading.local()
+
+
+def _entry_capacity(count: int) -> int:
+    return min(count + count // 8 + 4096, 0xffffffff)
+
+
+def _host_counts(device: torch.device) -> tuple[Tensor, torch.cuda.Event]:
+    """Pinned memory for the visibility counts and the event that marks their arrival (one
+    pair per host thread and device: a call waits for its counts before it returns)."""
+    per_device = getattr(_host, "counts", None)
+    if per_device is None:
+        per_device = _host.counts = {}
+    pair = per_device.get(device.index)
+    if pair is None:
+        pair = (torch.zeros(4, dtype=torch.int32, pin_memory=True), torch.cuda.Event())
+        per_device[device.index] = pair
+    return pair
+
+
 def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
     """Visibility keys [batch, height, width] (int64 holding the uint64 key bits)."""
     device = geo.pos.device
@@ -88,18 +115,43 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
     size = ctypes.c_size_t()
     call("dr_raster_workspace_size", ref(geo.struct), ctypes.byref(size))
     workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
-    counts = (ctypes.c_uint32 * 4)()
     prev = None if previous is None else previous.contiguous()
     stream = _lib.stream(device)
-    call("dr_raster_visibility_begin", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),
-         size.value, counts, stream)
-    if counts[1]:
-        # the tile lists, tile by tile
-        entries = torch.empty(counts[1], dtype=torch.int32, device=device)
+    host, arrived = _host_counts(device)
+    hint_key = (device.index, geo.shape, geo.struct.num_tri, geo.struct.num_instances,
+                prev is None)
+    hint = _ENTRY_HINTS.get(hint_key, 0)
+    capacity = _entry_capacity(hint) if hint else 0
+    counts = (ctypes.c_uint32 * 4)(0, capacity, 0, 0)
+    call("dr_raster_visibility_start", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),
+         size.value, host.data_ptr(), stream)
+    arrived.record(torch.cuda.current_stream(device))
+    try:
+        if capacity:
+            # the tile lists and the tile pass, queued before the counts are known
+            entries = torch.empty(capacity, dtype=torch.int32, device=device)
+            call("dr_raster_visibility_bin", ref(geo.struct), ptr(workspace), size.value,
+                 ptr(entries), counts, stream)
+            call("dr_raster_visibility_tiles", ref(geo.struct), ptr(prev), ptr(keys),
+                 ptr(workspace), size.value, ptr(entries), counts, stream)
+    finally:
+        arrived.synchronize()  # the buffer is free again for the next call
+    found = [v & 0xFFFFFFFF for v in host.tolist()]
+    if found[1] or hint:
+        if len(_ENTRY_HINTS) >= _ENTRY_HINTS_KEPT and hint_key not in _ENTRY_HINTS:
+            _ENTRY_HINTS.pop(next(iter(_ENTRY_HINTS)))
+        _ENTRY_HINTS[hint_key] = found[1]
+    if found[1] > capacity:
+        # the lists did not fit (or no size was known): bin again into a buffer that fits
+        counts[:] = (0, 0, 0, 0)  # the calls above processed nothing
+        counts = (ctypes.c_uint32 * 4)(*found)
+        entries = torch.empty(found[1], dtype=torch.int32, device=device)
         call("dr_raster_visibility_bin", ref(geo.struct), ptr(workspace), size.value,
              ptr(entries), counts, stream)
         call("dr_raster_visibility_tiles", ref(geo.struct), ptr(prev), ptr(keys),
              ptr(workspace), size.value, ptr(entries), counts, stream)
+    else:
+        counts[:] = found  # the calls above now describe the lists they processed
     return keys
 
 

@@ -67,7 +67,8 @@ struct Workspace {
                              // farthest vertex depth of an image (one when pos is shared)
   uint32_t* range_parts;     // [depth_ranges][kRangeParts][2] partial spans
   uint2* block_sums;         // [scan blocks] (entries, chunks)
-  uint32_t* counters;        // [1] entries, [2] tile pass workgroups, [3] busy tiles
+  uint32_t* counters;        // [0] setup workgroups, [1] entries, [2] tile pass
+                             // workgroups, [3] busy tiles
   uint32_t* block_records;   // [record_blocks] binned triangles of each setup workgroup
   uint32_t* tile_order;      // [tiles] tile pass order: heavy tiles first within each XCD's share
   uint8_t* tile_class;       // [tiles] work class of each tile (entries / 32, capped)
@@ -342,7 +343,7 @@ __global__ void raster_prepare(uint64_t* keys, int64_t pixels, Workspace ws, int
   for (int64_t i = t; i < kXcdShares * kWorkClasses; i += stride) ws.class_counts[i] = 0u;
   if (ws.ordered)
     for (int64_t i = t; i < kOrderBuckets; i += stride) ws.bucket_counts[i] = 0u;
-  if (t < 4) ws.counters[t] = 0u;
+  if (t < 4) ws.counters[t] = t == 0 ? (uint32_t)ws.record_blocks : 0u;
   for (int64_t i = t; i < width; i += stride) ws.px[i] = pixel_centre((int)i, width);
   for (int64_t i = t; i < height; i += stride) ws.py[i] = pixel_centre((int)i, height);
 }
@@ -895,8 +896,11 @@ __global__ __launch_bounds__(256) void raster_scan_apply(const uint32_t* counts,
 
 // Fills the per-tile lists: the workgroup counts its records per tile in LDS, reserves its
 // share of each tile's list with one global atomic, then writes the entries.
-__global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws,
-                                                         uint32_t* entries) {
+__global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint32_t* entries,
+                                                         uint32_t capacity) {
+  // Entries beyond the buffer's capacity: the pass is left to a later launch with a larger
+  // buffer (the cursors stay untouched, so that launch places every entry).
+  if (ws.counters[1] > capacity) return;  // uniform over the grid
   __shared__ TileTable table;
   table.clear();
   __syncthreads();
@@ -1076,7 +1080,8 @@ __global__ __launch_bounds__(256) void raster_tile_place(Workspace ws) {
 __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
                                                           const uint64_t* prev, uint64_t* keys,
                                                           Workspace ws,
-                                                          const uint32_t* entries) {
+                                                          const uint32_t* entries,
+                                                          uint32_t capacity) {
   // Per staged triangle: the three vertices, (reach_x, reach_y) and its row of tri.
   __shared__ float4 s_tri[kChunk][3];
   __shared__ float2 s_reach[kChunk];
@@ -1097,6 +1102,8 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   // one L2, heaviest first; the grid is 8 x the largest share, the surplus returns at once.
   const int share = (int)(blockIdx.x % kXcdShares);
   const uint32_t slot = blockIdx.x / kXcdShares;
+  // Lists that did not fit the entry buffer were not binned: nothing to read.
+  if (ws.counters[1] > capacity) return;     // uniform over the grid
   if (slot >= ws.share_info[share]) return;  // uniform over the workgroup
   const uint32_t tile = ws.tile_order[ws.share_info[kXcdShares + share] + slot];
   const uint32_t begin = ws.list_offsets[(size_t)tile * kDepthSlabs];
@@ -1527,13 +1534,17 @@ extern "C" int dr_raster_workspace_size(const DrRasterGeometry* g, size_t* bytes
   return DR_OK;
 }
 
-extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint64_t* prev_keys,
-                                          uint64_t* keys, void* workspace,
-                                          size_t workspace_bytes, uint32_t counts[4],
-                                          void* stream) {
-  if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
-  counts[0] = counts[1] = counts[2] = counts[3] = 0;
-  hipStream_t s = (hipStream_t)stream;
+// The tile pass's grid when the busy tiles are not known yet: 8 x the largest share of tiles
+// (its workgroups beyond a share's busy tiles return at once).
+static int64_t tile_grid_bound(const Workspace& ws) {
+  return ws.tiles < kXcdShares ? kXcdShares
+                               : kXcdShares * ((ws.tiles + kXcdShares - 1) / kXcdShares);
+}
+
+// Queues the first part of the visibility and the copy of its counts to host_counts.
+static int queue_visibility_start(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                                  uint64_t* keys, void* workspace, size_t workspace_bytes,
+                                  uint32_t* host_counts, hipStream_t s) {
   const int64_t pixels = (int64_t)g->batch * g->height * g->width;
   if (pixels == 0) return DR_OK;
   Workspace ws = layout(*g, (char*)workspace);
@@ -1568,8 +1579,30 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
     raster_tile_cursors<<<1, 256, 0, s>>>(ws);
     raster_tile_place<<<tile_blocks, 256, 0, s>>>(ws);
   }
-  int status = launch_status();
+  const int status = launch_status();
   if (status != DR_OK) return status;
+  if (hipMemcpyAsync(host_counts, ws.counters, 4 * sizeof(uint32_t), hipMemcpyDeviceToHost, s) !=
+      hipSuccess)
+    return DR_ERR_HIP;
+  return DR_OK;
+}
+
+extern "C" int dr_raster_visibility_start(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                                          uint64_t* keys, void* workspace,
+                                          size_t workspace_bytes, uint32_t* host_counts,
+                                          void* stream) {
+  if (!valid_geometry(g) || !host_counts) return DR_ERR_ARGUMENT;
+  host_counts[0] = host_counts[1] = host_counts[2] = host_counts[3] = 0;
+  return queue_visibility_start(g, prev_keys, keys, workspace, workspace_bytes, host_counts,
+                                (hipStream_t)stream);
+}
+
+extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                                          uint64_t* keys, void* workspace,
+                                          size_t workspace_bytes, uint32_t counts[4],
+                                          void* stream) {
+  if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
+  counts[0] = counts[1] = counts[2] = counts[3] = 0;
   // The counts come back through pinned host memory (one small buffer per host thread, kept
   // for the life of the process): a copy into pageable memory is staged and slower to return.
   static thread_local uint32_t* host = nullptr;
@@ -1577,14 +1610,13 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
     host = nullptr;
     return DR_ERR_HIP;
   }
-  if (hipMemcpyAsync(host, ws.counters, 4 * sizeof(uint32_t), hipMemcpyDeviceToHost, s) !=
-          hipSuccess ||
-      hipStreamSynchronize(s) != hipSuccess)
-    return DR_ERR_HIP;
-  counts[0] = (uint32_t)ws.record_blocks;
-  counts[1] = host[1];
-  counts[2] = host[2];
-  counts[3] = host[3];
+  host[0] = host[1] = host[2] = host[3] = 0;
+  hipStream_t s = (hipStream_t)stream;
+  const int status = queue_visibility_start(g, prev_keys, keys, workspace, workspace_bytes,
+                                            host, s);
+  if (status != DR_OK) return status;
+  if (hipStreamSynchronize(s) != hipSuccess) return DR_ERR_HIP;
+  for (int i = 0; i < 4; ++i) counts[i] = host[i];
   return DR_OK;
 }
 
@@ -1592,12 +1624,13 @@ extern "C" int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspa
                                         size_t workspace_bytes, uint32_t* entries,
                                         const uint32_t counts[4], void* stream) {
   if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
-  if (counts[1] == 0) return DR_OK;
-  if (!entries || counts[2] == 0) return DR_ERR_ARGUMENT;
+  // Nothing was binned without pixels or triangles (and the workspace was not prepared).
+  if (counts[1] == 0 || g->batch == 0 || g->num_instances == 0) return DR_OK;
+  if (!entries) return DR_ERR_ARGUMENT;
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
-  raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, entries);
+  raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, entries, counts[1]);
   return launch_status();
 }
 
@@ -1606,12 +1639,14 @@ extern "C" int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint6
                                           size_t workspace_bytes, const uint32_t* entries,
                                           const uint32_t counts[4], void* stream) {
   if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
-  if (counts[1] == 0) return DR_OK;
-  if (!entries || !keys || counts[2] == 0) return DR_ERR_ARGUMENT;
+  if (counts[1] == 0 || g->batch == 0 || g->num_instances == 0) return DR_OK;
+  if (!entries || !keys) return DR_ERR_ARGUMENT;
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
+  const int64_t grid = counts[2] != 0 ? (int64_t)counts[2] : tile_grid_bound(ws);
+  if (grid >= ((int64_t)1 << 24)) return DR_ERR_ARGUMENT;  // 256 threads each, 32-bit ids
   hipStream_t s = (hipStream_t)stream;
-  raster_tile_kernel<<<counts[2], 256, 0, s>>>(*g, prev_keys, keys, ws, entries);
+  raster_tile_kernel<<<(int)grid, 256, 0, s>>>(*g, prev_keys, keys, ws, entries, counts[1]);
   return launch_status();
 }
 

@@ -82,14 +82,29 @@ int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint64_t* prev_k
                                uint64_t* keys, void* workspace, size_t workspace_bytes,
                                uint32_t counts[4], void* stream);
 
+/* dr_raster_visibility_begin without the wait: queues the same work and a copy of the four
+ * counts into host_counts (pinned host memory, e.g. from hipHostMalloc), and returns. The
+ * counts are there once the stream has passed this point (an event recorded after the call).
+ * Meanwhile the caller may queue dr_raster_visibility_bin and dr_raster_visibility_tiles with
+ * counts {0, capacity of its entry buffer, 0, 0}: if the lists fit, they complete the
+ * visibility; if not (host_counts[1] > capacity), both returned at once and the caller calls
+ * them again with the counts and a buffer of host_counts[1] entries.
+ * (Same reference interfaces as dr_raster_visibility_begin.) */
+int dr_raster_visibility_start(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                               uint64_t* keys, void* workspace, size_t workspace_bytes,
+                               uint32_t* host_counts, void* stream);
+
 /* Visibility, second part: fills the per-tile lists. entries holds counts[1] uint32: the
- * lists of all tiles, tile by tile, near to far. Nothing to do when counts[1] == 0. (The reference has no binning: its visibility tests every triangle at every
+ * lists of all tiles, tile by tile, near to far. Nothing to do when counts[1] == 0. counts[1]
+ * may also be a capacity larger than the lists: the kernel returns at once if they exceed it. (The reference has no binning: its visibility tests every triangle at every
  * pixel, reference.py:368-397; _triton_raster.py:241-306 keeps the nearest per pixel.) */
 int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspace, size_t workspace_bytes,
                              uint32_t* entries, const uint32_t counts[4], void* stream);
 
 /* Visibility, third part: rasterizes the binned triangles tile by tile into keys, after
- * dr_raster_visibility_bin with the same entries. Nothing to do when counts[1] == 0. */
+ * dr_raster_visibility_bin with the same entries and counts. Nothing to do when
+ * counts[1] == 0. counts[2] == 0 (not known yet): one workgroup per tile of the largest XCD
+ * share, 8 x, of which those past the share's busy tiles return at once. */
 int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                uint64_t* keys, void* workspace, size_t workspace_bytes,
                                const uint32_t* entries, const uint32_t counts[4], void* stream);

@@ -388,3 +388,90 @@ def test_depth_peeler_range_mode_through_public_api():
     assert (second[..., 2][both] >= first[..., 2][both]).all()
     with pytest.raises(RuntimeError, match="closed"):
         peeler.rasterize_next_layer()
+
+
+def _keys_through_abi(pos, tri, res, capacity, prev=None):
+    """Keys from dr_raster_visibility_start with binning and the tile pass queued at once into
+    an entry buffer of `capacity` (none when 0), completed with a buffer of the exact size
+    when the lists do not fit."""
+    import ctypes
+
+    from diffrast_amd.backends import _lib
+
+    geo = hip._Geometry(pos, tri, res)
+    keys = torch.empty(geo.shape, dtype=torch.int64, device=pos.device)
+    size = ctypes.c_size_t()
+    _lib.call("dr_raster_workspace_size", _lib.ref(geo.struct), ctypes.byref(size))
+    workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=pos.device)
+    host = torch.full((4,), -1, dtype=torch.int32, pin_memory=True)
+    stream = _lib.stream(pos.device)
+    _lib.call("dr_raster_visibility_start", _lib.ref(geo.struct), _lib.ptr(prev),
+              _lib.ptr(keys), _lib.ptr(workspace), size.value, host.data_ptr(), stream)
+    arrived = torch.cuda.Event()
+    arrived.record()
+    entries = torch.empty(max(capacity, 1), dtype=torch.int32, device=pos.device)
+    if capacity:
+        spec = (ctypes.c_uint32 * 4)(0, capacity, 0, 0)
+        _lib.call("dr_raster_visibility_bin", _lib.ref(geo.struct), _lib.ptr(workspace),
+                  size.value, _lib.ptr(entries), spec, stream)
+        _lib.call("dr_raster_visibility_tiles", _lib.ref(geo.struct), _lib.ptr(prev),
+                  _lib.ptr(keys), _lib.ptr(workspace), size.value, _lib.ptr(entries), spec,
+                  stream)
+    arrived.synchronize()
+    counts = (ctypes.c_uint32 * 4)(*[v & 0xFFFFFFFF for v in host.tolist()])
+    if counts[1] > capacity:
+        entries = torch.empty(counts[1], dtype=torch.int32, device=pos.device)
+        _lib.call("dr_raster_visibility_bin", _lib.ref(geo.struct), _lib.ptr(workspace),
+                  size.value, _lib.ptr(entries), counts, stream)
+        _lib.call("dr_raster_visibility_tiles", _lib.ref(geo.struct), _lib.ptr(prev),
+                  _lib.ptr(keys), _lib.ptr(workspace), size.value, _lib.ptr(entries), counts,
+                  stream)
+    torch.cuda.synchronize()
+    return keys, list(counts)
+
+
+def _keys_waiting(pos, tri, res, prev=None):
+    """Keys from dr_raster_visibility_begin (which waits for the counts), bin and tiles."""
+    import ctypes
+
+    from diffrast_amd.backends import _lib
+
+    geo = hip._Geometry(pos, tri, res)
+    keys = torch.empty(geo.shape, dtype=torch.int64, device=pos.device)
+    size = ctypes.c_size_t()
+    _lib.call("dr_raster_workspace_size", _lib.ref(geo.struct), ctypes.byref(size))
+    workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=pos.device)
+    counts = (ctypes.c_uint32 * 4)()
+    stream = _lib.stream(pos.device)
+    _lib.call("dr_raster_visibility_begin", _lib.ref(geo.struct), _lib.ptr(prev),
+              _lib.ptr(keys), _lib.ptr(workspace), size.value, counts, stream)
+    if counts[1]:
+        entries = torch.empty(counts[1], dtype=torch.int32, device=pos.device)
+        _lib.call("dr_raster_visibility_bin", _lib.ref(geo.struct), _lib.ptr(workspace),
+                  size.value, _lib.ptr(entries), counts, stream)
+        _lib.call("dr_raster_visibility_tiles", _lib.ref(geo.struct), _lib.ptr(prev),
+                  _lib.ptr(keys), _lib.ptr(workspace), size.value, _lib.ptr(entries), counts,
+                  stream)
+    torch.cuda.synchronize()
+    return keys, list(counts)
+
+
+@pytest.mark.parametrize("resolution", [(96, 80), (40, 24), (300, 17)])
+def test_visibility_with_entry_buffer_queued_before_the_counts(resolution):
+    # Binning and the tile pass queued with an entry buffer that is large enough, exactly large
+    # enough, one entry short or far too small must give the keys and counts of the calls that
+    # wait for the counts, for the first layer and for a peeled one.
+    pos, tri = mixed_mesh(torch.Generator().manual_seed(11), batch=3)
+    pos, tri = pos.cuda().contiguous(), tri.cuda().int().contiguous()
+    prev = None
+    for layer in range(2):
+        expected, counts = _keys_waiting(pos, tri, resolution, prev)
+        n = counts[1]
+        assert n > 0 and counts[2] > 0 and counts[0] > 0
+        for capacity in (0, n + 5000, n, n - 1, 1):
+            keys, got = _keys_through_abi(pos, tri, resolution, capacity, prev)
+            assert got == counts, (layer, capacity)
+            assert torch.equal(keys, expected), (layer, capacity)
+        prev = expected
+    ours = [hip.rasterize_layer(pos, tri, resolution, True, None)[0] for _ in range(3)]
+    assert torch.equal(ours[0], ours[1]) and torch.equal(ours[0], ours[2])
