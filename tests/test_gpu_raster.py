@@ -475,3 +475,24 @@ def test_visibility_with_entry_buffer_queued_before_the_counts(resolution):
         prev = expected
     ours = [hip.rasterize_layer(pos, tri, resolution, True, None)[0] for _ in range(3)]
     assert torch.equal(ours[0], ours[1]) and torch.equal(ours[0], ours[2])
+
+
+def test_entry_buffer_hint_outgrown_through_public_path():
+    # The same mesh shape drawn at a quarter of its size, then whole: the second call's tile
+    # lists outgrow the buffer sized from the first, are binned again into one that fits, and
+    # must still match the oracle; the third call (small again) runs in the buffer sized from
+    # the second.
+    gen = torch.Generator().manual_seed(5)
+    pos, tri = random_mesh(2000, gen, batch=2)
+    small = pos.clone()
+    small[..., :2] *= 0.25
+    res = (128, 128)
+    hip._ENTRY_HINTS.clear()
+    seen = []
+    for p in (small, pos, small):
+        assert_layers_match(p, tri, res, count=2)
+        first_layer = [v for k, v in hip._ENTRY_HINTS.items() if k[-1]]
+        assert len(first_layer) == 1
+        seen.append(first_layer[0])
+    assert seen[0] > 0 and seen[1] > hip._entry_capacity(seen[0]), seen
+    assert seen[2] == seen[0], seen
