@@ -36,6 +36,13 @@ FILTERS = {"nearest": 0, "linear": 1, "linear-mipmap-nearest": 2, "linear-mipmap
 BOUNDARIES = {"wrap": 0, "clamp": 1, "zero": 2, "cube": 3}
 
 
+def _require(name: str, t: Tensor | None, dtype: torch.dtype) -> None:
+    """The kernels read raw pointers: a tensor of another type would be reinterpreted, so it
+    is refused here (the reference backend module accepts only what its kernels compute in)."""
+    if t is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}.")
+
+
 def _dense(t: Tensor | None) -> Tensor | None:
     return None if t is None else t.contiguous()
 
@@ -88,6 +95,7 @@ class _Geometry:
 # size only when the lists outgrow it.
 _ENTRY_HINTS: dict[tuple, int] = {}
 _ENTRY_HINTS_KEPT = 64
+_hints_lock = threading.Lock()
 _host = threading.local()
 
 
@@ -120,7 +128,8 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
     host, arrived = _host_counts(device)
     hint_key = (device.index, geo.shape, geo.struct.num_tri, geo.struct.num_instances,
                 prev is None)
-    hint = _ENTRY_HINTS.get(hint_key, 0)
+    with _hints_lock:
+        hint = _ENTRY_HINTS.get(hint_key, 0)
     capacity = _entry_capacity(hint) if hint else 0
     counts = (ctypes.c_uint32 * 4)(0, capacity, 0, 0)
     call("dr_raster_visibility_start", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),
@@ -138,9 +147,10 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
         arrived.synchronize()  # the buffer is free again for the next call
     found = [v & 0xFFFFFFFF for v in host.tolist()]
     if found[1] or hint:
-        if len(_ENTRY_HINTS) >= _ENTRY_HINTS_KEPT and hint_key not in _ENTRY_HINTS:
-            _ENTRY_HINTS.pop(next(iter(_ENTRY_HINTS)))
-        _ENTRY_HINTS[hint_key] = found[1]
+        with _hints_lock:
+            if len(_ENTRY_HINTS) >= _ENTRY_HINTS_KEPT and hint_key not in _ENTRY_HINTS:
+                _ENTRY_HINTS.pop(next(iter(_ENTRY_HINTS)), None)
+            _ENTRY_HINTS[hint_key] = found[1]
     if found[1] > capacity:
         # the lists did not fit (or no size was known): bin again into a buffer that fits
         counts[:] = (0, 0, 0, 0)  # the calls above processed nothing
@@ -207,6 +217,9 @@ def rasterize_layer(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad_
                     previous: Tensor | None):
     """One depth layer behind ``previous`` (the keys returned for the layer before) and its
     keys (reference: triton.py:21-40, reference.py:45-66)."""
+    _require("pos", pos, torch.float32)
+    _require("tri", tri, torch.int32)
+    _require("previous", previous, torch.int64)
     if tri.shape[0] == 0 or pos.shape[0] == 0:
         return _empty_layer(pos, pos.shape[0], resolution)
     pos, tri = pos.contiguous(), tri.contiguous()
@@ -221,6 +234,9 @@ def rasterize_ranges(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad
     """Range mode in one launch: image i draws ``tri[start_i : start_i + count_i]`` of the
     shared ``pos`` ([vertices, 4]); ids count from the start of ``tri``, as after the
     reference's join_ranges (ops.py:490-508). Returns ``(rast, rast_db, keys)``."""
+    _require("pos", pos, torch.float32)
+    _require("tri", tri, torch.int32)
+    _require("previous", previous, torch.int64)
     table = [(int(s), int(c)) for s, c in ranges.tolist()]
     batch = len(table)
     if batch == 0 or tri.shape[0] == 0:
@@ -316,6 +332,9 @@ class _Interpolate(torch.autograd.Function):
 def interpolate(attr: Tensor, rast: Tensor, tri: Tensor, rast_db: Tensor | None,
                 diff_attrs: Sequence[int]):
     """(reference: triton.py:50-56)"""
+    for name, t in (("attr", attr), ("rast", rast), ("rast_db", rast_db)):
+        _require(name, t, torch.float32)
+    _require("tri", tri, torch.int32)
     return _Interpolate.apply(attr, rast, rast_db, tri, tuple(int(c) for c in diff_attrs))
 
 
@@ -462,6 +481,7 @@ def pack(levels: Sequence[Tensor]):
 def texture_construct_mip(tex: Tensor, max_mip_level: int | None) -> list[Tensor]:
     """Mip levels 1 and up of ``tex`` as views of one packed buffer, differentiable with
     respect to ``tex`` (reference.py:197-199)."""
+    _require("tex", tex, torch.float32)
     packed, (heights, widths, offsets) = _mip_chain(tex, max_mip_level)
     faces = 6 if tex.ndim == 5 else 1
     levels = []
@@ -476,6 +496,10 @@ def texture(tex: Tensor, uv: Tensor, uv_da: Tensor | None, filter_mode: str, bou
             max_mip_level: int | None, mip_level_bias: Tensor | None = None,
             mip: Sequence[Tensor] | None = None, packed=None):
     """(reference: triton.py:59-79, reference.py:149-194)"""
+    for name, t in (("tex", tex), ("uv", uv), ("uv_da", uv_da), ("mip_level_bias", mip_level_bias),
+                    *((f"mip[{k}]", m) for k, m in enumerate(mip or ())),
+                    ("packed texels", None if packed is None else packed[0])):
+        _require(name, t, torch.float32)
     mipmapped = "mipmap" in filter_mode
     if not mipmapped:
         faces = 6 if boundary_mode == "cube" else 1
@@ -504,6 +528,7 @@ def texture(tex: Tensor, uv: Tensor, uv_da: Tensor | None, filter_mode: str, bou
 def edge_neighbours(tri: Tensor) -> Tensor:
     """Partner of each edge, int32 [triangles, 3], -1 when unshared or non-manifold
     (reference.py:768-787), from a GPU hash table."""
+    _require("tri", tri, torch.int32)
     tri = tri.contiguous()
     out = torch.empty(tri.shape[0], 3, dtype=torch.int32, device=tri.device)
     if tri.shape[0] == 0:
@@ -579,6 +604,9 @@ class _Antialias(torch.autograd.Function):
 def antialias(color: Tensor, rast: Tensor, pos: Tensor, tri: Tensor, pos_gradient_boost: float,
               neighbours: Tensor | None = None) -> Tensor:
     """(reference: triton.py:82-92, reference.py:202-265)"""
+    for name, t in (("color", color), ("rast", rast), ("pos", pos)):
+        _require(name, t, torch.float32)
+    _require("tri", tri, torch.int32)
     if tri.shape[0] == 0:
         return color.clone()
     tri = tri.contiguous()

@@ -140,9 +140,7 @@ def test_texture_golden_fixture(filter_mode, boundary):
                            "cuda")
     assert rel_error(outs[0], g[f"{key}/out"]) < VALUE_TOL
     names = ("tex", "uv", "uv_da", "bias")
-    # Texel weights and coordinate gradients scale with the texture size: 1e-3 relative to
-    # the largest gradient covers float32 differences in the level-of-detail log2.
-    assert_grads_close(grads, [g[f"{key}/grad_{n}"] for n in names], tol=1e-3)
+    assert_grads_close(grads, [g[f"{key}/grad_{n}"] for n in names])
 
 
 @pytest.mark.parametrize("boundary", BOUNDARIES)
@@ -156,7 +154,7 @@ def test_texture_gradients(filter_mode, boundary):
     ours = grads_of(lambda t, c, d: hip.texture(t, c, d if mip else None, filter_mode, boundary,
                                                 None), [tex, uv, uv_da], [weights], "cuda")
     assert rel_error(ours[0][0], ref[0][0]) < VALUE_TOL
-    assert_grads_close(ours[1], ref[1], tol=1e-3)
+    assert_grads_close(ours[1], ref[1])
 
 
 @pytest.mark.parametrize("boundary", ["wrap", "clamp", "zero"])
@@ -185,7 +183,7 @@ def test_texture_gradients_smooth_mapping(filter_mode, boundary, channels):
     ours = grads_of(lambda t, c, d: hip.texture(t, c, d if mip else None, filter_mode,
                                                 boundary, None), [tex, uv, da], [weights], "cuda")
     assert rel_error(ours[0][0], ref[0][0]) < VALUE_TOL
-    assert_grads_close(ours[1][:1], ref[1][:1], tol=1e-3)
+    assert_grads_close(ours[1], ref[1])
 
 
 @pytest.mark.parametrize("pattern", ["constant", "magnified", "mixed"])
@@ -205,7 +203,7 @@ def test_texture_gradients_where_pixels_share_texels(filter_mode, pattern):
         fn(t, uv.to(device), uv_da.to(device) if mip else None, filter_mode, "clamp",
            None).sum().backward()
         grads.append(t.grad.cpu())
-    torch.testing.assert_close(grads[0], grads[1], atol=1e-3, rtol=1e-4)
+    assert_grads_close(grads[:1], grads[1:])
 
 
 @pytest.mark.parametrize("max_mip_level", [0, 2])
@@ -293,7 +291,7 @@ def test_cube_map_golden_fixture(filter_mode):
                            [g["cube/weights"]], "cuda")
     assert rel_error(outs[0], g[f"cube/{filter_mode}/out"]) < VALUE_TOL
     assert_grads_close(grads, [g[f"cube/{filter_mode}/grad_{n}"] for n in ("tex", "dirs",
-                                                                           "dirs_da")], tol=1e-3)
+                                                                           "dirs_da")])
 
 
 # ---- antialias -------------------------------------------------------------------------------
@@ -371,3 +369,22 @@ def test_topology_hash_through_public_api():
     a = dr.antialias(color.cuda(), rast.cuda(), pos.cuda(), tri_gpu, topology_hash=topo)
     b = dr.antialias(color.cuda(), rast.cuda(), pos.cuda(), tri_gpu)
     assert torch.equal(a, b)
+
+
+# ---- argument types at the backend boundary --------------------------------------------------
+
+
+def test_backend_refuses_types_its_kernels_do_not_compute_in():
+    attr, rast, db, tri = interp_scene(3, "shared")
+    with pytest.raises(TypeError, match="tri"):
+        hip.interpolate(attr.cuda(), rast.cuda(), tri.long().cuda(), None, [])
+    with pytest.raises(TypeError, match="attr"):
+        hip.interpolate(attr.half().cuda(), rast.cuda(), tri.cuda(), None, [])
+    pos, tri2 = random_mesh(4, torch.Generator().manual_seed(0))
+    with pytest.raises(TypeError, match="tri"):
+        hip.rasterize(pos.cuda(), tri2.long().cuda(), (8, 8), True)
+    with pytest.raises(TypeError, match="pos"):
+        hip.rasterize(pos.half().cuda(), tri2.cuda(), (8, 8), True)
+    tex, uv, uv_da = tex_scene()
+    with pytest.raises(TypeError, match="uv"):
+        hip.texture(tex.cuda(), uv.half().cuda(), None, "linear", "wrap", None)
