@@ -65,29 +65,21 @@ SINGLE_KERNEL = {
 
 
 class KernelTimer:
-    """HIP events around the backend's C-ABI calls, on the current stream, and the algorithmic
-    bytes of each call."""
+    """HIP events around the backend's C-ABI calls, on the current stream, with the algorithmic
+    bytes of each call: its kernel's own (``kernel_bytes``) and its share of its op's
+    (``op_bytes``)."""
 
-    def __init__(self, bytes_of):
-        self.events = defaultdict(list)
-        self.bytes = defaultdict(float)
-        self.pending = defaultdict(list)
-        self.bytes_of = bytes_of
+    def __init__(self, model):
+        self.model = model
         self.active = False
         self.only = None  # entry point names to time (None: every one)
         self._call = hip.call
+        self.reset()
 
     def reset(self):
         self.events = defaultdict(list)
         self.bytes = defaultdict(float)
-        self.pending = defaultdict(list)
-
-    def resolve(self):
-        """Bytes of the timed calls; a model may return a function of counts that are known
-        only after the call (the tile pass queued before its list sizes arrive)."""
-        for name, amounts in self.pending.items():
-            self.bytes[name] += sum(a() if callable(a) else a for a in amounts)
-        self.pending = defaultdict(list)
+        self.op_bytes = defaultdict(float)
 
     def install(self):
         def timed(name, *args):
@@ -99,9 +91,8 @@ class KernelTimer:
             self._call(name, *args)
             end.record()
             self.events[name].append((start, end))
-            amount = self.bytes_of(name, args)
-            if amount is not None:
-                self.pending[name].append(amount)
+            self.bytes[name] += self.model.kernel_bytes(name, args)
+            self.op_bytes[name] += self.model.op_bytes(name, args)
 
         hip.call = timed
 
@@ -110,7 +101,6 @@ class KernelTimer:
 
     def summary(self):
         torch.cuda.synchronize()
-        self.resolve()
         out = {}
         for name, pairs in self.events.items():
             times = [s.elapsed_time(e) for s, e in pairs]
@@ -118,135 +108,147 @@ class KernelTimer:
         return out
 
 
-# Tile rasterization, per tile list entry: the entry (4 B) and the 64-byte record it names
-# (three clip-space vertices, triangle row, tile rectangle); per tile with entries: its 256
-# keys read and written once (16 B each).
-TILE_ENTRY_BYTES = 4 + 64
-TILE_KEY_BYTES = 256 * 16
-
-
 def _struct(arg):
     """The ctypes structure a byref() argument points to."""
     return arg._obj
 
 
+# Which of the four ops each C-ABI entry point belongs to (its event time counts there).
+OP_OF = {
+    "dr_raster_visibility_begin": "rasterize",
+    "dr_raster_visibility_start": "rasterize",
+    "dr_raster_visibility_bin": "rasterize",
+    "dr_raster_visibility_tiles": "rasterize",
+    "dr_resolve_forward": "rasterize",
+    "dr_resolve_backward": "rasterize",
+    "dr_interpolate_forward": "interpolate",
+    "dr_interpolate_backward": "interpolate",
+    "dr_texture_forward": "texture",
+    "dr_texture_backward": "texture",
+    "dr_mip_build": "texture",
+    "dr_mip_build_backward": "texture",
+    "dr_edge_neighbours": "antialias",
+    "dr_silhouette_mask": "antialias",
+    "dr_antialias_forward": "antialias",
+    "dr_antialias_backward": "antialias",
+}
+
+
 class BytesModel:
-    """Algorithmic bytes of each C-ABI call: the unique bytes its algorithm must move (inputs
-    read once, outputs written once, fp32 = 4 B), from the call's own arguments and the
-    workload's mesh sizes. Gathered arrays (pos, tri, attributes, texels) count whole."""
+    """Algorithmic bytes: the unique-byte model -- every input tensor read once and every output
+    written once, 4 B per fp32 value, 12 B per triangle of ``tri``, 24 B per triangle of int64
+    edge neighbours, gathered arrays (pos, tri, attributes, texels) counted whole -- from each
+    call's own arguments and the workload's mesh sizes. With P pixels, Pb images of ``pos``, V
+    vertices, T triangles, C channels, D derivative channels, L texels of the packed mip chain
+    and N0 of its base level, the op formulas are
+
+        rasterize fwd    Pb V 16 + T 12 + P 16 (1 + [rast_db])
+        rasterize bwd    P 16 (1 + [rast_db]) + P 8 (keys) + 2 Pb V 16 + T 12
+        interpolate fwd  P 16 (1 + [D>0]) + T 12 + V C 4 + P C 4 + P 2D 4
+        interpolate bwd  P C 4 + P 2D 4 + 2 P 16 (1 + [D>0]) + T 12 + 2 V C 4
+        texture fwd      L C 4 + P (coords + derivatives) 4 + P C 4 + mip build L C 4
+        texture bwd      P C 4 + 2 P (coords + derivatives) 4 + 2 L C 4 + mip adjoint L C 4
+        antialias fwd    2 P C 4 + P 16 + Pb V 16 + T 12 + T 24
+        antialias bwd    3 P C 4 + P 16 + 2 Pb V 16 + T 12 + T 24
+
+    (coordinates: 2 and 4 derivative values per pixel for a 2D texture, 3 and 6 for a cube
+    map; a per-pixel mip level bias adds P 4). ``op_bytes`` gives each entry point's share of
+    its op (the visibility passes carry none: rasterize's bytes sit on the resolve calls).
+    ``kernel_bytes`` gives the unique bytes of the work a single-kernel entry point does, for
+    the per-kernel roofline: the tile pass of the visibility is credited with the whole
+    visibility's unique bytes (pos and tri read, the keys written, the previous layer's keys
+    read when peeling), since its setup and binning passes move only intermediate data."""
 
     def __init__(self, w):
         pos = w.tensors["pos"]
         self.vertices = pos.shape[-2]
-        self.pos_images = pos.shape[0] if pos.ndim == 3 else 1
         self.tri = w.tensors["tri"].shape[0]
 
-    def pos_bytes(self, images):
+    def pos_bytes(self, g_or_a) -> int:
+        images = g_or_a.batch if g_or_a.pos_batch_stride else 1
         return images * self.vertices * 16
 
-    def __call__(self, name, args):
-        model = getattr(self, name[3:], None)
-        return None if model is None else model(args)
-
     @staticmethod
-    def _pixels(g):
-        return g.batch * g.height * g.width
+    def _pixels(a):
+        return a.batch * a.height * a.width
 
-    def raster_visibility_start(self, args):
+    def op_bytes(self, name, args):
+        model = getattr(self, "op_" + name[3:], None)
+        return 0 if model is None else model(args)
+
+    def kernel_bytes(self, name, args):
+        if name == "dr_raster_visibility_tiles":
+            g = _struct(args[0])
+            P = self._pixels(g)
+            return self.pos_bytes(g) + self.tri * 12 + P * 8 * (2 if args[1] else 1)
+        return self.op_bytes(name, args)
+
+    def op_resolve_forward(self, args):
         g = _struct(args[0])
-        return self.pos_bytes(self.pos_images) + self.tri * 12 + self._pixels(g) * 8
+        P = self._pixels(g)
+        return self.pos_bytes(g) + self.tri * 12 + P * 16 * (2 if args[3] else 1)
 
-    def raster_visibility_tiles(self, args):
-        # The counts array holds the list sizes once the caller has them (after the call when
-        # the pass was queued before they arrived).
-        counts = args[6]
-        return lambda: counts[1] * TILE_ENTRY_BYTES + counts[3] * TILE_KEY_BYTES
-
-    def resolve_forward(self, args):
-        P = self._pixels(_struct(args[0]))
-        return (P * 8 + self.pos_bytes(self.pos_images) + self.tri * 12
-                + P * 16 * (2 if args[3] else 1))
-
-    def resolve_backward(self, args):
-        P = self._pixels(_struct(args[0]))
-        return (P * 8 + P * 16 * (2 if args[3] else 1) + 2 * self.pos_bytes(self.pos_images)
-                + self.tri * 12)
-
-    def interpolate_forward(self, args):
-        a = _struct(args[0])
-        P, ch, nd = a.batch * a.height * a.width, a.channels, a.num_diff
-        images = a.batch if a.attr_batch_stride else 1
-        return (P * 16 * (2 if nd else 1) + self.tri * 12 + images * a.num_vertices * ch * 4
-                + P * ch * 4 + P * 2 * nd * 4)
-
-    def interpolate_backward(self, args):
-        a = _struct(args[0])
-        P, ch, nd = a.batch * a.height * a.width, a.channels, a.num_diff
-        images = a.batch if a.attr_batch_stride else 1
-        return (P * ch * 4 + P * 2 * nd * 4 + P * 16 * (2 if nd else 1) + self.tri * 12
-                + 2 * images * a.num_vertices * ch * 4 + P * 16 * (2 if nd else 1))
+    def op_resolve_backward(self, args):
+        g = _struct(args[0])
+        P = self._pixels(g)
+        return P * 16 * (2 if args[3] else 1) + P * 8 + 2 * self.pos_bytes(g) + self.tri * 12
 
     @staticmethod
-    def _texture_io(a):
+    def _interp(a):
+        P, C, D = a.batch * a.height * a.width, a.channels, a.num_diff
+        attr = (a.batch if a.attr_batch_stride else 1) * a.num_vertices * C * 4
+        return P, C, D, attr, P * 16 * (2 if D else 1)
+
+    def op_interpolate_forward(self, args):
+        P, C, D, attr, rast = self._interp(_struct(args[0]))
+        return rast + self.tri * 12 + attr + P * C * 4 + P * 2 * D * 4
+
+    def op_interpolate_backward(self, args):
+        P, C, D, attr, rast = self._interp(_struct(args[0]))
+        return P * C * 4 + P * 2 * D * 4 + 2 * rast + self.tri * 12 + 2 * attr
+
+    @staticmethod
+    def _texture(a):
         P, C = a.batch * a.height * a.width, a.channels
         cube = a.boundary == hip.BOUNDARIES["cube"]
         coords = P * (12 if cube else 8) + (P * (24 if cube else 16) if a.uv_da else 0)
-        return P, C, coords + (P * 4 if a.bias else 0), a.tex_batch * a.num_texels * C * 4
+        coords += P * 4 if a.bias else 0
+        return P, C, coords, a.tex_batch * a.num_texels * C * 4
 
-    def texture_forward(self, args):
-        P, C, coords, texels = self._texture_io(_struct(args[0]))
+    def op_texture_forward(self, args):
+        P, C, coords, texels = self._texture(_struct(args[0]))
         return texels + coords + P * C * 4
 
-    def texture_backward(self, args):
-        P, C, coords, texels = self._texture_io(_struct(args[0]))
+    def op_texture_backward(self, args):
+        P, C, coords, texels = self._texture(_struct(args[0]))
         return P * C * 4 + 2 * coords + 2 * texels
 
     @staticmethod
     def _mip(args):
-        tex_batch, channels, total, faces = args[1], args[2], args[3], args[4]
-        base = faces * args[6][0] * args[7][0]
-        return tex_batch * channels * 4 * (2 * total - base)
+        tex_batch, channels, total = args[1], args[2], args[3]
+        return tex_batch * total * channels * 4  # base read + levels written, or the adjoint
 
-    def mip_build(self, args):
+    def op_mip_build(self, args):
         return self._mip(args)
 
-    def mip_build_backward(self, args):
+    def op_mip_build_backward(self, args):
         return self._mip(args)
 
-    def silhouette_mask(self, args):
-        pos_batch, num_tri, batch, height, width = args[2], args[4], args[7], args[8], args[9]
-        P = batch * height * width if args[6] else 0
-        return P * 16 + 2 * pos_batch * num_tri + self.pos_bytes(pos_batch) + num_tri * 24
-
-    def antialias_forward(self, args):
+    def _aa(self, args):
         a = _struct(args[0])
-        P, C = a.batch * a.height * a.width, a.channels
-        images = a.batch if a.pos_batch_stride else 1
-        return (2 * P * C * 4 + P * 16 + self.pos_bytes(images) + a.num_tri * 12
-                + images * a.num_tri + P * 10)
+        P, C = self._pixels(a), a.channels
+        return P, C, self.pos_bytes(a), a.num_tri
 
-    def antialias_backward(self, args):
-        a = _struct(args[0])
-        P, C = a.batch * a.height * a.width, a.channels
-        images = a.batch if a.pos_batch_stride else 1
-        return (3 * P * C * 4 + P * 16 + P * 10 + 2 * self.pos_bytes(images)
-                + a.num_tri * 12 + images * a.num_tri)
+    def op_antialias_forward(self, args):
+        P, C, pos, T = self._aa(args)
+        return 2 * P * C * 4 + P * 16 + pos + T * 12 + T * 24
+
+    def op_antialias_backward(self, args):
+        P, C, pos, T = self._aa(args)
+        return 3 * P * C * 4 + P * 16 + 2 * pos + T * 12 + T * 24
 
 
 # ---- the five workloads' steps ----------------------------------------------------------------
-
-def reflect(view, n, n_da):
-    """Reflection of the view rays about the interpolated normals, and its screen-space
-    derivatives from those of the normals (the rays' own derivatives are left out)."""
-    d = (view * n).sum(-1, keepdim=True)
-    dirs = view - 2 * d * n
-    parts = []
-    for axis in (0, 1):
-        dn = n_da[..., axis::2]
-        dd = (view * dn).sum(-1, keepdim=True)
-        parts.append(-2 * (dd * n + d * dn))
-    return dirs, torch.stack(parts, -1).reshape(*dirs.shape[:-1], 6)
-
 
 def _mse(x, target):
     return torch.nn.functional.mse_loss(x, target)
@@ -297,7 +299,7 @@ def make_step(w, device):
             mip = dr.texture_construct_mip(tex)
             col = dr.texture(tex, uv, uv_da, mip=mip, filter_mode="linear-mipmap-linear",
                              boundary_mode="wrap")
-            return _mse(col, target)
+            return _mse(dr.antialias(col, rast, pos, tri), target)
     elif w.name == "large":
         pos, feat, tex = leaf("pos"), leaf("feat"), leaf("tex")
         tri, uv_attr, target = t["tri"], t["uv"], t["target"]
@@ -312,15 +314,16 @@ def make_step(w, device):
             return _mse(dr.antialias(shaded, rast, pos, tri), target)
     elif w.name == "cubemap":
         pos, cube = leaf("pos"), leaf("cube")
-        tri, normals, view, target = t["tri"], t["normals"], t["view"], t["target"]
+        tri, normals, target = t["tri"], t["normals"], t["target"]
+        view, view_da = t["view"], t["view_da"]
 
         def body():
             rast, rast_db = dr.rasterize(ctx, pos, tri, res)
             n, n_da = dr.interpolate(normals, rast, tri, rast_db, diff_attrs="all")
-            dirs, dirs_da = reflect(view, n, n_da)
+            dirs, dirs_da = workloads.reflect(view, view_da, n, n_da)
             col = dr.texture(cube, dirs, dirs_da, filter_mode="linear-mipmap-linear",
                              boundary_mode="cube")
-            return _mse(col, target)
+            return _mse(dr.antialias(col, rast, pos, tri), target)
     elif w.name == "instances":
         pos, color = leaf("pos"), leaf("color")
         tri, ranges = t["tri"], t["ranges"]
@@ -399,7 +402,7 @@ def cpu_baseline(w, sample_tris: int, ids) -> dict:
         rast, rast_db = R.rasterize_from_ids(p, tri, ids, True)
         uv, uv_da = R.interpolate(t["uv"], rast, tri, rast_db, [0, 1])
         col = R.texture(tex, uv, uv_da, "linear-mipmap-linear", "wrap", None)
-        _mse(col, t["target"][:1]).backward()
+        _mse(R.antialias(col, rast, p, tri), t["target"][:1]).backward()
     elif w.name == "large":
         feat = t["feat"].clone().requires_grad_(True)
         tex = t["tex"].clone().requires_grad_(True)
@@ -413,9 +416,9 @@ def cpu_baseline(w, sample_tris: int, ids) -> dict:
         cube = t["cube"].clone().requires_grad_(True)
         rast, rast_db = R.rasterize_from_ids(p, tri, ids, True)
         n, n_da = R.interpolate(t["normals"], rast, tri, rast_db, [0, 1, 2])
-        dirs, dirs_da = reflect(t["view"][:1], n, n_da)
+        dirs, dirs_da = workloads.reflect(t["view"][:1], t["view_da"][:1], n, n_da)
         col = R.texture(cube, dirs, dirs_da, "linear-mipmap-linear", "cube", None)
-        _mse(col, t["target"][:1]).backward()
+        _mse(R.antialias(col, rast, p, tri), t["target"][:1]).backward()
     elif w.name == "instances":
         color = t["color"][:1].clone().requires_grad_(True)
         rast, _ = R.rasterize_from_ids(p, tri, ids, False)
@@ -427,6 +430,7 @@ def cpu_baseline(w, sample_tris: int, ids) -> dict:
         "value": round(total_ms, 1),
         "unit": "ms",
         "cores": torch.get_num_threads(),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": (f"one {what} of {B} at {H}x{W}: reference brute-force visibility over "
                    f"{sample} of its {T} triangles ({vis_s:.1f} s), x{layers} layer(s), and the "
@@ -453,29 +457,46 @@ def profiled_traffic(kernel: str, workload: str) -> dict | None:
         path.relative_to(ROOT))}
 
 
-# fp32 vector issue peak of the MI355X in lane operations per second: 256 CUs x 4 SIMDs x 32
-# lanes x 2.4 GHz (the published 157.3 TFLOP/s counts a fused multiply-add as two operations).
-VALU_PEAK = 256 * 4 * 32 * 2.4e9
+# Vector issue of the MI355X: 256 CUs x 4 SIMDs, each issuing one wave64 VALU instruction
+# (64 lanes over a 16-lane SIMD) every 4 clocks without packed fp32, which this build does not
+# use; at 2.4 GHz that is 614 G wave instructions/s (39.3 T lane operations/s; with fused
+# multiply-adds counted twice and packed fp32, the published 157.3 TFLOP/s).
+SIMDS = 256 * 4
+CLOCK_HZ = 2.4e9
+VALU_ISSUE_PEAK = SIMDS * CLOCK_HZ / 4  # wave64 VALU instructions per second
+
+
+def _profile_fields(path: Path) -> dict:
+    fields = {}
+    for line in path.read_text().splitlines():
+        key, sep, value = line.partition(":")
+        if sep:
+            try:
+                fields[key.strip()] = float(value)
+            except ValueError:
+                pass
+    return fields
 
 
 def profiled_valu(kernel: str, workload: str, mean_ms: float) -> dict | None:
-    """VALU utilisation of ``kernel``: its vector instructions per launch (SQ_INSTS_VALU, wave64
-    instructions, from its committed rocprofv3 counter summary) times 64 lanes, over its mean
-    duration, against VALU_PEAK."""
+    """Vector issue of ``kernel`` from its committed rocprofv3 counter summary: wave64 VALU
+    instructions per launch (SQ_INSTS_VALU) over the live mean duration, against the issue
+    peak, and the VALU-busy fraction that the summary derives from SQ_ACTIVE_INST_VALU (its
+    header states how)."""
     path = ROOT / "profiles" / f"{kernel}.{workload}.valu.txt"
     if not path.exists():
         return None
-    n = None
-    for line in path.read_text().splitlines():
-        key, sep, value = line.partition(":")
-        if sep and key.strip() == "valu_instructions":
-            n = float(value)
-    if n is None:
+    f = _profile_fields(path)
+    if "valu_instructions" not in f:
         return None
-    ops = n * 64 / (mean_ms * 1e-3)
-    return {"instructions": int(n), "achieved": round(ops / 1e12, 2), "peak": VALU_PEAK / 1e12,
-            "unit": "T lane-ops/s", "frac": round(ops / VALU_PEAK, 4),
-            "source": str(path.relative_to(ROOT))}
+    rate = f["valu_instructions"] / (mean_ms * 1e-3)
+    out = {"instructions": int(f["valu_instructions"]),
+           "issue_rate": round(rate / 1e9, 1), "issue_peak": round(VALU_ISSUE_PEAK / 1e9, 1),
+           "unit": "G wave64 instructions/s", "issue_frac": round(rate / VALU_ISSUE_PEAK, 4)}
+    if "valu_busy" in f:
+        out["busy_frac"] = round(f["valu_busy"], 4)
+    out["source"] = str(path.relative_to(ROOT))
+    return out
 
 
 def copy_probe(mib: int, device) -> None:
@@ -497,42 +518,51 @@ WORKLOADS = {
               "rasterize + interpolate + antialias, MSE, grads to pos/colours",
     "textured": "icosphere(5) (20,480 triangles), 4 views at 512x512, spherical uv with "
                 "derivatives, 512x512x3 texture with mips from texture_construct_mip, trilinear "
-                "wrap, MSE, grads to pos/texture",
+                "wrap, antialias, MSE, grads to pos/texture",
     "large": "icosphere(8) radially perturbed, 1,310,720 triangles, 8 views x 1024x1024, "
              "features [1,V,8] + uv with derivatives, 1024x1024x4 texture with a full mip chain "
              "per call, trilinear wrap, antialias, MSE, grads to pos/feat/tex",
     "cubemap": "(2,3) torus knot 512x32 (32,768 triangles), 4 views at 1024x1024, reflected "
-               "view rays from interpolated normals with derivatives, 6x512x512x3 cube map, "
-               "trilinear, MSE, grads to pos/cube map",
+               "view rays from interpolated normals, derivatives by the chain rule through rays "
+               "and normals, 6x512x512x3 cube map, trilinear, antialias, MSE, grads to "
+               "pos/cube map",
     "instances": "256 icosphere(4) instances (1,310,720 triangles) in range mode at 512x512, "
                  "depth peeling to 4 layers, antialias of layer 0, MSE, grads to pos/colours",
 }
 
 
-def dominant_entry(per_kernel: dict, timed_bytes: dict) -> str:
+def dominant_entry(per_kernel: dict) -> str:
     """The longest-running entry point that launches a single kernel (so that its event time is
-    that kernel's time) and has a byte model."""
-    return max((n for n in per_kernel if n in SINGLE_KERNEL and n in timed_bytes),
-               key=lambda n: per_kernel[n][0])
+    that kernel's time)."""
+    return max((n for n in per_kernel if n in SINGLE_KERNEL), key=lambda n: per_kernel[n][0])
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int) -> dict:
     """Warm-up steps (timed per entry point after the first, to find the dominant kernel), then
     exactly `steps` timed steps in which only the dominant entry point carries HIP events (the
     roofline's live launch time; events around every call would add ~0.13 ms per step), then a
-    few more steps with every entry point timed, for the per-kernel table."""
+    few more steps with every entry point timed, for the per-kernel and per-op tables."""
     w = workloads.build(name)
     step = make_step(w, device)
-    timer = KernelTimer(BytesModel(w))
+    model = BytesModel(w)
+    timer = KernelTimer(model)
     timer.install()
     for i in range(warmup):
         timer.active = i > 0 or warmup == 1
         step()
     timer.active = False
     torch.cuda.synchronize()
-    dominant = None
-    if timer.events:
-        dominant = dominant_entry(timer.summary(), timer.bytes)
+    dominant = dominant_entry(timer.summary()) if timer.events else None
     timer.reset()
     timer.only = None if dominant is None else {dominant}
 
@@ -547,12 +577,12 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int)
     ms_per_step = elapsed * 1e3 / steps
     live = timer.summary()
     if dominant is None:  # no warm-up: every entry point was timed in the timed steps
-        dominant = dominant_entry(live, timer.bytes)
+        dominant = dominant_entry(live)
     dom_total, dom_count = live[dominant]
     dom_ms = dom_total / dom_count
     dom_bytes = timer.bytes[dominant] / dom_count
 
-    # The per-kernel table, from its own steps after the timed ones.
+    # The per-kernel and per-op tables, from their own steps after the timed ones.
     table_steps = min(steps, 5)
     timer.reset()
     timer.only = None
@@ -564,15 +594,29 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int)
     timer.uninstall()
     per_kernel = timer.summary()
     kernels = {}
+    op_ms, op_bytes = defaultdict(float), defaultdict(float)
     for kname, (total_ms, count) in per_kernel.items():
         mean_ms = total_ms / count
         entry = {"ms_per_step": round(total_ms / table_steps, 4), "launches_per_step":
-                 count // table_steps, "mean_launch_ms": round(mean_ms, 4)}
-        if kname in timer.bytes:
+                 round(count / table_steps, 2), "mean_launch_ms": round(mean_ms, 4)}
+        if timer.bytes[kname]:
             gbs = timer.bytes[kname] / count / (mean_ms * 1e-3) / 1e9
             entry["GB/s"] = round(gbs, 1)
             entry["frac"] = round(gbs * 1e9 / HBM_PEAK, 4)
         kernels[kname] = entry
+        op = OP_OF.get(kname)
+        if op is not None:
+            op_ms[op] += total_ms / table_steps
+            op_bytes[op] += timer.op_bytes[kname] / table_steps
+    ops = {}
+    for op in ("rasterize", "interpolate", "texture", "antialias"):
+        if op not in op_ms:
+            continue
+        floor_ms = op_bytes[op] / HBM_PEAK * 1e3
+        ops[op] = {"ms": round(op_ms[op], 4), "bytes": int(op_bytes[op]),
+                   "roofline_ms": round(floor_ms, 4), "frac": round(floor_ms / op_ms[op], 4)}
+    step_bytes = sum(op_bytes.values())
+    step_floor_ms = step_bytes / HBM_PEAK * 1e3
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     traffic = profiled_traffic(SINGLE_KERNEL[dominant], name)
 
@@ -615,6 +659,12 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int)
             "mean_launch_ms": round(dom_ms, 4),
             # The rasterizer's own bound: vector issue (no HBM stream limits it).
             "valu": profiled_valu(SINGLE_KERNEL[dominant], name, dom_ms),
+            # Each op's forward+backward against the HBM time of its unique bytes, and the
+            # whole step (the ops' bytes; the glue between them is timed but not credited).
+            "ops": ops,
+            "step": {"bytes": int(step_bytes), "roofline_ms": round(step_floor_ms, 4),
+                     "frac": round(step_floor_ms / ms_per_step, 4),
+                     "ops_ms": round(sum(op_ms.values()), 4)},
         },
         "cpu_baseline": baseline,
         "kernels": kernels,

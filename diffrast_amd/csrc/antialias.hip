@@ -188,7 +188,14 @@ __device__ __forceinline__ void silhouette_bits(const float* pos, int64_t stride
     }
     const XYW& s = p[(k + 1) % 3];
     const XYW& e = p[(k + 2) % 3];
-    const float line[3] = {s.y * e.w - s.w * e.y, s.w * e.x - s.x * e.w, s.x * e.y - s.y * e.x};
+    // The reference takes this cross product with torch.linalg.cross, whose CPU kernel rounds
+    // each component as one fused multiply-add of the first product with the rounded second
+    // (u_i v_j - u_j v_i = fma(u_i, v_j, -(u_j v_i)); checked bit for bit on a million random
+    // float32 triples). A fold is classified by the sign of what follows, so near-degenerate
+    // (edge-on) triangles at a silhouette need the same rounding.
+    const float line[3] = {__builtin_fmaf(s.y, e.w, -(s.w * e.y)),
+                           __builtin_fmaf(s.w, e.x, -(s.x * e.w)),
+                           __builtin_fmaf(s.x, e.y, -(s.y * e.x))};
     const XYW theirs = load_xyw(P, tri[partner[k]]);  // vertex opposite the partner edge
     if (side(line, p[k]) * side(line, theirs) > 0.0f) bits |= (uint8_t)(1u << k);
   }

@@ -17,7 +17,9 @@ Workloads (per-image resolution, images per batch):
   chain built per call, trilinear lookup, antialias on the shaded colour, MSE; gradients to
   positions, features and texture.
 * ``cubemap``  -- (2, 3) torus knot, 512 x 32 tube segments (32,768 triangles), 4 x 1024x1024,
-  reflection vectors from interpolated normals into a 6x512x512x3 cube map.
+  reflection vectors (and their derivatives, by the chain rule through the view rays and the
+  interpolated normals) into a 6x512x512x3 cube map, antialias, MSE; gradients to the cube
+  map and positions.
 * ``instances`` -- 256 icosphere(4) instances (1,310,720 triangles) in range mode, 512x512,
   four depth layers, then antialias on layer 0.
 """
@@ -176,6 +178,42 @@ def clip_positions(verts: Tensor, eyes: Tensor, aspect: float) -> Tensor:
     return (homogeneous @ matrix.transpose(-1, -2)).contiguous()
 
 
+def view_rays(eyes: Tensor, h: int, w: int) -> tuple[Tensor, Tensor]:
+    """Unit world-space view rays through the pixel centres of each camera [batch, h, w, 3] and
+    their derivatives per pixel step [batch, h, w, 6], laid out like interpolate's ``out_da``
+    ((d/dx, d/dy) of each component in turn). The derivatives are exact (forward-mode
+    differentiation of the ray through the inverse view-projection, one pixel = 2 / size in
+    NDC)."""
+    inv = torch.linalg.inv(perspective(45.0, w / h) @ look_at(eyes)).double()
+    xs = (torch.arange(w, dtype=torch.float64) * 2 + 1) / w - 1
+    ys = (torch.arange(h, dtype=torch.float64) * 2 + 1) / h - 1
+    gy, gx = (g.contiguous() for g in torch.meshgrid(ys, xs, indexing="ij"))
+
+    def ray(x, y):
+        ndc = torch.stack([x, y, torch.ones_like(x), torch.ones_like(x)], -1)
+        far = torch.einsum("bij,hwj->bhwi", inv, ndc)
+        return F.normalize(far[..., :3] / far[..., 3:] - eyes.double()[:, None, None], dim=-1)
+
+    view, dx = torch.func.jvp(lambda x: ray(x, gy), (gx,), (torch.full_like(gx, 2.0 / w),))
+    _, dy = torch.func.jvp(lambda y: ray(gx, y), (gy,), (torch.full_like(gy, 2.0 / h),))
+    view_da = torch.stack([dx, dy], -1).reshape(*view.shape[:-1], 6)
+    return view.float().contiguous(), view_da.float().contiguous()
+
+
+def reflect(view: Tensor, view_da: Tensor, n: Tensor, n_da: Tensor) -> tuple[Tensor, Tensor]:
+    """Reflection r = v - 2 (n . v) n of the view rays about the interpolated normals, and its
+    screen-space derivatives by the chain rule from those of both the rays and the normals
+    (layouts of interpolate's ``out_da``: (d/dx, d/dy) per component)."""
+    d = (view * n).sum(-1, keepdim=True)
+    dirs = view - 2 * d * n
+    parts = []
+    for axis in (0, 1):
+        dv, dn = view_da[..., axis::2], n_da[..., axis::2]
+        dd = (dv * n).sum(-1, keepdim=True) + (view * dn).sum(-1, keepdim=True)
+        parts.append(dv - 2 * (dd * n + d * dn))
+    return dirs, torch.stack(parts, -1).reshape(*dirs.shape[:-1], 6)
+
+
 # ---------------------------------------------------------------------------------------------
 # Workloads
 # ---------------------------------------------------------------------------------------------
@@ -246,17 +284,10 @@ def _cubemap(scale):
     pos = clip_positions(verts, eyes, w / h)
     cube = torch.rand(1, 6, 512 // scale, 512 // scale, 3, generator=gen)
     target = torch.rand(4, h, w, 3, generator=gen)
-    # Per-pixel view rays in world space, from the inverse view-projection.
-    inv = torch.linalg.inv(perspective(45.0, w / h) @ look_at(eyes))
-    xs = (torch.arange(w, dtype=torch.float32) * 2 + 1) / w - 1
-    ys = (torch.arange(h, dtype=torch.float32) * 2 + 1) / h - 1
-    gy, gx = torch.meshgrid(ys, xs, indexing="ij")
-    ndc = torch.stack([gx, gy, torch.ones_like(gx), torch.ones_like(gx)], -1)
-    far = torch.einsum("bij,hwj->bhwi", inv, ndc)
-    view = F.normalize(far[..., :3] / far[..., 3:] - eyes[:, None, None], dim=-1)
+    view, view_da = view_rays(eyes, h, w)
     return Workload("cubemap", 4, (h, w), {"pos": pos, "tri": tri,
                                            "normals": vertex_normals(verts, tri)[None],
-                                           "view": view.contiguous(), "cube": cube,
+                                           "view": view, "view_da": view_da, "cube": cube,
                                            "target": target})
 
 

@@ -9,11 +9,13 @@ stated tolerance (interpolate bit-exact). Gradients are checked at the small siz
 test files.
 """
 
+import contextlib
+import math
+
 import pytest
 import torch
 
 import diffrast_amd as dr
-from bench import reflect
 from diffrast_amd import workloads
 from helpers import rel_error
 from oracle import reference as R
@@ -157,7 +159,7 @@ def test_cubemap_workload_at_sampled_pixels():
     rast, rast_db = dr.rasterize(dr.RasterizeContext(dev), t["pos"].to(dev), tri.to(dev),
                                  w.resolution)
     n, n_da = dr.interpolate(t["normals"].to(dev), rast, tri.to(dev), rast_db, diff_attrs="all")
-    dirs, dirs_da = reflect(t["view"].to(dev), n, n_da)
+    dirs, dirs_da = workloads.reflect(t["view"].to(dev), t["view_da"].to(dev), n, n_da)
     col = dr.texture(t["cube"].to(dev), dirs, dirs_da, filter_mode="linear-mipmap-linear",
                      boundary_mode="cube")
     rast, rast_db, n, n_da, dirs, dirs_da, col = (
@@ -173,8 +175,8 @@ def test_cubemap_workload_at_sampled_pixels():
 
 
 def test_instances_workload_layers_at_sampled_pixels():
-    # Range mode with depth peeling: item i draws triangles [start, start + count); every
-    # layer must match the oracle's peel of that item alone.
+    # Range mode with depth peeling: item i draws triangles [start, start + count); each of
+    # the four layers must match the oracle's peel of that item alone.
     w = workloads.build("instances")
     t = w.tensors
     dev = torch.device("cuda", 0)
@@ -182,7 +184,7 @@ def test_instances_workload_layers_at_sampled_pixels():
     layers = []
     with dr.DepthPeeler(dr.RasterizeContext(dev), pos.to(dev), tri.to(dev), w.resolution,
                         ranges=ranges) as peeler:
-        for _ in range(3):
+        for _ in range(4):
             layers.append(peeler.rasterize_next_layer()[0].cpu())
     gen = torch.Generator().manual_seed(33)
     for item in (0, 97, 255):
@@ -200,3 +202,185 @@ def test_instances_workload_layers_at_sampled_pixels():
             depth, ids = R.visible_at(pos[None], own, *w.resolution, b, row, col, previous)
             assert torch.equal(gpu_ids[b, row, col], torch.where(ids >= 0, ids + start, ids))
             previous = (depth, ids)
+
+
+# ---- one view of each textured workload, forward and backward in full ------------------------
+
+
+class _Gpu:
+    """The public API on the GPU."""
+
+    def __init__(self, w):
+        self.ctx = dr.RasterizeContext(torch.device("cuda", 0))
+        self.w = w
+
+    def rasterize(self, pos, tri, ids=None):
+        return dr.rasterize(self.ctx, pos, tri, self.w.resolution)
+
+    interpolate = staticmethod(lambda a, r, tri, db=None, diff=None: dr.interpolate(
+        a, r, tri, rast_db=db, diff_attrs=diff))
+    construct_mip = staticmethod(dr.texture_construct_mip)
+
+    @staticmethod
+    def texture(tex, uv, uv_da, boundary, mip=None):
+        return dr.texture(tex, uv, uv_da, mip=mip, filter_mode="linear-mipmap-linear",
+                          boundary_mode=boundary)
+
+    antialias = staticmethod(dr.antialias)
+
+
+class _Oracle:
+    """The oracle on the CPU, rasterizing from given triangle ids."""
+
+    def rasterize(self, pos, tri, ids=None):
+        return R.rasterize_from_ids(pos, tri, ids, True)
+
+    @staticmethod
+    def interpolate(a, r, tri, db=None, diff=None):
+        channels = a.shape[-1]
+        return R.interpolate(a, r, tri, db, list(range(channels)) if diff == "all" else [])
+
+    construct_mip = staticmethod(lambda tex: R.texture_construct_mip(tex, None))
+
+    @staticmethod
+    def texture(tex, uv, uv_da, boundary, mip=None):
+        return R.texture(tex, uv, uv_da, "linear-mipmap-linear", boundary, None, mip=mip)
+
+    antialias = staticmethod(lambda c, r, p, tri: R.antialias(c, r, p, tri, 1.0))
+
+
+def _one_view(w, ops, device, ids=None):
+    """View 0 of workload ``w`` through ``ops``: the outputs of every stage and the gradients
+    of the MSE loss to every leaf, on the CPU."""
+    t = w.tensors
+    one = {"pos": t["pos"][:1], "target": t["target"][:1]}
+    for k in ("tri", "uv", "feat", "tex", "normals", "cube"):
+        if k in t:
+            one[k] = t[k]
+    if "view" in t:
+        one["view"], one["view_da"] = t["view"][:1], t["view_da"][:1]
+    x = {k: v.clone().to(device) for k, v in one.items()}
+    leaves = {k: x[k].requires_grad_(True) for k in ("pos", "feat", "tex", "cube") if k in x}
+    tri = x["tri"]
+    rast, rast_db = ops.rasterize(x["pos"], tri, ids)
+    outs = {"rast": rast, "rast_db": rast_db}
+    if w.name == "textured":
+        outs["uv"], outs["uv_da"] = ops.interpolate(x["uv"], rast, tri, rast_db, "all")
+        mip = ops.construct_mip(x["tex"])
+        col = ops.texture(x["tex"], outs["uv"], outs["uv_da"], "wrap", mip=mip)
+    elif w.name == "large":
+        outs["f"], _ = ops.interpolate(x["feat"], rast, tri)
+        outs["st"], outs["st_da"] = ops.interpolate(x["uv"], rast, tri, rast_db, "all")
+        col = ops.texture(x["tex"], outs["st"], outs["st_da"], "wrap")
+        f = outs["f"]
+        col = col + 0.1 * (f[..., :4] + f[..., 4:])
+    else:
+        outs["n"], outs["n_da"] = ops.interpolate(x["normals"], rast, tri, rast_db, "all")
+        dirs, dirs_da = workloads.reflect(x["view"], x["view_da"], outs["n"], outs["n_da"])
+        col = ops.texture(x["cube"], dirs, dirs_da, "cube")
+    outs["col"] = col
+    outs["aa"] = ops.antialias(col, rast, x["pos"], tri)
+    loss = torch.nn.functional.mse_loss(outs["aa"], x["target"])
+    loss.backward()
+    grads = {k: v.grad.detach().cpu() for k, v in leaves.items()}
+    return {k: v.detach().cpu() for k, v in outs.items()}, grads
+
+
+@contextlib.contextmanager
+def _lod_shifted(ulps):
+    """The oracle with its level of detail moved by ``ulps`` units in the last place (its value
+    only; the gradient through it is unchanged)."""
+    original = R.level_of_detail
+
+    def shifted(uv_da, height, width):
+        lod = original(uv_da, height, width)
+        target = torch.full_like(lod, math.copysign(math.inf, ulps))
+        moved = lod.detach()
+        for _ in range(abs(ulps)):
+            moved = torch.nextafter(moved, target)
+        return lod + (moved - lod.detach())
+
+    R.level_of_detail = shifted
+    try:
+        yield
+    finally:
+        R.level_of_detail = original
+
+
+@pytest.mark.parametrize("name", ["textured", "large", "cubemap"])
+def test_one_view_forward_and_backward_in_full(name):
+    """Every output and every gradient of view 0 at the workload's full size, against the
+    oracle run from the GPU's triangle ids (the ids themselves are checked against the oracle's
+    brute force at sampled pixels above): values within 1e-5, gradients within 1e-4 of the
+    largest.
+
+    The level of detail is 0.5 log2 of the footprint, and log2's last bit is not pinned: the
+    GPU's and the host's log2 may differ by one unit in the last place. Where the level sits on
+    a whole number, that bit picks which two levels a trilinear lookup blends, and the gradient
+    with respect to the level (texel difference of those levels) jumps. Measured on the cube-map
+    workload: one such pixel moves the position gradient by 7.3e-4 of its largest value, and
+    moving the oracle's level up by one unit reproduces the GPU's gradient there to 4 digits.
+    So each gradient entry must be within tolerance of the oracle's with the level as computed,
+    or one unit above, or one below."""
+    w = workloads.build(name)
+    ours, our_grads = _one_view(w, _Gpu(w), "cuda")
+    ids = ours["rast"][..., 3].long() - 1
+    ref, ref_grads = _one_view(w, _Oracle(), "cpu", ids)
+    assert (ids >= 0).any()
+    assert torch.equal(ours["rast"][..., 3], ref["rast"][..., 3])
+    assert (ours["aa"] != ours["col"]).any(), "antialiasing should change silhouette pixels"
+    errors = {key: rel_error(ours[key], expect) for key, expect in ref.items()}
+    assert all(e < VALUE_TOL for e in errors.values()), errors
+
+    def excess(grads):
+        out = {}
+        for key, expect in ref_grads.items():
+            scale = expect.abs().max().item()
+            assert scale > 0, key
+            out[key] = ((our_grads[key] - grads[key]).abs() - GRAD_TOL * expect.abs()) / scale
+        return out
+
+    worst = excess(ref_grads)
+    as_computed = {key: e.max().item() for key, e in worst.items()}
+    if any(e >= GRAD_TOL for e in as_computed.values()):
+        for ulps in (1, -1):
+            with _lod_shifted(ulps):
+                _, shifted = _one_view(w, _Oracle(), "cpu", ids)
+            worst = {key: torch.minimum(e, excess(shifted)[key]) for key, e in worst.items()}
+    final = {key: e.max().item() for key, e in worst.items()}
+    print(name, "values", errors, "gradient excess / max: as computed", as_computed,
+          "within one unit of the level", final)
+    assert all(e < GRAD_TOL for e in final.values()), final
+
+
+def test_instances_antialias_on_layer_zero():
+    """Range mode, layer 0 of every item, then antialias forward and backward on all 256 items
+    (colour gradients per item) and on three items alone (their position gradient), against
+    the oracle on the same items."""
+    w = workloads.build("instances")
+    t = w.tensors
+    dev = torch.device("cuda", 0)
+    pos, tri, ranges = t["pos"], t["tri"], t["ranges"]
+    ctx = dr.RasterizeContext(dev)
+    rast, _ = dr.rasterize(ctx, pos.to(dev), tri.to(dev), w.resolution, ranges=ranges)
+    color = t["color"].to(dev).requires_grad_(True)
+    out = dr.antialias(color, rast, pos.to(dev), tri.to(dev))
+    weights = torch.randn(out.shape, generator=torch.Generator().manual_seed(40))
+    (out * weights.to(dev)).sum().backward()
+    out, color_grad, rast = out.detach().cpu(), color.grad.cpu(), rast.cpu()
+    items = [0, 97, 255]
+    neighbours = R.edge_neighbours(tri)
+    p = pos.clone().requires_grad_(True)
+    c = t["color"][items].clone().requires_grad_(True)
+    ref = R.antialias(c, rast[items], p, tri, 1.0, neighbours)
+    (ref * weights[items]).sum().backward()
+    assert (ref != t["color"][items]).any()
+    assert rel_error(out[items], ref.detach()) < VALUE_TOL
+    assert rel_error(color_grad[items], c.grad) < VALUE_TOL
+    # Position gradient of the three items alone.
+    p_gpu = pos.to(dev).requires_grad_(True)
+    sub = dr.antialias(t["color"][items].to(dev), rast[items].to(dev), p_gpu, tri.to(dev))
+    (sub * weights[items].to(dev)).sum().backward()
+    scale = p.grad.abs().max().item()
+    assert scale > 0
+    torch.testing.assert_close(p_gpu.grad.cpu(), p.grad, atol=GRAD_TOL * scale, rtol=GRAD_TOL)

@@ -540,3 +540,16 @@ def test_antialias_gradient_matches_finite_differences():
             step[0, vertex, axis] = eps
             numeric = (loss(pos + step) - loss(pos - step)) / (2 * eps)
             torch.testing.assert_close(p.grad[0, vertex, axis], numeric, rtol=1e-4, atol=1e-6)
+
+
+def test_cross_product_rounding_the_silhouettes_rely_on():
+    """The reference classifies folds with torch.linalg.cross, whose CPU kernel rounds each
+    component as fma(u_i, v_j, -(u_j v_i)); the HIP silhouette pass computes exactly that. A host
+    whose torch rounds otherwise would classify near-degenerate folds differently."""
+    gen = torch.Generator().manual_seed(3)
+    u, v = torch.randn(2, 1, 200_000, 3, generator=gen)
+    got = torch.linalg.cross(u, v, dim=-1)
+    U, V = u.double(), v.double()
+    for k, (i, j) in enumerate(((1, 2), (2, 0), (0, 1))):
+        fused = (U[..., i] * V[..., j] - (U[..., j] * V[..., i]).float().double()).float()
+        assert torch.equal(got[..., k], fused), k
