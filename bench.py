@@ -83,8 +83,9 @@ class KernelTimer:
 
     def install(self):
         def timed(name, *args):
-            if not self.active or (self.only is not None and name not in self.only):
-                return self._call(name, *args)
+            if (not self.active or name.endswith("_size")
+                    or (self.only is not None and name not in self.only)):
+                return self._call(name, *args)  # (size queries launch nothing)
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
             start.record()
@@ -119,6 +120,8 @@ OP_OF = {
     "dr_raster_visibility_start": "rasterize",
     "dr_raster_visibility_bin": "rasterize",
     "dr_raster_visibility_tiles": "rasterize",
+    "dr_raster_visibility": "rasterize",
+    "dr_raster_visibility_overflow": "rasterize",
     "dr_resolve_forward": "rasterize",
     "dr_resolve_backward": "rasterize",
     "dr_interpolate_forward": "interpolate",

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent.parent / "libdiffrast_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 MAX_LEVELS = 32
 
 c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -112,6 +112,10 @@ _SIGNATURES = {
         [_P, _P, ctypes.c_size_t, _P, ctypes.POINTER(ctypes.c_uint32), _P], ctypes.c_int),
     "dr_raster_visibility_tiles": (
         [_P, _P, _P, _P, ctypes.c_size_t, _P, ctypes.POINTER(ctypes.c_uint32), _P], ctypes.c_int),
+    "dr_raster_visibility_overflow": ([_P, _P, _P, _P, ctypes.c_size_t, ctypes.c_uint32, _P],
+                                      ctypes.c_int),
+    "dr_raster_visibility": ([_P, _P, _P, _P, ctypes.c_size_t, _P, ctypes.c_uint32,
+                              ctypes.c_uint32, _P, _P], ctypes.c_int),
     "dr_resolve_forward": ([_P, _P, _P, _P, _P], ctypes.c_int),
     "dr_resolve_backward": ([_P, _P, _P, _P, _P, _P], ctypes.c_int),
     "dr_interpolate_forward": ([_P, _P, _P, _P], ctypes.c_int),

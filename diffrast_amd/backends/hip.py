@@ -89,13 +89,31 @@ class _Geometry:
         self.shape = (self.batch, int(height), int(width))
 
 
-# Tile entries seen last for a geometry shape: the next call with that shape queues binning
-# and the tile pass with a buffer this large (plus a margin) before the count reaches the host,
-# so that the device does not wait for the host, and bins again with a buffer of the exact
-# size only when the lists outgrow it.
-_ENTRY_HINTS: dict[tuple, int] = {}
-_ENTRY_HINTS_KEPT = 64
-_hints_lock = threading.Lock()
+class _Sizes:
+    """What the last finished visibility call of one geometry shape found -- its tile entries
+    and tile-pass workgroups -- and the pinned buffer and event through which a later call's
+    counts come back without anyone waiting for them."""
+
+    __slots__ = ("entries", "groups", "counts", "event", "pending", "lock")
+
+    def __init__(self, entries: int, groups: int):
+        self.entries, self.groups = entries, groups
+        self.counts = torch.zeros(4, dtype=torch.int32, pin_memory=True)
+        self.event = torch.cuda.Event()
+        self.pending = False
+        self.lock = threading.Lock()
+
+    def refresh(self) -> None:
+        """Takes in the counts of the last call that sent them back, if they have arrived."""
+        if self.pending and self.event.query():
+            found = [v & 0xFFFFFFFF for v in self.counts.tolist()]
+            self.entries, self.groups = found[1], found[2]
+            self.pending = False
+
+
+_SIZES: dict[tuple, _Sizes] = {}
+_SIZES_KEPT = 64
+_sizes_lock = threading.Lock()
 _host = threading.local()
 
 
@@ -104,8 +122,8 @@ def _entry_capacity(count: int) -> int:
 
 
 def _host_counts(device: torch.device) -> tuple[Tensor, torch.cuda.Event]:
-    """Pinned memory for the visibility counts and the event that marks their arrival (one
-    pair per host thread and device: a call waits for its counts before it returns)."""
+    """Pinned memory for the counts of a first call and the event that marks their arrival
+    (one pair per host thread and device: such a call waits for its counts)."""
     per_device = getattr(_host, "counts", None)
     if per_device is None:
         per_device = _host.counts = {}
@@ -116,8 +134,22 @@ def _host_counts(device: torch.device) -> tuple[Tensor, torch.cuda.Event]:
     return pair
 
 
+def _remember(key: tuple, sizes: _Sizes) -> None:
+    with _sizes_lock:
+        if len(_SIZES) >= _SIZES_KEPT and key not in _SIZES:
+            _SIZES.pop(next(iter(_SIZES)), None)
+        _SIZES[key] = sizes
+
+
 def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
-    """Visibility keys [batch, height, width] (int64 holding the uint64 key bits)."""
+    """Visibility keys [batch, height, width] (int64 holding the uint64 key bits).
+
+    The first call of a geometry shape learns the tile-list sizes from the device (one wait
+    for four counts) and bins into a buffer of exactly that size. Later calls -- and every call
+    under HIP graph capture -- queue the whole visibility at once with a buffer sized from the
+    last counts seen for the shape, which come back through pinned memory without a wait; if
+    the lists outgrow the buffer, the device rasterizes the binned triangles through its
+    overflow pass instead (same keys)."""
     device = geo.pos.device
     keys = torch.empty(geo.shape, dtype=torch.int64, device=device)
     size = ctypes.c_size_t()
@@ -125,43 +157,57 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
     workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
     prev = None if previous is None else previous.contiguous()
     stream = _lib.stream(device)
-    host, arrived = _host_counts(device)
-    hint_key = (device.index, geo.shape, geo.struct.num_tri, geo.struct.num_instances,
-                prev is None)
-    with _hints_lock:
-        hint = _ENTRY_HINTS.get(hint_key, 0)
-    capacity = _entry_capacity(hint) if hint else 0
-    counts = (ctypes.c_uint32 * 4)(0, capacity, 0, 0)
-    call("dr_raster_visibility_start", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),
-         size.value, host.data_ptr(), stream)
-    arrived.record(torch.cuda.current_stream(device))
-    try:
-        if capacity:
-            # the tile lists and the tile pass, queued before the counts are known
-            entries = torch.empty(capacity, dtype=torch.int32, device=device)
-            call("dr_raster_visibility_bin", ref(geo.struct), ptr(workspace), size.value,
-                 ptr(entries), counts, stream)
-            call("dr_raster_visibility_tiles", ref(geo.struct), ptr(prev), ptr(keys),
-                 ptr(workspace), size.value, ptr(entries), counts, stream)
-    finally:
-        arrived.synchronize()  # the buffer is free again for the next call
-    found = [v & 0xFFFFFFFF for v in host.tolist()]
-    if found[1] or hint:
-        with _hints_lock:
-            if len(_ENTRY_HINTS) >= _ENTRY_HINTS_KEPT and hint_key not in _ENTRY_HINTS:
-                _ENTRY_HINTS.pop(next(iter(_ENTRY_HINTS)), None)
-            _ENTRY_HINTS[hint_key] = found[1]
-    if found[1] > capacity:
-        # the lists did not fit (or no size was known): bin again into a buffer that fits
-        counts[:] = (0, 0, 0, 0)  # the calls above processed nothing
+    key = (device.index, geo.shape, geo.struct.num_tri, geo.struct.num_instances, prev is None)
+    capturing = torch.cuda.is_current_stream_capturing()
+    with _sizes_lock:
+        sizes = _SIZES.get(key)
+    if sizes is None and not capturing:
+        host, arrived = _host_counts(device)
+        call("dr_raster_visibility_start", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),
+             size.value, host.data_ptr(), stream)
+        arrived.record(torch.cuda.current_stream(device))
+        arrived.synchronize()
+        found = [v & 0xFFFFFFFF for v in host.tolist()]
         counts = (ctypes.c_uint32 * 4)(*found)
-        entries = torch.empty(found[1], dtype=torch.int32, device=device)
+        entries = torch.empty(max(found[1], 1), dtype=torch.int32, device=device)
         call("dr_raster_visibility_bin", ref(geo.struct), ptr(workspace), size.value,
              ptr(entries), counts, stream)
         call("dr_raster_visibility_tiles", ref(geo.struct), ptr(prev), ptr(keys),
              ptr(workspace), size.value, ptr(entries), counts, stream)
+        _remember(key, _Sizes(found[1], found[2]))
+        return keys
+    if sizes is None:  # captured before any eager call of this shape: a generous guess
+        capacity, groups = min(4 * geo.struct.num_instances + 4096, 0x7fffffff), 0
     else:
-        counts[:] = found  # the calls above now describe the lists they processed
+        with sizes.lock:
+            if not capturing:  # no event may be queried while a stream is captured
+                sizes.refresh()
+            capacity = _entry_capacity(sizes.entries)
+            groups = min(sizes.groups + sizes.groups // 8 + 8, 0xffffffff) if sizes.groups else 0
+    entries = torch.empty(capacity, dtype=torch.int32, device=device)
+    # The four passes of dr_raster_visibility, queued one call each (so that each can be timed
+    # on its own): start, bin and tiles into the buffer, overflow when it was too small.
+    spec = (ctypes.c_uint32 * 4)(0, capacity, groups, 0)
+
+    def passes(readback):
+        call("dr_raster_visibility_start", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),
+             size.value, ptr(readback), stream)
+        call("dr_raster_visibility_bin", ref(geo.struct), ptr(workspace), size.value,
+             ptr(entries), spec, stream)
+        call("dr_raster_visibility_tiles", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),
+             size.value, ptr(entries), spec, stream)
+        call("dr_raster_visibility_overflow", ref(geo.struct), ptr(prev), ptr(keys),
+             ptr(workspace), size.value, capacity, stream)
+
+    if sizes is None or capturing:
+        passes(None)
+        return keys
+    with sizes.lock:
+        readback = None if sizes.pending else sizes.counts
+        passes(readback)
+        if readback is not None:
+            sizes.event.record(torch.cuda.current_stream(device))
+            sizes.pending = True
     return keys
 
 

@@ -11,7 +11,7 @@ extern "C" const char* dr_error_string(int code) {
   }
 }
 
-extern "C" int dr_abi_version(void) { return 9; }
+extern "C" int dr_abi_version(void) { return 10; }
 
 extern "C" int dr_struct_size(int which) {
   switch (which) {

@@ -1077,6 +1077,7 @@ __global__ __launch_bounds__(256) void raster_tile_place(Workspace ws) {
 // items. Hits merge into the keys in LDS (64-bit min). Before each chunk the tile's farthest key
 // bounds what can still win: triangles entirely behind it are skipped, and so are single pixels
 // that already hold a nearer key. The improved keys are stored once at the end.
+template <bool kLoop>
 __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
                                                           const uint64_t* prev, uint64_t* keys,
                                                           Workspace ws,
@@ -1099,16 +1100,24 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
 
   // Workgroups are dispatched round-robin over the 8 XCDs: XCD k runs the busy tiles of share
   // k (for a batch of 8 images, one image), so the records that neighbouring tiles share stay in
-  // one L2, heaviest first; the grid is 8 x the largest share, the surplus returns at once.
+  // one L2, heaviest first. The grid is a multiple of 8 and workgroup b takes slot b / 8 of its
+  // share; with kLoop also slots b / 8 + grid / 8, b / 8 + 2 grid / 8, ..., so that a grid
+  // sized before the shares were known still covers every tile. (The loop costs registers:
+  // 90 VGPRs and five waves per SIMD instead of 80 and six, so it is compiled only for that.)
   const int share = (int)(blockIdx.x % kXcdShares);
-  const uint32_t slot = blockIdx.x / kXcdShares;
-  // Lists that did not fit the entry buffer were not binned: nothing to read.
-  if (ws.counters[1] > capacity) return;     // uniform over the grid
-  if (slot >= ws.share_info[share]) return;  // uniform over the workgroup
+  // Lists that did not fit the entry buffer were not binned: nothing to read (the overflow
+  // pass rasterizes the binned triangles instead).
+  if (ws.counters[1] > capacity) return;  // uniform over the grid
+  const uint32_t busy = ws.share_info[share];
+  const uint32_t stride = gridDim.x / kXcdShares;
+  for (uint32_t slot = blockIdx.x / kXcdShares; slot < busy; slot += stride) {
   const uint32_t tile = ws.tile_order[ws.share_info[kXcdShares + share] + slot];
   const uint32_t begin = ws.list_offsets[(size_t)tile * kDepthSlabs];
   const uint32_t end = ws.list_offsets[(size_t)(tile + 1) * kDepthSlabs];
-  if (begin == end) return;  // uniform over the workgroup
+  if (begin == end) {  // uniform over the workgroup
+    if (!kLoop) break;
+    continue;
+  }
 
   // This thread's entry of the next chunk, read ahead.
   uint32_t next = begin + threadIdx.x < end ? entries[begin + threadIdx.x] : 0u;
@@ -1289,6 +1298,54 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   if (inside)
     keys[tile_pixel0 + (int64_t)(threadIdx.x / kTile) * g.width + threadIdx.x % kTile] =
         s_key[threadIdx.x];
+  if (!kLoop) break;
+  __syncthreads();  // the next tile's set-up reuses the LDS
+  }
+}
+
+// Visibility of the binned triangles when their tile lists did not fit the entry buffer (the
+// bin and tile passes then returned without work): each workgroup takes the records of every
+// gridDim.x-th setup workgroup, one triangle at a time, and its 256 threads test the pixel centres of the
+// triangle's box, merging hits into the keys with 64-bit atomic min. The result is the same as
+// the tile pass's; the work is not (no spans, no depth culling, one atomic per hit).
+__global__ __launch_bounds__(256) void raster_overflow_kernel(DrRasterGeometry g,
+                                                              const uint64_t* prev,
+                                                              uint64_t* keys, Workspace ws,
+                                                              uint32_t capacity) {
+  if (ws.counters[1] <= capacity) return;  // uniform over the grid: the lists fitted
+  for (int block = blockIdx.x; block < ws.record_blocks; block += gridDim.x) {
+  const uint32_t count = ws.block_records[block];
+  for (uint32_t j = 0; j < count; ++j) {
+    const float4* rec = ws.records + ((size_t)block * 256 + j) * kRecord;
+    Tri T;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const float4 v = rec[k];
+      T.x[k] = v.x;
+      T.y[k] = v.y;
+      T.z[k] = v.z;
+      T.w[k] = v.w;
+    }
+    const float4 meta = rec[3];
+    const int b = __float_as_int(meta.x);
+    const uint32_t row = __float_as_uint(meta.y) & 0xffffffu;
+    T.reach_x = reach(T.x, T.w);
+    T.reach_y = reach(T.y, T.w);
+    int x_lo, x_hi, y_lo, y_hi;
+    candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
+    if (x_lo > x_hi || y_lo > y_hi) continue;  // uniform: every thread read the same record
+    const int bw = x_hi - x_lo + 1;
+    const int64_t area = (int64_t)bw * (y_hi - y_lo + 1);
+    for (int64_t p = threadIdx.x; p < area; p += blockDim.x) {
+      const int y = y_lo + (int)(p / bw), x = x_lo + (int)(p % bw);
+      float depth;
+      if (covers(T.x, T.y, T.z, T.w, T.reach_x, T.reach_y, ws.px[x], ws.py[y], depth)) {
+        const int64_t pixel = ((int64_t)b * g.height + y) * g.width + x;
+        merge_key(keys, prev, pixel, depth_key(depth, row));
+      }
+    }
+  }
+  }
 }
 
 // ---- resolve ----------------------------------------------------------------------------
@@ -1581,18 +1638,93 @@ static int queue_visibility_start(const DrRasterGeometry* g, const uint64_t* pre
   }
   const int status = launch_status();
   if (status != DR_OK) return status;
-  if (hipMemcpyAsync(host_counts, ws.counters, 4 * sizeof(uint32_t), hipMemcpyDeviceToHost, s) !=
-      hipSuccess)
+  if (host_counts != nullptr &&
+      hipMemcpyAsync(host_counts, ws.counters, 4 * sizeof(uint32_t), hipMemcpyDeviceToHost, s) !=
+          hipSuccess)
     return DR_ERR_HIP;
   return DR_OK;
+}
+
+// Up to this many workgroups, a tile pass whose busy tiles are not known launches one per tile
+// (the idle ones return at once, ~0.2 us per thousand) rather than the looping kernel.
+constexpr int64_t kPlainTileGrid = 1 << 16;
+
+// Launches the tile pass. exact: `requested` is the grid this call's counts give (8 x the busy
+// tiles of the largest share), so one workgroup per busy tile. Otherwise it is a guess (0: none)
+// and the grid is one workgroup per tile up to kPlainTileGrid tiles, else the guess (at least
+// 8, a multiple of 8, below 2^24) with the looping kernel, which covers every tile whatever
+// the grid.
+static void launch_tile_pass(const DrRasterGeometry& g, const uint64_t* prev, uint64_t* keys,
+                             const Workspace& ws, const uint32_t* entries, uint32_t capacity,
+                             uint32_t requested, bool exact, hipStream_t s) {
+  const int64_t bound = tile_grid_bound(ws);
+  const int64_t limit = ((int64_t)1 << 24) - kXcdShares;
+  if ((exact && requested > 0 && requested <= limit) || (!exact && bound <= kPlainTileGrid)) {
+    const int64_t grid = exact ? (int64_t)requested : bound;
+    raster_tile_kernel<false><<<(int)grid, 256, 0, s>>>(g, prev, keys, ws, entries, capacity);
+    return;
+  }
+  int64_t grid = requested == 0 ? bound : ((int64_t)requested + kXcdShares - 1) / kXcdShares *
+                                              kXcdShares;
+  grid = std::min(std::min(std::max<int64_t>(grid, kXcdShares), bound), limit);
+  raster_tile_kernel<true><<<(int)grid, 256, 0, s>>>(g, prev, keys, ws, entries, capacity);
+}
+
+// The overflow pass's grid: it walks the setup workgroups' records with a grid stride, so that
+// it costs little when there is nothing to do.
+static int overflow_grid(const Workspace& ws) { return std::min(ws.record_blocks, 2048); }
+
+// The whole visibility, queued: the first part, then the bin and tile passes with an entry
+// buffer of `capacity` entries, then the overflow pass, which rasterizes the binned triangles
+// itself when the lists turned out larger than the buffer (the device decides; nothing waits
+// for the host).
+static int queue_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                            uint64_t* keys, void* workspace, size_t workspace_bytes,
+                            uint32_t* entries, uint32_t capacity, uint32_t tile_groups,
+                            uint32_t* host_counts, hipStream_t s) {
+  const int status = queue_visibility_start(g, prev_keys, keys, workspace, workspace_bytes,
+                                            host_counts, s);
+  if (status != DR_OK) return status;
+  if ((int64_t)g->batch * g->height * g->width == 0 || g->num_instances == 0) return DR_OK;
+  Workspace ws = layout(*g, (char*)workspace);
+  if (capacity > 0) {
+    raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, entries, capacity);
+    launch_tile_pass(*g, prev_keys, keys, ws, entries, capacity, tile_groups, false, s);
+  }
+  raster_overflow_kernel<<<overflow_grid(ws), 256, 0, s>>>(*g, prev_keys, keys, ws, capacity);
+  return launch_status();
+}
+
+extern "C" int dr_raster_visibility_overflow(const DrRasterGeometry* g,
+                                             const uint64_t* prev_keys, uint64_t* keys,
+                                             void* workspace, size_t workspace_bytes,
+                                             uint32_t entry_capacity, void* stream) {
+  if (!valid_geometry(g)) return DR_ERR_ARGUMENT;
+  if ((int64_t)g->batch * g->height * g->width == 0 || g->num_instances == 0) return DR_OK;
+  if (!keys) return DR_ERR_ARGUMENT;
+  Workspace ws = layout(*g, (char*)workspace);
+  if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
+  raster_overflow_kernel<<<overflow_grid(ws), 256, 0, (hipStream_t)stream>>>(
+      *g, prev_keys, keys, ws, entry_capacity);
+  return launch_status();
+}
+
+extern "C" int dr_raster_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                                    uint64_t* keys, void* workspace, size_t workspace_bytes,
+                                    uint32_t* entries, uint32_t entry_capacity,
+                                    uint32_t tile_groups, uint32_t* host_counts, void* stream) {
+  if (!valid_geometry(g) || (entry_capacity > 0 && !entries)) return DR_ERR_ARGUMENT;
+  if (host_counts) host_counts[0] = host_counts[1] = host_counts[2] = host_counts[3] = 0;
+  return queue_visibility(g, prev_keys, keys, workspace, workspace_bytes, entries,
+                          entry_capacity, tile_groups, host_counts, (hipStream_t)stream);
 }
 
 extern "C" int dr_raster_visibility_start(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                           uint64_t* keys, void* workspace,
                                           size_t workspace_bytes, uint32_t* host_counts,
                                           void* stream) {
-  if (!valid_geometry(g) || !host_counts) return DR_ERR_ARGUMENT;
-  host_counts[0] = host_counts[1] = host_counts[2] = host_counts[3] = 0;
+  if (!valid_geometry(g)) return DR_ERR_ARGUMENT;
+  if (host_counts) host_counts[0] = host_counts[1] = host_counts[2] = host_counts[3] = 0;
   return queue_visibility_start(g, prev_keys, keys, workspace, workspace_bytes, host_counts,
                                 (hipStream_t)stream);
 }
@@ -1643,10 +1775,9 @@ extern "C" int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint6
   if (!entries || !keys) return DR_ERR_ARGUMENT;
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
-  const int64_t grid = counts[2] != 0 ? (int64_t)counts[2] : tile_grid_bound(ws);
-  if (grid >= ((int64_t)1 << 24)) return DR_ERR_ARGUMENT;  // 256 threads each, 32-bit ids
-  hipStream_t s = (hipStream_t)stream;
-  raster_tile_kernel<<<(int)grid, 256, 0, s>>>(*g, prev_keys, keys, ws, entries, counts[1]);
+  // counts[3] (busy tiles) is known only with this call's own counts: then counts[2] is exact.
+  launch_tile_pass(*g, prev_keys, keys, ws, entries, counts[1], counts[2], counts[3] != 0,
+                   (hipStream_t)stream);
   return launch_status();
 }
 

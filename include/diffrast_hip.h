@@ -87,8 +87,9 @@ int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint64_t* prev_k
  * counts are there once the stream has passed this point (an event recorded after the call).
  * Meanwhile the caller may queue dr_raster_visibility_bin and dr_raster_visibility_tiles with
  * counts {0, capacity of its entry buffer, 0, 0}: if the lists fit, they complete the
- * visibility; if not (host_counts[1] > capacity), both returned at once and the caller calls
- * them again with the counts and a buffer of host_counts[1] entries.
+ * visibility; if not (host_counts[1] > capacity), both returned at once and the caller either
+ * calls them again with the counts and a buffer of host_counts[1] entries, or queues
+ * dr_raster_visibility_overflow right after them (no wait). host_counts may be NULL (no copy).
  * (Same reference interfaces as dr_raster_visibility_begin.) */
 int dr_raster_visibility_start(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                uint64_t* keys, void* workspace, size_t workspace_bytes,
@@ -96,18 +97,49 @@ int dr_raster_visibility_start(const DrRasterGeometry* g, const uint64_t* prev_k
 
 /* Visibility, second part: fills the per-tile lists. entries holds counts[1] uint32: the
  * lists of all tiles, tile by tile, near to far. Nothing to do when counts[1] == 0. counts[1]
- * may also be a capacity larger than the lists: the kernel returns at once if they exceed it. (The reference has no binning: its visibility tests every triangle at every
- * pixel, reference.py:368-397; _triton_raster.py:241-306 keeps the nearest per pixel.) */
+ * may also be a capacity larger than the lists: the kernel returns at once if they exceed it.
+ * (The reference's pure-PyTorch visibility tests every triangle at every pixel,
+ * reference.py:368-397; its Triton path bins triangles into tile chunks,
+ * _triton_rasterize.py:371-424, and keeps the nearest per pixel in _tile_kernel,
+ * _triton_rasterize.py:219-269.) */
 int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspace, size_t workspace_bytes,
                              uint32_t* entries, const uint32_t counts[4], void* stream);
 
 /* Visibility, third part: rasterizes the binned triangles tile by tile into keys, after
  * dr_raster_visibility_bin with the same entries and counts. Nothing to do when
- * counts[1] == 0. counts[2] == 0 (not known yet): one workgroup per tile of the largest XCD
- * share, 8 x, of which those past the share's busy tiles return at once. */
+ * counts[1] == 0. The pass runs counts[2] workgroups (rounded up to a multiple of 8; 0: one per
+ * tile of the largest XCD share, 8 x); each takes every (grid / 8)-th busy tile of its share,
+ * so any grid covers all tiles. */
 int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                uint64_t* keys, void* workspace, size_t workspace_bytes,
                                const uint32_t* entries, const uint32_t counts[4], void* stream);
+
+/* The overflow pass on its own, after dr_raster_visibility_bin and _tiles were queued with a
+ * buffer of entry_capacity entries: when the lists turned out longer (the device knows; the
+ * host need not), it rasterizes the binned triangles straight into keys; otherwise it returns
+ * at once. dr_raster_visibility_start (host_counts may be NULL), _bin, _tiles and this pass,
+ * queued in turn, are dr_raster_visibility below in four calls. */
+int dr_raster_visibility_overflow(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                                  uint64_t* keys, void* workspace, size_t workspace_bytes,
+                                  uint32_t entry_capacity, void* stream);
+
+/* The whole visibility in one call that never waits for the host: the work of
+ * dr_raster_visibility_start, then the bin and tile passes with an entry buffer of
+ * entry_capacity uint32 (entries may be NULL when it is 0) and a tile pass of tile_groups
+ * workgroups (as counts[2] above; 0: one per tile), then an overflow pass. If the tile lists
+ * turn out longer than the buffer, the bin and tile passes return without work and the overflow
+ * pass rasterizes the binned triangles straight into keys (64-bit atomic min per covered pixel:
+ * the same keys, more work), so the result never depends on the capacity. host_counts
+ * (nullable; pinned host memory) receives the four counts of dr_raster_visibility_begin once
+ * the stream passes this call, for sizing the next call of the same shape. Nothing here
+ * allocates or synchronises, so the call can be captured in a HIP graph (host_counts NULL).
+ * (Same reference interfaces as dr_raster_visibility_begin: rasterize_layer,
+ * src/diffrast/backends/triton.py:21-40, whose binning sizes its buffers on the host,
+ * _triton_rasterize.py:387-424.) */
+int dr_raster_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys, uint64_t* keys,
+                         void* workspace, size_t workspace_bytes, uint32_t* entries,
+                         uint32_t entry_capacity, uint32_t tile_groups, uint32_t* host_counts,
+                         void* stream);
 
 /* rast [batch, h, w, 4] = (u, v, z/w, id + 1) and rast_db [batch, h, w, 4] = (du/dx, du/dy,
  * dv/dx, dv/dy) from keys; zeros where a key is empty. rast_db may be NULL.

@@ -430,6 +430,27 @@ def _keys_through_abi(pos, tri, res, capacity, prev=None):
     return keys, list(counts)
 
 
+def _keys_one_call(pos, tri, res, capacity, groups, prev=None):
+    """Keys from dr_raster_visibility (no wait: an entry buffer of ``capacity``, a tile pass of
+    ``groups`` workgroups, the overflow pass when the lists do not fit) and its counts."""
+    import ctypes
+
+    from diffrast_amd.backends import _lib
+
+    geo = hip._Geometry(pos, tri, res)
+    keys = torch.empty(geo.shape, dtype=torch.int64, device=pos.device)
+    size = ctypes.c_size_t()
+    _lib.call("dr_raster_workspace_size", _lib.ref(geo.struct), ctypes.byref(size))
+    workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=pos.device)
+    host = torch.full((4,), -1, dtype=torch.int32, pin_memory=True)
+    entries = torch.empty(max(capacity, 1), dtype=torch.int32, device=pos.device)
+    _lib.call("dr_raster_visibility", _lib.ref(geo.struct), _lib.ptr(prev), _lib.ptr(keys),
+              _lib.ptr(workspace), size.value, _lib.ptr(entries) if capacity else None,
+              capacity, groups, host.data_ptr(), _lib.stream(pos.device))
+    torch.cuda.synchronize()
+    return keys, [v & 0xFFFFFFFF for v in host.tolist()]
+
+
 def _keys_waiting(pos, tri, res, prev=None):
     """Keys from dr_raster_visibility_begin (which waits for the counts), bin and tiles."""
     import ctypes
@@ -472,27 +493,35 @@ def test_visibility_with_entry_buffer_queued_before_the_counts(resolution):
             keys, got = _keys_through_abi(pos, tri, resolution, capacity, prev)
             assert got == counts, (layer, capacity)
             assert torch.equal(keys, expected), (layer, capacity)
+            # The one-call form: lists that do not fit go through the overflow pass; a tile
+            # pass of fewer workgroups than busy tiles loops over them.
+            for groups in (0, 8, 24, counts[2]):
+                keys, got = _keys_one_call(pos, tri, resolution, capacity, groups, prev)
+                assert got == counts, (layer, capacity, groups)
+                assert torch.equal(keys, expected), (layer, capacity, groups)
         prev = expected
     ours = [hip.rasterize_layer(pos, tri, resolution, True, None)[0] for _ in range(3)]
     assert torch.equal(ours[0], ours[1]) and torch.equal(ours[0], ours[2])
 
 
-def test_entry_buffer_hint_outgrown_through_public_path():
-    # The same mesh shape drawn at a quarter of its size, then whole: the second call's tile
-    # lists outgrow the buffer sized from the first, are binned again into one that fits, and
-    # must still match the oracle; the third call (small again) runs in the buffer sized from
-    # the second.
+def test_tile_lists_outgrowing_the_remembered_size_through_public_path():
+    # The same mesh shape drawn at a quarter of its size, then whole, alternately: the first
+    # call learns its list sizes from the device; each whole-size call outgrows the buffer sized
+    # from the call before and goes through the overflow pass; each small call fits. Every
+    # layer must match the oracle, and the sizes remembered must follow the calls.
     gen = torch.Generator().manual_seed(5)
     pos, tri = random_mesh(2000, gen, batch=2)
     small = pos.clone()
     small[..., :2] *= 0.25
     res = (128, 128)
-    hip._ENTRY_HINTS.clear()
+    hip._SIZES.clear()
     seen = []
-    for p in (small, pos, small):
+    for p in (small, pos, small, pos):
         assert_layers_match(p, tri, res, count=2)
-        first_layer = [v for k, v in hip._ENTRY_HINTS.items() if k[-1]]
+        torch.cuda.synchronize()
+        first_layer = [v for k, v in hip._SIZES.items() if k[-1]]
         assert len(first_layer) == 1
-        seen.append(first_layer[0])
+        first_layer[0].refresh()
+        seen.append(first_layer[0].entries)
     assert seen[0] > 0 and seen[1] > hip._entry_capacity(seen[0]), seen
-    assert seen[2] == seen[0], seen
+    assert seen[2] == seen[0] and seen[3] == seen[1], seen
