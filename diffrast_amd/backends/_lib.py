@@ -116,6 +116,7 @@ _SIGNATURES = {
                                       ctypes.c_int),
     "dr_raster_visibility": ([_P, _P, _P, _P, ctypes.c_size_t, _P, ctypes.c_uint32,
                               ctypes.c_uint32, _P, _P], ctypes.c_int),
+    "dr_raster_visibility_static": ([_P, _P, _P, _P], ctypes.c_int),
     "dr_resolve_forward": ([_P, _P, _P, _P, _P], ctypes.c_int),
     "dr_resolve_backward": ([_P, _P, _P, _P, _P, _P], ctypes.c_int),
     "dr_interpolate_forward": ([_P, _P, _P, _P], ctypes.c_int),

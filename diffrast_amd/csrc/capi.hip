@@ -7,6 +7,10 @@ extern "C" const char* dr_error_string(int code) {
     case DR_ERR_ARGUMENT: return "invalid argument (a size, pointer or mode is out of range)";
     case DR_ERR_CAPACITY: return "workspace or buffer smaller than required";
     case DR_ERR_HIP: return hipGetErrorString(hipPeekAtLastError());
+    case DR_ERR_SCRATCH:
+      return "the call needs more memory than the 64 MiB static scratch buffer of the "
+             "allocation-free entry point holds (at most 48 MiB of visibility workspace, "
+             "dr_raster_workspace_size)";
     default: return "unknown error";
   }
 }

@@ -31,6 +31,8 @@
 //
 // The resolve kernels turn keys into rast / rast_db (reference.py:69-114) and carry gradients
 // back to the vertices.
+#include <mutex>
+
 #include "common.h"
 #include "coverage.h"
 
@@ -1707,6 +1709,55 @@ extern "C" int dr_raster_visibility_overflow(const DrRasterGeometry* g,
   raster_overflow_kernel<<<overflow_grid(ws), 256, 0, (hipStream_t)stream>>>(
       *g, prev_keys, keys, ws, entry_capacity);
   return launch_status();
+}
+
+// ---- the allocation-free visibility ---------------------------------------------------------
+//
+// One static device buffer holds the workspace and the tile entries of
+// dr_raster_visibility_static, for callers that cannot allocate. Each GPU that runs it holds its
+// own copy for the life of the process. Host code never passes the array's name to a kernel (on
+// the host it is only a stand-in for the symbol): its device address, per device, comes from
+// hipGetSymbolAddress on the first call with that device current.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+constexpr size_t kScratchMinEntries = 4096;  // the workspace leaves room for at least these
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex scratch_mutex;
+static void* scratch_address[kMaxDevices] = {};
+
+static int scratch_of_current_device(void** address) {
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess) return DR_ERR_HIP;
+  if (device < 0 || device >= kMaxDevices) return DR_ERR_ARGUMENT;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_address[device] == nullptr) {
+    void* found = nullptr;
+    if (hipGetSymbolAddress(&found, HIP_SYMBOL(scratch)) != hipSuccess || found == nullptr)
+      return DR_ERR_HIP;
+    scratch_address[device] = found;
+  }
+  *address = scratch_address[device];
+  return DR_OK;
+}
+
+extern "C" int dr_raster_visibility_static(const DrRasterGeometry* g,
+                                           const uint64_t* prev_keys, uint64_t* keys,
+                                           void* stream) {
+  if (!valid_geometry(g)) return DR_ERR_ARGUMENT;
+  const size_t workspace_bytes = layout(*g, nullptr).bytes;  // a multiple of 256
+  if (workspace_bytes + kScratchMinEntries * sizeof(uint32_t) > kScratchBytes)
+    return DR_ERR_SCRATCH;
+  void* base = nullptr;
+  const int status = scratch_of_current_device(&base);
+  if (status != DR_OK) return status;
+  uint32_t* entries = (uint32_t*)((char*)base + workspace_bytes);
+  const size_t capacity =
+      std::min<size_t>((kScratchBytes - workspace_bytes) / sizeof(uint32_t), 0xffffffffu);
+  // Everything the passes read is set up by raster_prepare at the start of the call (keys,
+  // list counts, counters), so what the previous call left in the buffer does not matter.
+  return queue_visibility(g, prev_keys, keys, base, workspace_bytes, entries,
+                          (uint32_t)capacity, 0, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int dr_raster_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys,

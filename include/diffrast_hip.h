@@ -30,6 +30,7 @@ enum {
   DR_ERR_ARGUMENT = 1001,  /* a size, pointer or mode is out of range */
   DR_ERR_CAPACITY = 1002,  /* a workspace or buffer is smaller than required */
   DR_ERR_HIP = 1003,       /* the HIP runtime reported an error (see dr_error_string) */
+  DR_ERR_SCRATCH = 1004,   /* more than the allocation-free entry point's static buffer holds */
 };
 
 /* Message for a code returned by any entry point (static storage). */
@@ -140,6 +141,21 @@ int dr_raster_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys, u
                          void* workspace, size_t workspace_bytes, uint32_t* entries,
                          uint32_t entry_capacity, uint32_t tile_groups, uint32_t* host_counts,
                          void* stream);
+
+/* dr_raster_visibility without a workspace or an entry buffer from the caller: both live in
+ * one static device buffer of 64 MiB, `scratch`, so the call allocates nothing (no hipMalloc,
+ * no allocating library routine) and waits for nothing. No counterpart in the reference: it is
+ * for callers that cannot allocate -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation. Limit: the visibility workspace of the geometry
+ * (dr_raster_workspace_size) must leave room for 4096 tile entries, i.e. be at most
+ * 64 MiB - 16 KiB (DR_ERR_SCRATCH otherwise: about 690K triangle instances at 512x512, 870K
+ * at 4 x 1024^2); tile lists beyond the rest of the buffer go through the overflow pass.
+ * Each GPU holds its own copy of the buffer from the first call on it (the device current at
+ * the call) until the process ends. Every call on a GPU shares that GPU's buffer: calls that
+ * overlap on one GPU (other streams, other threads) race and must be serialised by the caller.
+ * Each call prepares what it reads, so what an earlier call left there does not matter. */
+int dr_raster_visibility_static(const DrRasterGeometry* g, const uint64_t* prev_keys,
+                                uint64_t* keys, void* stream);
 
 /* rast [batch, h, w, 4] = (u, v, z/w, id + 1) and rast_db [batch, h, w, 4] = (du/dx, du/dy,
  * dv/dx, dv/dy) from keys; zeros where a key is empty. rast_db may be NULL.
