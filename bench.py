@@ -227,16 +227,13 @@ class BytesModel:
         P, C, coords, texels = self._texture(_struct(args[0]))
         return P * C * 4 + 2 * coords + 2 * texels
 
-    @staticmethod
-    def _mip(args):
-        tex_batch, channels, total = args[1], args[2], args[3]
-        return tex_batch * total * channels * 4  # base read + levels written, or the adjoint
-
     def op_mip_build(self, args):
-        return self._mip(args)
+        tex_batch, channels, total = args[2], args[3], args[4]
+        return tex_batch * total * channels * 4  # base read, levels written
 
     def op_mip_build_backward(self, args):
-        return self._mip(args)
+        tex_batch, channels, total = args[1], args[2], args[3]
+        return tex_batch * total * channels * 4  # the adjoint
 
     def _aa(self, args):
         a = _struct(args[0])
@@ -254,23 +251,42 @@ class BytesModel:
 
 # ---- the five workloads' steps ----------------------------------------------------------------
 
-def _mse(x, target):
-    return torch.nn.functional.mse_loss(x, target)
-
-
-class _Shade(torch.autograd.Function):
-    """col + 0.1 * (f[..., :4] + f[..., 4:]) for 8-channel features. The same values and
-    gradients as autograd through the expression (bit for bit); its backward repeats the
-    gradient into both halves in one copy, where autograd's view/sum backward makes a strided
-    copy of the expanded gradient (~0.11 ms at 8 x 1024^2)."""
+class _MSE(torch.autograd.Function):
+    """mean((x - target)^2) with a gradient for x only: the difference once (kept for the
+    backward pass) and its dot product with itself; the backward pass scales the difference.
+    Three full-size passes (the library form takes six launches and five passes)."""
 
     @staticmethod
-    def forward(ctx, col, f):
-        return col + 0.1 * (f[..., :4] + f[..., 4:])
+    def forward(ctx, x, target):
+        d = torch.sub(x, target)
+        ctx.save_for_backward(d)
+        flat = d.view(-1)
+        return torch.dot(flat, flat).div_(flat.numel())
 
     @staticmethod
     def backward(ctx, g):
-        return g, (0.1 * g).repeat(*([1] * (g.dim() - 1)), 2)
+        (d,) = ctx.saved_tensors
+        return torch.mul(d, g * (2.0 / d.numel())), None
+
+
+def _mse(x, target):
+    return _MSE.apply(x, target)
+
+
+class _Shade(torch.autograd.Function):
+    """col + 0.1 * (f[..., :4] + f[..., 4:]) for 8-channel features, in two launches: the two
+    halves summed, then scaled and added to col in one kernel; the backward pass writes 0.1 * g
+    into both halves of the feature gradient in one kernel (autograd through the expression
+    takes five launches forward and a strided copy backward)."""
+
+    @staticmethod
+    def forward(ctx, col, f):
+        return torch.add(col, f[..., :4] + f[..., 4:], alpha=0.1)
+
+    @staticmethod
+    def backward(ctx, g):
+        halves = g.unsqueeze(-2).expand(*g.shape[:-1], 2, g.shape[-1])
+        return g, torch.mul(halves, 0.1).flatten(-2)
 
 
 def make_step(w, device):

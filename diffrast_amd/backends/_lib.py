@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent.parent / "libdiffrast_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 MAX_LEVELS = 32
 
 c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -123,7 +123,7 @@ _SIGNATURES = {
     "dr_interpolate_backward": ([_P, _P, _P, _P, _P, _P, _P], ctypes.c_int),
     "dr_texture_forward": ([_P, _P, _P], ctypes.c_int),
     "dr_texture_backward": ([_P, _P, _P, _P, _P, _P, _P], ctypes.c_int),
-    "dr_mip_build": ([_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+    "dr_mip_build": ([_P, _P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
                       ctypes.c_int32, _P, _P, _P, _P], ctypes.c_int),
     "dr_mip_build_backward": ([_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64,
                                ctypes.c_int32, ctypes.c_int32, _P, _P, _P, _P], ctypes.c_int),

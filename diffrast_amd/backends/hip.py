@@ -414,32 +414,42 @@ def _level_arrays(heights, widths, offsets):
             (ctypes.c_int64 * n)(*offsets))
 
 
+def _build_chain(tex: Tensor, tables) -> tuple[Tensor, tuple]:
+    """The packed buffer [tex_batch, texels, channels] of tex and its box-filtered levels
+    (reference.py:433-519); level 0 is copied in by the pass that reads it."""
+    tex = tex.contiguous()
+    faces = 6 if tex.ndim == 5 else 1
+    heights, widths, offsets = tables
+    tex_batch, channels = tex.shape[0], tex.shape[-1]
+    total = offsets[-1] + faces * heights[-1] * widths[-1]
+    packed = tex.new_empty(tex_batch, total, channels)
+    call("dr_mip_build", ptr(packed), ptr(tex), tex_batch, channels, total, faces, len(heights),
+         *_level_arrays(heights, widths, offsets), _stream(tex))
+    return packed, (tex.shape, faces, tables, total, faces * heights[0] * widths[0])
+
+
+def _fold_chain(grad: Tensor, meta) -> Tensor:
+    """Adjoint of _build_chain, in place on the packed gradient: returns the gradient of tex (a
+    view of level 0)."""
+    shape, faces, (heights, widths, offsets), total, base = meta
+    call("dr_mip_build_backward", ptr(grad), shape[0], shape[-1], total, faces, len(heights),
+         *_level_arrays(heights, widths, offsets), _stream(grad))
+    return grad[:, :base].reshape(shape)
+
+
 class _MipChain(torch.autograd.Function):
-    """Packed buffer [tex_batch, texels, channels] of tex and its box-filtered levels; the
-    backward pass folds level gradients down into tex (reference.py:433-519)."""
+    """The packed chain of tex as a differentiable result (texture_construct_mip)."""
 
     @staticmethod
     def forward(ctx, tex, tables):
-        faces = 6 if tex.ndim == 5 else 1
-        heights, widths, offsets = tables
-        tex_batch, channels = tex.shape[0], tex.shape[-1]
-        total = offsets[-1] + faces * heights[-1] * widths[-1]
-        base = faces * heights[0] * widths[0]
-        packed = tex.new_empty(tex_batch, total, channels)
-        packed[:, :base].copy_(tex.reshape(tex_batch, base, channels))
-        call("dr_mip_build", ptr(packed), tex_batch, channels, total, faces, len(heights),
-             *_level_arrays(heights, widths, offsets), _stream(tex))
-        ctx.meta = (tex.shape, faces, tables, total, base)
+        packed, ctx.meta = _build_chain(tex, tables)
         return packed
 
     @staticmethod
     @first_order("texture")
     def backward(ctx, grad_packed):
-        shape, faces, (heights, widths, offsets), total, base = ctx.meta
-        grad = grad_packed.contiguous().clone()
-        call("dr_mip_build_backward", ptr(grad), shape[0], shape[-1], total, faces,
-             len(heights), *_level_arrays(heights, widths, offsets), _stream(grad))
-        return grad[:, :base].reshape(shape), None
+        # The incoming gradient may be shared with other consumers: fold a copy.
+        return _fold_chain(grad_packed.contiguous().clone(), ctx.meta), None
 
 
 def _mip_chain(tex: Tensor, max_mip_level: int | None):
@@ -450,39 +460,68 @@ def _mip_chain(tex: Tensor, max_mip_level: int | None):
     return _MipChain.apply(tex, tables), tables
 
 
+def _sample(ctx, texels, uv, uv_da, bias, tables, filter_mode, boundary_mode):
+    texels, uv = texels.contiguous(), uv.contiguous()
+    uv_da, bias = _dense(uv_da), _dense(bias)
+    batch, height, width = uv.shape[:3]
+    out = texels.new_empty(batch, height, width, texels.shape[-1])
+    args = _texture_args(texels, uv, uv_da, bias, tables, filter_mode, boundary_mode)
+    call("dr_texture_forward", ref(args), ptr(out), _stream(uv))
+    ctx.meta = (tables, filter_mode, boundary_mode)
+    ctx.save_for_backward(_saveable(texels), _saveable(uv), _saveable(uv_da), _saveable(bias))
+    return out
+
+
+def _sample_backward(ctx, grad_out, need_texels):
+    """(grad_texels, grad_uv, grad_uv_da, grad_bias) of a lookup; grad_texels in the packed
+    layout, accumulated from zero."""
+    texels, uv, uv_da, bias = ctx.saved_tensors
+    tables, filter_mode, boundary_mode = ctx.meta
+    need_uv, need_da, need_bias = ctx.needs_input_grad[1:4]
+    grad_texels = torch.zeros_like(texels) if need_texels else None
+    coord_grad = filter_mode != "nearest"
+    grad_uv = torch.empty_like(uv) if (need_uv and coord_grad) else None
+    grad_da = torch.empty_like(uv_da) if (need_da and uv_da is not None) else None
+    grad_bias = torch.empty_like(bias) if (need_bias and bias is not None) else None
+    if grad_texels is None and grad_uv is None and grad_da is None and grad_bias is None:
+        return None, None, None, None
+    args = _texture_args(texels, uv, uv_da, bias, tables, filter_mode, boundary_mode)
+    call("dr_texture_backward", ref(args), ptr(grad_out.contiguous()), ptr(grad_texels),
+         ptr(grad_uv), ptr(grad_da), ptr(grad_bias), _stream(uv))
+    return grad_texels, grad_uv, grad_da, grad_bias
+
+
 class _Texture(torch.autograd.Function):
-    """(reference: _triton_texture.py:429-508, reference.py:149-194, _cube.py)"""
+    """A lookup in packed texels (reference: _triton_texture.py:429-508, reference.py:149-194,
+    _cube.py)."""
 
     @staticmethod
     def forward(ctx, texels, uv, uv_da, bias, tables, filter_mode, boundary_mode):
-        texels, uv = texels.contiguous(), uv.contiguous()
-        uv_da, bias = _dense(uv_da), _dense(bias)
-        batch, height, width = uv.shape[:3]
-        out = texels.new_empty(batch, height, width, texels.shape[-1])
-        args = _texture_args(texels, uv, uv_da, bias, tables, filter_mode, boundary_mode)
-        call("dr_texture_forward", ref(args), ptr(out), _stream(uv))
-        ctx.meta = (tables, filter_mode, boundary_mode)
-        ctx.save_for_backward(_saveable(texels), _saveable(uv), _saveable(uv_da),
-                              _saveable(bias))
+        return _sample(ctx, texels, uv, uv_da, bias, tables, filter_mode, boundary_mode)
+
+    @staticmethod
+    @first_order("texture")
+    def backward(ctx, grad_out):
+        return (*_sample_backward(ctx, grad_out, ctx.needs_input_grad[0]), None, None, None)
+
+
+class _ChainTexture(torch.autograd.Function):
+    """A lookup with the mip chain of tex built in the call (mip=None): one node, so that the
+    backward pass folds the packed gradient it made itself, in place."""
+
+    @staticmethod
+    def forward(ctx, tex, uv, uv_da, bias, tables, filter_mode, boundary_mode):
+        packed, chain = _build_chain(tex, tables)
+        out = _sample(ctx, packed, uv, uv_da, bias, tables, filter_mode, boundary_mode)
+        ctx.chain = chain
         return out
 
     @staticmethod
     @first_order("texture")
     def backward(ctx, grad_out):
-        texels, uv, uv_da, bias = ctx.saved_tensors
-        tables, filter_mode, boundary_mode = ctx.meta
-        need_tex, need_uv, need_da, need_bias = ctx.needs_input_grad[:4]
-        grad_texels = torch.zeros_like(texels) if need_tex else None
-        coord_grad = filter_mode != "nearest"
-        grad_uv = torch.empty_like(uv) if (need_uv and coord_grad) else None
-        grad_da = torch.empty_like(uv_da) if (need_da and uv_da is not None) else None
-        grad_bias = torch.empty_like(bias) if (need_bias and bias is not None) else None
-        if grad_texels is None and grad_uv is None and grad_da is None and grad_bias is None:
-            return None, None, None, None, None, None, None
-        args = _texture_args(texels, uv, uv_da, bias, tables, filter_mode, boundary_mode)
-        call("dr_texture_backward", ref(args), ptr(grad_out.contiguous()), ptr(grad_texels),
-             ptr(grad_uv), ptr(grad_da), ptr(grad_bias), _stream(uv))
-        return grad_texels, grad_uv, grad_da, grad_bias, None, None, None
+        grads = _sample_backward(ctx, grad_out, ctx.needs_input_grad[0])
+        grad_tex = None if grads[0] is None else _fold_chain(grads[0], ctx.chain)
+        return grad_tex, *grads[1:], None, None, None
 
 
 def _texture_args(texels, uv, uv_da, bias, tables, filter_mode, boundary_mode):
@@ -562,7 +601,11 @@ def texture(tex: Tensor, uv: Tensor, uv_da: Tensor | None, filter_mode: str, bou
         texels, heights, widths, offsets = pack(levels)
         tables = (heights, widths, offsets)
     else:
-        texels, tables = _mip_chain(tex, max_mip_level)
+        faces = 6 if tex.ndim == 5 else 1
+        heights, widths, offsets, _ = _tables(_chain_sizes(tex.shape[-3], tex.shape[-2],
+                                                           max_mip_level), faces)
+        return _ChainTexture.apply(tex, uv, uv_da, mip_level_bias, (heights, widths, offsets),
+                                   filter_mode, boundary_mode)
     return _Texture.apply(texels, uv, uv_da, mip_level_bias, tables, filter_mode, boundary_mode)
 
 

@@ -909,24 +909,38 @@ __device__ __forceinline__ float* mip_level(float* texels, int64_t num_texels, i
   return texels + T.image * num_texels * C + (L.off[lvl] + (int64_t)T.face * L.h[lvl] * L.w[lvl]) * C;
 }
 
-// Levels k + 1 .. k + G from level k, one tile per workgroup.
-__global__ __launch_bounds__(256) void mip_down_stage(float* texels, int C, int64_t num_texels,
-                                                      int faces, MipLevels L, int k, int G) {
+// Levels k + 1 .. k + G from level k, one tile per workgroup. With `base` (k == 0 only), level
+// 0 is read from there -- [images, faces * h * w, C], the layout of level 0 on its own -- and
+// copied into the packed buffer on the way (each of its texels is read once).
+__global__ __launch_bounds__(256) void mip_down_stage(float* texels, const float* base, int C,
+                                                      int64_t num_texels, int faces,
+                                                      MipLevels L, int k, int G) {
   __shared__ float4 s_buf[2][1 << (2 * kMipStageLevels - 2)];
   const MipTile T = mip_tile(L, k, G, faces);
-  const bool vec = C == 4 && (reinterpret_cast<uintptr_t>(texels) & 15u) == 0;
+  const bool vec = C == 4 && (reinterpret_cast<uintptr_t>(texels) & 15u) == 0 &&
+                   (reinterpret_cast<uintptr_t>(base) & 15u) == 0;
   for (int c0 = 0; c0 < C; c0 += 4) {
     const int n = min(4, C - c0);
     int side = 1 << (G - 1);  // the tile's side at level k + 1
     {
-      const float* src = mip_level(texels, num_texels, C, L, T, k) + c0;
+      float* level = mip_level(texels, num_texels, C, L, T, k) + c0;
+      const float* src =
+          base ? base + (T.image * faces + T.face) * (int64_t)L.h[0] * L.w[0] * C + c0 : level;
       float* dst = mip_level(texels, num_texels, C, L, T, k + 1) + c0;
       const int64_t w = L.w[k], w1 = L.w[k + 1];
       for (int i = threadIdx.x; i < side * side; i += blockDim.x) {
         const int r = T.ty * side + i / side, c = T.tx * side + i % side;
-        const float* p = src + ((int64_t)(2 * r) * w + 2 * c) * C;
+        const int64_t at = ((int64_t)(2 * r) * w + 2 * c) * C;
+        const float* p = src + at;
         const float4 a = load_texel(p, n, vec), b = load_texel(p + C, n, vec);
         const float4 cc = load_texel(p + w * C, n, vec), d = load_texel(p + w * C + C, n, vec);
+        if (base) {
+          float* q = level + at;
+          store_texel(q, a, n, vec);
+          store_texel(q + C, b, n, vec);
+          store_texel(q + w * C, cc, n, vec);
+          store_texel(q + w * C + C, d, n, vec);
+        }
         const float4 o = quad_mean(a, b, cc, d);
         store_texel(dst + ((int64_t)r * w1 + c) * C, o, n, vec);
         s_buf[0][i] = o;
@@ -1103,21 +1117,42 @@ extern "C" int dr_texture_backward(const DrTextureArgs* a, const float* grad_out
   });
 }
 
-extern "C" int dr_mip_build(float* texels, int32_t tex_batch, int32_t channels,
-                            int64_t num_texels, int32_t faces, int32_t num_levels,
-                            const int32_t* level_height, const int32_t* level_width,
-                            const int64_t* level_offset, void* stream) {
+// Copies level 0 from its own array into the packed buffer (when no tile stage does it):
+// `count` values, base_values per batch entry of `base`, packed_values per entry of `texels`.
+__global__ __launch_bounds__(256) void mip_copy_base(float* texels, const float* base,
+                                                     int64_t packed_values, int64_t base_values,
+                                                     int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const int64_t image = i / base_values, v = i - image * base_values;
+  texels[image * packed_values + v] = base[i];
+}
+
+extern "C" int dr_mip_build(float* texels, const float* base, int32_t tex_batch,
+                            int32_t channels, int64_t num_texels, int32_t faces,
+                            int32_t num_levels, const int32_t* level_height,
+                            const int32_t* level_width, const int64_t* level_offset,
+                            void* stream) {
   if (!texels || tex_batch < 1 || channels < 1 || (faces != 1 && faces != 6) ||
       !valid_levels(num_levels, level_height, level_width, level_offset))
     return DR_ERR_ARGUMENT;
   const MipLevels L = copy_levels(num_levels, level_height, level_width, level_offset);
   const MipPlan P = mip_plan(L, num_levels);
   const int64_t images = (int64_t)tex_batch * faces;
+  const int64_t base_texels = (int64_t)faces * L.h[0] * L.w[0];
+  if (base != nullptr && base_texels > num_texels) return DR_ERR_ARGUMENT;
+  // Level 0 from `base`: the first tile stage copies it as it reads it; otherwise a copy first.
+  const bool staged_copy = base != nullptr && P.count > 0 && P.G[0] >= 2;
+  if (base != nullptr && !staged_copy) {
+    const int64_t count = (int64_t)tex_batch * base_texels * channels;
+    mip_copy_base<<<blocks_for(count, 256), 256, 0, (hipStream_t)stream>>>(
+        texels, base, num_texels * channels, base_texels * channels, count);
+  }
   for (int s = 0; s < P.count; ++s) {
     const int k = P.k[s], G = P.G[s];
     if (G >= 2) {
       mip_down_stage<<<(unsigned)stage_tiles(L, k, G, images), 256, 0, (hipStream_t)stream>>>(
-          texels, channels, num_texels, faces, L, k, G);
+          texels, s == 0 && staged_copy ? base : nullptr, channels, num_texels, faces, L, k, G);
       continue;
     }
     const int64_t count = images * L.h[k + 1] * L.w[k + 1] * channels;

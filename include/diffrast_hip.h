@@ -241,11 +241,14 @@ int dr_texture_forward(const DrTextureArgs* a, float* out, void* stream);
 int dr_texture_backward(const DrTextureArgs* a, const float* grad_out, float* grad_texels,
                         float* grad_uv, float* grad_uv_da, float* grad_bias, void* stream);
 
-/* Builds levels 1 .. num_levels-1 of the packed buffer in place from level 0, halving each
- * size (rounding up) with exact area weights (reference.py:433-488). */
-int dr_mip_build(float* texels, int32_t tex_batch, int32_t channels, int64_t num_texels,
-                 int32_t faces, int32_t num_levels, const int32_t* level_height,
-                 const int32_t* level_width, const int64_t* level_offset, void* stream);
+/* Builds levels 1 .. num_levels-1 of the packed buffer from level 0, halving each size
+ * (rounding up) with exact area weights (reference.py:433-488). base (nullable) holds level 0
+ * on its own, [tex_batch, faces * level_height[0] * level_width[0], channels]: it is copied
+ * into the packed buffer by the same pass that reads it; NULL: level 0 is there already. */
+int dr_mip_build(float* texels, const float* base, int32_t tex_batch, int32_t channels,
+                 int64_t num_texels, int32_t faces, int32_t num_levels,
+                 const int32_t* level_height, const int32_t* level_width,
+                 const int64_t* level_offset, void* stream);
 
 /* Adjoint of dr_mip_build: adds the gradient held in levels num_levels-1 .. 1 of the packed
  * gradient buffer down into level 0, in place. */

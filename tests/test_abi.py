@@ -67,6 +67,6 @@ def test_argument_checks_before_launch():
     heights = (ctypes.c_int32 * 2)(4, 3)  # 4 halves to 2, not 3
     widths = (ctypes.c_int32 * 2)(4, 2)
     offsets = (ctypes.c_int64 * 2)(0, 16)
-    assert lib.dr_mip_build(1, 1, 3, 22, 1, 2, heights, widths, offsets, None) == 1001
+    assert lib.dr_mip_build(1, None, 1, 3, 22, 1, 2, heights, widths, offsets, None) == 1001
     with pytest.raises(RuntimeError, match="invalid argument"):
         _lib.check(1001, "probe")

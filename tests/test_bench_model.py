@@ -57,7 +57,7 @@ def test_headline_op_bytes():
         "interp bwd": [("dr_interpolate_backward", (ctypes.byref(_interp(8, 0)),)),
                        ("dr_interpolate_backward", (ctypes.byref(_interp(2, 2)),))],
         "tex fwd": [("dr_texture_forward", (ctypes.byref(_texture()),)),
-                    ("dr_mip_build", (None, 1, 4, 1_398_101, 1, 11, levels, levels))],
+                    ("dr_mip_build", (None, None, 1, 4, 1_398_101, 1, 11, levels, levels))],
         "tex bwd": [("dr_texture_backward", (ctypes.byref(_texture()),)),
                     ("dr_mip_build_backward", (None, 1, 4, 1_398_101, 1, 11, levels, levels))],
         "aa fwd": [("dr_antialias_forward", (ctypes.byref(_aa()),))],
