@@ -1,7 +1,8 @@
-"""Depth peeling (reference: peeling.py:1-92).
+"""Depth peeling (the reference's src/diffrast/peeling.py API: ``DepthPeeler``).
 
-Each layer is one backend call carrying the previous layer's 64-bit visibility keys. In range
-mode all items are peeled together in one launch per layer, rather than one call per item.
+A layer is one backend call that carries the previous layer's per-pixel state -- here the 64-bit
+visibility keys -- and keeps keys strictly behind it. Range mode peels every item of the batch in
+the same call.
 """
 
 from __future__ import annotations
@@ -14,17 +15,21 @@ from diffrast_amd.backends import get_backend
 from diffrast_amd.context import RasterizeContext
 from diffrast_amd.ops import check_rasterize_inputs
 
+_CLOSED = ("This DepthPeeler was closed when its with block exited; create a new one to "
+           "rasterize more layers.")
+
 
 class DepthPeeler:
-    """Rasterize successive depth layers of the same geometry.
+    """Successive depth layers of one geometry, nearest first.
 
-    The first :meth:`rasterize_next_layer` equals :func:`rasterize`; each later call gives, per
-    pixel, the nearest triangle behind the previous one, ordered by depth and then by index, so
-    triangles at exactly equal depth come in index order. Layers have the format of
-    :func:`rasterize` and pass gradients to ``pos``. Arguments are as for :func:`rasterize`,
-    including range mode. The peeler copies ``pos``, ``tri`` and ``ranges``, so later edits of
-    those tensors do not mix geometries; gradients still reach the ``pos`` passed in. After its
-    ``with`` block it raises::
+    The first :meth:`rasterize_next_layer` is :func:`diffrast_amd.rasterize`'s result; each
+    later one holds, per pixel, the nearest triangle behind the previous layer's, in order of
+    depth and then of triangle index (equal depths come in index order), and stays empty where
+    none is left. Layers have :func:`diffrast_amd.rasterize`'s format and pass gradients back to
+    ``pos``. The arguments are :func:`diffrast_amd.rasterize`'s, range mode included. The peeler
+    works on copies of ``pos``, ``tri`` and ``ranges`` taken when it is made, so later edits of
+    those tensors do not reach it (gradients still reach the ``pos`` given). Used as a context
+    manager, it refuses further layers after its block::
 
         with dr.DepthPeeler(glctx, pos, tri, (512, 512)) as peeler:
             for _ in range(num_layers):
@@ -36,35 +41,33 @@ class DepthPeeler:
                  grad_db: bool = True) -> None:
         self._resolution = check_rasterize_inputs(glctx, pos, tri, resolution, ranges)
         self._output_db = getattr(glctx, "output_db", True)
-        self._grad_db = grad_db and self._output_db
-        self._pos, self._tri = pos.clone(), tri.clone()
-        self._ranges = ranges.clone() if pos.ndim == 2 else None
-        # The per-pixel state belongs to the backend that made it.
+        self._grad_db = bool(grad_db) and self._output_db
+        self._geometry = (pos.clone(), tri.clone(), ranges.clone() if pos.ndim == 2 else None)
+        # The per-pixel state belongs to the backend that made it: the backend is fixed now.
         self._backend = get_backend(pos.device, "rasterize")
         self._state = None
-        self._closed = False
+        self._open = True
 
     def __enter__(self) -> DepthPeeler:
         return self
 
     def __exit__(self, exc_type: type[BaseException] | None, exc_value: BaseException | None,
                  traceback: TracebackType | None) -> None:
+        self._open = False
         self._state = None
-        self._closed = True
 
     def rasterize_next_layer(self) -> tuple[Tensor, Tensor]:
-        """``(rast, rast_db)`` of the next depth layer."""
-        if self._closed:
-            raise RuntimeError(
-                "This DepthPeeler was closed when its with block exited; create a new one to "
-                "rasterize more layers."
-            )
-        if self._ranges is None:
-            rast, rast_db, self._state = self._backend.rasterize_layer(
-                self._pos, self._tri, self._resolution, self._grad_db, self._state
-            )
+        """``(rast, rast_db)`` of the next layer."""
+        if not self._open:
+            raise RuntimeError(_CLOSED)
+        pos, tri, ranges = self._geometry
+        if ranges is None:
+            rast, rast_db, state = self._backend.rasterize_layer(
+                pos, tri, self._resolution, self._grad_db, self._state)
         else:
-            rast, rast_db, self._state = self._backend.rasterize_ranges(
-                self._pos, self._tri, self._resolution, self._grad_db, self._ranges, self._state
-            )
-        return rast, (rast_db if self._output_db else rast.new_zeros(*rast.shape[:3], 0))
+            rast, rast_db, state = self._backend.rasterize_ranges(
+                pos, tri, self._resolution, self._grad_db, ranges, self._state)
+        self._state = state
+        if not self._output_db:
+            rast_db = rast.new_zeros(*rast.shape[:3], 0)
+        return rast, rast_db
