@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent.parent / "libdiffrast_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 MAX_LEVELS = 32
 
 c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -135,6 +135,22 @@ _SIGNATURES = {
     "dr_antialias_workspace_size": ([_P, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "dr_antialias_forward": ([_P, _P, ctypes.c_size_t, _P, _P], ctypes.c_int),
     "dr_antialias_backward": ([_P, _P, ctypes.c_size_t, _P, _P, _P, _P], ctypes.c_int),
+    "dr_resolve_forward_f64": ([_P, _P, _P, _P, _P], ctypes.c_int),
+    "dr_resolve_backward_f64": ([_P, _P, _P, _P, _P, _P], ctypes.c_int),
+    "dr_interpolate_forward_f64": ([_P, _P, _P, _P], ctypes.c_int),
+    "dr_interpolate_backward_f64": ([_P, _P, _P, _P, _P, _P, _P], ctypes.c_int),
+    "dr_texture_forward_f64": ([_P, _P, _P], ctypes.c_int),
+    "dr_texture_backward_f64": ([_P, _P, _P, _P, _P, _P, _P], ctypes.c_int),
+    "dr_mip_build_f64": ([_P, _P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64,
+                          ctypes.c_int32, ctypes.c_int32, _P, _P, _P, _P], ctypes.c_int),
+    "dr_mip_build_backward_f64": ([_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64,
+                                   ctypes.c_int32, ctypes.c_int32, _P, _P, _P, _P],
+                                  ctypes.c_int),
+    "dr_silhouette_mask_f64": ([_P, ctypes.c_int64, ctypes.c_int32, _P, ctypes.c_int32, _P, _P,
+                                _P], ctypes.c_int),
+    "dr_antialias_workspace_size_f64": ([_P, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+    "dr_antialias_forward_f64": ([_P, _P, ctypes.c_size_t, _P, _P], ctypes.c_int),
+    "dr_antialias_backward_f64": ([_P, _P, ctypes.c_size_t, _P, _P, _P, _P], ctypes.c_int),
 }
 EXPORTS = tuple(_SIGNATURES)
 

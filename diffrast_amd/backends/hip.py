@@ -43,6 +43,23 @@ def _require(name: str, t: Tensor | None, dtype: torch.dtype) -> None:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}.")
 
 
+def _real(*named: tuple[str, Tensor | None]) -> torch.dtype:
+    """The one floating type of the given tensors: float32 (the product kernels) or float64
+    (their gradient-check twins, as the reference's GPU backend accepts at this level)."""
+    first = next((t for _, t in named if t is not None), None)
+    dtype = torch.float32 if first is None else first.dtype
+    if dtype not in (torch.float32, torch.float64):
+        dtype = torch.float32  # names the first tensor below
+    for name, t in named:
+        _require(name, t, dtype)
+    return dtype
+
+
+def _entry(name: str, t: Tensor) -> str:
+    """The C-ABI entry point for computing in t's type: name, or its float64 twin."""
+    return name + "_f64" if t.dtype == torch.float64 else name
+
+
 def _dense(t: Tensor | None) -> Tensor | None:
     return None if t is None else t.contiguous()
 
@@ -219,7 +236,7 @@ class _Resolve(torch.autograd.Function):
         batch, height, width = geo.shape
         rast = pos.new_empty(batch, height, width, 4)
         rast_db = pos.new_empty(batch, height, width, 4)
-        call("dr_resolve_forward", ref(geo.struct), ptr(keys), ptr(rast), ptr(rast_db),
+        call(_entry("dr_resolve_forward", pos), ref(geo.struct), ptr(keys), ptr(rast), ptr(rast_db),
              _stream(pos))
         ctx.geo = geo
         ctx.grad_db = grad_db
@@ -242,7 +259,7 @@ class _Resolve(torch.autograd.Function):
         # The geometry points at the forward's tensors, which are still alive (saved).
         struct = _lib.RasterGeometry.from_buffer_copy(geo.struct)
         struct.pos = ptr(pos)
-        call("dr_resolve_backward", ref(struct), ptr(keys), ptr(grad_rast.contiguous()),
+        call(_entry("dr_resolve_backward", pos), ref(struct), ptr(keys), ptr(grad_rast.contiguous()),
              ptr(grad_db), ptr(grad_pos), _stream(pos))
         return grad_pos, None, None, None
 
@@ -251,6 +268,12 @@ def _empty_layer(pos: Tensor, batch: int, resolution) -> tuple[Tensor, Tensor, T
     empty = pos.new_zeros(batch, *resolution, 4)
     keys = torch.full((batch, *resolution), EMPTY_KEY, dtype=torch.int64, device=pos.device)
     return empty, empty.clone(), keys
+
+
+def _single(geo: _Geometry, pos: Tensor, make) -> _Geometry:
+    """The geometry visibility runs on: float32 positions (a float32 copy of float64 ones: as in
+    the reference's GPU backend, visibility is float32 and only the resolve follows pos)."""
+    return geo if pos.dtype == torch.float32 else make(pos.float())
 
 
 def rasterize(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad_db: bool):
@@ -263,14 +286,14 @@ def rasterize_layer(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad_
                     previous: Tensor | None):
     """One depth layer behind ``previous`` (the keys returned for the layer before) and its
     keys (reference: triton.py:21-40, reference.py:45-66)."""
-    _require("pos", pos, torch.float32)
+    _real(("pos", pos))
     _require("tri", tri, torch.int32)
     _require("previous", previous, torch.int64)
     if tri.shape[0] == 0 or pos.shape[0] == 0:
         return _empty_layer(pos, pos.shape[0], resolution)
     pos, tri = pos.contiguous(), tri.contiguous()
     geo = _Geometry(pos, tri, resolution)
-    keys = _visibility(geo, previous)
+    keys = _visibility(_single(geo, pos, lambda p: _Geometry(p, tri, resolution)), previous)
     rast, rast_db = _Resolve.apply(pos, keys, geo, grad_db)
     return rast, rast_db, keys
 
@@ -280,7 +303,7 @@ def rasterize_ranges(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad
     """Range mode in one launch: image i draws ``tri[start_i : start_i + count_i]`` of the
     shared ``pos`` ([vertices, 4]); ids count from the start of ``tri``, as after the
     reference's join_ranges (ops.py:490-508). Returns ``(rast, rast_db, keys)``."""
-    _require("pos", pos, torch.float32)
+    _real(("pos", pos))
     _require("tri", tri, torch.int32)
     _require("previous", previous, torch.int64)
     table = [(int(s), int(c)) for s, c in ranges.tolist()]
@@ -297,9 +320,12 @@ def rasterize_ranges(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad
     pos, tri = pos.contiguous(), tri.contiguous()
     ranges_dev = torch.tensor(table, dtype=torch.int32).to(device, non_blocking=True)
     prefix_dev = torch.tensor(prefix, dtype=torch.int64).to(device, non_blocking=True)
-    geo = _Geometry(pos, tri, resolution, ranges=ranges_dev, range_prefix=prefix_dev,
-                    batch=batch, num_instances=prefix[-1])
-    keys = _visibility(geo, previous)
+    def geometry(p):
+        return _Geometry(p, tri, resolution, ranges=ranges_dev, range_prefix=prefix_dev,
+                         batch=batch, num_instances=prefix[-1])
+
+    geo = geometry(pos)
+    keys = _visibility(_single(geo, pos, geometry), previous)
     rast, rast_db = _Resolve.apply(pos, keys, geo, grad_db)
     return rast, rast_db, keys
 
@@ -345,7 +371,7 @@ class _Interpolate(torch.autograd.Function):
         out = attr.new_empty(batch, height, width, attr.shape[-1])
         out_da = attr.new_empty(batch, height, width, 2 * len(diff))
         args = _interp_args(attr, rast, rast_db, tri, diff_dev, len(diff))
-        call("dr_interpolate_forward", ref(args), ptr(out), ptr(out_da) if diff else None,
+        call(_entry("dr_interpolate_forward", attr), ref(args), ptr(out), ptr(out_da) if diff else None,
              _stream(rast))
         ctx.diff = diff
         ctx.save_for_backward(_saveable(attr), _saveable(rast), _saveable(rast_db), tri,
@@ -370,7 +396,7 @@ class _Interpolate(torch.autograd.Function):
         grad_rast = torch.empty_like(rast) if need_rast else None
         grad_db = torch.empty_like(rast_db) if (need_db and diff) else None
         args = _interp_args(attr, rast, rast_db, tri, diff_dev, len(diff))
-        call("dr_interpolate_backward", ref(args), ptr(grad_out), ptr(grad_da), ptr(grad_attr),
+        call(_entry("dr_interpolate_backward", attr), ref(args), ptr(grad_out), ptr(grad_da), ptr(grad_attr),
              ptr(grad_rast), ptr(grad_db), _stream(rast))
         return grad_attr, grad_rast, grad_db, None, None
 
@@ -378,8 +404,7 @@ class _Interpolate(torch.autograd.Function):
 def interpolate(attr: Tensor, rast: Tensor, tri: Tensor, rast_db: Tensor | None,
                 diff_attrs: Sequence[int]):
     """(reference: triton.py:50-56)"""
-    for name, t in (("attr", attr), ("rast", rast), ("rast_db", rast_db)):
-        _require(name, t, torch.float32)
+    _real(("attr", attr), ("rast", rast), ("rast_db", rast_db))
     _require("tri", tri, torch.int32)
     return _Interpolate.apply(attr, rast, rast_db, tri, tuple(int(c) for c in diff_attrs))
 
@@ -423,7 +448,8 @@ def _build_chain(tex: Tensor, tables) -> tuple[Tensor, tuple]:
     tex_batch, channels = tex.shape[0], tex.shape[-1]
     total = offsets[-1] + faces * heights[-1] * widths[-1]
     packed = tex.new_empty(tex_batch, total, channels)
-    call("dr_mip_build", ptr(packed), ptr(tex), tex_batch, channels, total, faces, len(heights),
+    call(_entry("dr_mip_build", tex), ptr(packed), ptr(tex), tex_batch, channels, total, faces,
+         len(heights),
          *_level_arrays(heights, widths, offsets), _stream(tex))
     return packed, (tex.shape, faces, tables, total, faces * heights[0] * widths[0])
 
@@ -432,7 +458,8 @@ def _fold_chain(grad: Tensor, meta) -> Tensor:
     """Adjoint of _build_chain, in place on the packed gradient: returns the gradient of tex (a
     view of level 0)."""
     shape, faces, (heights, widths, offsets), total, base = meta
-    call("dr_mip_build_backward", ptr(grad), shape[0], shape[-1], total, faces, len(heights),
+    call(_entry("dr_mip_build_backward", grad), ptr(grad), shape[0], shape[-1], total, faces,
+         len(heights),
          *_level_arrays(heights, widths, offsets), _stream(grad))
     return grad[:, :base].reshape(shape)
 
@@ -466,7 +493,7 @@ def _sample(ctx, texels, uv, uv_da, bias, tables, filter_mode, boundary_mode):
     batch, height, width = uv.shape[:3]
     out = texels.new_empty(batch, height, width, texels.shape[-1])
     args = _texture_args(texels, uv, uv_da, bias, tables, filter_mode, boundary_mode)
-    call("dr_texture_forward", ref(args), ptr(out), _stream(uv))
+    call(_entry("dr_texture_forward", texels), ref(args), ptr(out), _stream(uv))
     ctx.meta = (tables, filter_mode, boundary_mode)
     ctx.save_for_backward(_saveable(texels), _saveable(uv), _saveable(uv_da), _saveable(bias))
     return out
@@ -486,7 +513,8 @@ def _sample_backward(ctx, grad_out, need_texels):
     if grad_texels is None and grad_uv is None and grad_da is None and grad_bias is None:
         return None, None, None, None
     args = _texture_args(texels, uv, uv_da, bias, tables, filter_mode, boundary_mode)
-    call("dr_texture_backward", ref(args), ptr(grad_out.contiguous()), ptr(grad_texels),
+    call(_entry("dr_texture_backward", texels), ref(args), ptr(grad_out.contiguous()),
+         ptr(grad_texels),
          ptr(grad_uv), ptr(grad_da), ptr(grad_bias), _stream(uv))
     return grad_texels, grad_uv, grad_da, grad_bias
 
@@ -566,7 +594,7 @@ def pack(levels: Sequence[Tensor]):
 def texture_construct_mip(tex: Tensor, max_mip_level: int | None) -> list[Tensor]:
     """Mip levels 1 and up of ``tex`` as views of one packed buffer, differentiable with
     respect to ``tex`` (reference.py:197-199)."""
-    _require("tex", tex, torch.float32)
+    _real(("tex", tex))
     packed, (heights, widths, offsets) = _mip_chain(tex, max_mip_level)
     faces = 6 if tex.ndim == 5 else 1
     levels = []
@@ -581,10 +609,9 @@ def texture(tex: Tensor, uv: Tensor, uv_da: Tensor | None, filter_mode: str, bou
             max_mip_level: int | None, mip_level_bias: Tensor | None = None,
             mip: Sequence[Tensor] | None = None, packed=None):
     """(reference: triton.py:59-79, reference.py:149-194)"""
-    for name, t in (("tex", tex), ("uv", uv), ("uv_da", uv_da), ("mip_level_bias", mip_level_bias),
-                    *((f"mip[{k}]", m) for k, m in enumerate(mip or ())),
-                    ("packed texels", None if packed is None else packed[0])):
-        _require(name, t, torch.float32)
+    _real(("tex", tex), ("uv", uv), ("uv_da", uv_da), ("mip_level_bias", mip_level_bias),
+          *((f"mip[{k}]", m) for k, m in enumerate(mip or ())),
+          ("packed texels", None if packed is None else packed[0]))
     mipmapped = "mipmap" in filter_mode
     if not mipmapped:
         faces = 6 if boundary_mode == "cube" else 1
@@ -638,6 +665,10 @@ def silhouette_mask(pos: Tensor, tri: Tensor, neighbours: Tensor,
     pos3 = pos3.contiguous()
     mask = torch.empty(pos3.shape[0], tri.shape[0], dtype=torch.uint8, device=pos.device)
     batch, height, width = (0, 1, 1) if rast is None else rast.shape[:3]
+    if pos3.dtype == torch.float64:  # every triangle's bits, from the float64 positions
+        call("dr_silhouette_mask_f64", ptr(pos3), pos3.shape[1] * 4, pos3.shape[0], ptr(tri),
+             tri.shape[0], ptr(neighbours), ptr(mask), _stream(pos))
+        return mask
     if rast is not None:
         rast = rast.contiguous()
     call("dr_silhouette_mask", ptr(pos3), pos3.shape[1] * 4, pos3.shape[0], ptr(tri),
@@ -667,9 +698,9 @@ class _Antialias(torch.autograd.Function):
         out = torch.empty_like(color)
         args = _aa_args(color, rast, pos, tri, mask, boost)
         size = ctypes.c_size_t()
-        call("dr_antialias_workspace_size", ref(args), ctypes.byref(size))
+        call(_entry("dr_antialias_workspace_size", color), ref(args), ctypes.byref(size))
         pairs = torch.empty(max(size.value, 1), dtype=torch.uint8, device=color.device)
-        call("dr_antialias_forward", ref(args), ptr(pairs), size.value, ptr(out),
+        call(_entry("dr_antialias_forward", color), ref(args), ptr(pairs), size.value, ptr(out),
              _stream(color))
         ctx.boost = boost
         ctx.save_for_backward(_saveable(color), _saveable(rast), _saveable(pos), tri, mask, pairs)
@@ -685,7 +716,7 @@ class _Antialias(torch.autograd.Function):
         if grad_color is None and grad_pos is None:
             return None, None, None, None, None, None
         args = _aa_args(color, rast, pos, tri, mask, ctx.boost)
-        call("dr_antialias_backward", ref(args), ptr(pairs), pairs.numel(),
+        call(_entry("dr_antialias_backward", color), ref(args), ptr(pairs), pairs.numel(),
              ptr(grad_out.contiguous()), ptr(grad_color), ptr(grad_pos), _stream(color))
         return grad_color, None, grad_pos, None, None, None
 
@@ -693,8 +724,7 @@ class _Antialias(torch.autograd.Function):
 def antialias(color: Tensor, rast: Tensor, pos: Tensor, tri: Tensor, pos_gradient_boost: float,
               neighbours: Tensor | None = None) -> Tensor:
     """(reference: triton.py:82-92, reference.py:202-265)"""
-    for name, t in (("color", color), ("rast", rast), ("pos", pos)):
-        _require(name, t, torch.float32)
+    _real(("color", color), ("rast", rast), ("pos", pos))
     _require("tri", tri, torch.int32)
     if tri.shape[0] == 0:
         return color.clone()

@@ -18,265 +18,17 @@
 #include <type_traits>
 
 #include "common.h"
+#include "texture_math.h"
 
 namespace dr {
 namespace {
 
-constexpr float kFootprintLimit = 1e18f;  // reference.py:402
-constexpr float kDerivativeLimit = 1e18f; // _cube.py:36
-constexpr float kMinFootprint = 1e-30f;   // reference.py:501
-constexpr float kLn2 = 0.693147180559945309f;
-
-// ---- cube geometry (_cube.py) -----------------------------------------------------------
-
-// Per face: major axis, s axis and t axis as integer 3-vectors (_cube.py:31-33).
-__constant__ int kMajor[6][3] = {{1, 0, 0}, {-1, 0, 0}, {0, 1, 0}, {0, -1, 0}, {0, 0, 1}, {0, 0, -1}};
-__constant__ int kSAxis[6][3] = {{0, 0, -1}, {0, 0, 1}, {1, 0, 0}, {1, 0, 0}, {1, 0, 0}, {-1, 0, 0}};
-__constant__ int kTAxis[6][3] = {{0, -1, 0}, {0, -1, 0}, {0, 0, 1}, {0, 0, -1}, {0, -1, 0}, {0, -1, 0}};
-
-__device__ __forceinline__ int floor_div2(int v) { return v >= 0 ? v / 2 : -((-v + 1) / 2); }
-
-// Fold a texel one step outside its face onto the neighbouring face (_cube.py:105-143).
-// Returns false beyond a corner, where no texel exists.
-__device__ __forceinline__ bool cube_fold(int& face, int& row, int& col, int size) {
-  const bool over_col = col < 0 || col >= size;
-  const bool over_row = row < 0 || row >= size;
-  const int sc = 2 * col + 1 - size, tc = 2 * row + 1 - size;
-  int point[3];
-#pragma unroll
-  for (int k = 0; k < 3; ++k) {
-    int p = size * kMajor[face][k] + sc * kSAxis[face][k] + tc * kTAxis[face][k];
-    p = min(max(p, -size), size);
-    if (over_col || over_row) p -= kMajor[face][k];
-    point[k] = p;
-  }
-  int axis = 0;
-  int best = abs(point[0]);
-  if (abs(point[1]) > best) { axis = 1; best = abs(point[1]); }
-  if (abs(point[2]) > best) axis = 2;
-  face = 2 * axis + (point[axis] < 0 ? 1 : 0);
-  int s_dot = 0, t_dot = 0;
-#pragma unroll
-  for (int k = 0; k < 3; ++k) {
-    s_dot += point[k] * kSAxis[face][k];
-    t_dot += point[k] * kTAxis[face][k];
-  }
-  col = max(floor_div2(s_dot + size - 1), 0);
-  row = max(floor_div2(t_dot + size - 1), 0);
-  return !(over_col && over_row);
-}
-
-struct CubeProj {
-  bool valid, undefined;
-  int face;
-  float length, ma, rs, rt;
-  float dn[3];
-  float da[3][2];       // clamped, scaled derivatives
-  bool da_pass[3][2];   // inside the clamp
-  float d_ma[2], d_sc[2], d_tc[2];
-  float st[2];
-  float st_da[4];       // ds/dx, ds/dy, dt/dx, dt/dy
-};
-
-// Face selection and face coordinates of a direction (_cube.py:44-102).
-__device__ __forceinline__ void cube_project(const float* dir, const float* dir_da, CubeProj& P) {
-  float d[3] = {dir[0], dir[1], dir[2]};
-  const float ax0 = fabsf(d[0]), ay0 = fabsf(d[1]), az0 = fabsf(d[2]);
-  P.valid = isfinite(d[0]) && isfinite(d[1]) && isfinite(d[2]) &&
-            fmaxf(fmaxf(ax0, ay0), az0) >= 1.17549435e-38f;
-  if (!P.valid) {
-    d[0] = 0.0f;
-    d[1] = 0.0f;
-    d[2] = 1.0f;
-  }
-  const float ax = fabsf(d[0]), ay = fabsf(d[1]), az = fabsf(d[2]);
-  const bool x_major = ax >= ay && ax >= az;
-  const bool y_major = !x_major && ay >= az;
-  const int axis = x_major ? 0 : (y_major ? 1 : 2);
-  P.face = 2 * axis + (d[axis] < 0.0f ? 1 : 0);
-  P.length = fmaxf(fmaxf(ax, ay), az);
-#pragma unroll
-  for (int k = 0; k < 3; ++k) P.dn[k] = d[k] / P.length;
-  const int* M = kMajor[P.face];
-  const int* S = kSAxis[P.face];
-  const int* T = kTAxis[P.face];
-  P.ma = P.dn[0] * (float)M[0] + P.dn[1] * (float)M[1] + P.dn[2] * (float)M[2];
-  const float sc = P.dn[0] * (float)S[0] + P.dn[1] * (float)S[1] + P.dn[2] * (float)S[2];
-  const float tc = P.dn[0] * (float)T[0] + P.dn[1] * (float)T[1] + P.dn[2] * (float)T[2];
-  P.rs = sc / P.ma;
-  P.rt = tc / P.ma;
-  P.st[0] = 0.5f * (P.rs + 1.0f);
-  P.st[1] = 0.5f * (P.rt + 1.0f);
-  P.undefined = false;
-  if (dir_da == nullptr) return;
-  bool any_nan = false;
-  for (int i = 0; i < 6; ++i) any_nan = any_nan || isnan(dir_da[i]);
-  P.undefined = P.valid && any_nan;
-  const bool use = P.valid && !P.undefined;
-#pragma unroll
-  for (int k = 0; k < 3; ++k)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const float v = (use ? dir_da[2 * k + j] : 0.0f) / P.length;
-      P.da_pass[k][j] = v >= -kDerivativeLimit && v <= kDerivativeLimit;
-      P.da[k][j] = fminf(fmaxf(v, -kDerivativeLimit), kDerivativeLimit);
-    }
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    P.d_ma[j] = P.da[0][j] * (float)M[0] + P.da[1][j] * (float)M[1] + P.da[2][j] * (float)M[2];
-    P.d_sc[j] = P.da[0][j] * (float)S[0] + P.da[1][j] * (float)S[1] + P.da[2][j] * (float)S[2];
-    P.d_tc[j] = P.da[0][j] * (float)T[0] + P.da[1][j] * (float)T[1] + P.da[2][j] * (float)T[2];
-  }
-  const float nan = __int_as_float(0x7fc00000);
-  P.st_da[0] = P.undefined ? nan : 0.5f * (P.d_sc[0] - P.rs * P.d_ma[0]) / P.ma;
-  P.st_da[1] = P.undefined ? nan : 0.5f * (P.d_sc[1] - P.rs * P.d_ma[1]) / P.ma;
-  P.st_da[2] = P.undefined ? nan : 0.5f * (P.d_tc[0] - P.rt * P.d_ma[0]) / P.ma;
-  P.st_da[3] = P.undefined ? nan : 0.5f * (P.d_tc[1] - P.rt * P.d_ma[1]) / P.ma;
-}
-
-// Gradient of cube_project: from d(loss)/d(st) and d(loss)/d(st_da) to the direction and
-// its derivatives (3 and 6 values); g_sda is used when use_sda is set.
-__device__ __forceinline__ void cube_project_backward(const CubeProj& P, float g_s, float g_t,
-                                                      bool use_sda, const float (&g_sda)[4],
-                                                      float (&grad_dir)[3],
-                                                      float (&grad_dir_da)[6]) {
-  const int* M = kMajor[P.face];
-  const int* S = kSAxis[P.face];
-  const int* T = kTAxis[P.face];
-  float g_rs = 0.5f * g_s, g_rt = 0.5f * g_t, g_ma = 0.0f;
-  float g_dsc[2] = {0.f, 0.f}, g_dtc[2] = {0.f, 0.f}, g_dma[2] = {0.f, 0.f};
-  if (use_sda && !P.undefined) {
-    const float gds[2] = {g_sda[0], g_sda[1]}, gdt[2] = {g_sda[2], g_sda[3]};
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const float ds = P.st_da[j], dt = P.st_da[2 + j];
-      g_rs += gds[j] * (-0.5f * P.d_ma[j] / P.ma);
-      g_rt += gdt[j] * (-0.5f * P.d_ma[j] / P.ma);
-      g_ma -= (gds[j] * ds + gdt[j] * dt) / P.ma;
-      g_dsc[j] = 0.5f * gds[j] / P.ma;
-      g_dtc[j] = 0.5f * gdt[j] / P.ma;
-      g_dma[j] = -0.5f * (gds[j] * P.rs + gdt[j] * P.rt) / P.ma;
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < 3; ++k)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float g = g_dsc[j] * (float)S[k] + g_dtc[j] * (float)T[k] + g_dma[j] * (float)M[k];
-      g = (P.valid && !P.undefined && P.da_pass[k][j]) ? g / P.length : 0.0f;
-      grad_dir_da[2 * k + j] = g;
-    }
-  g_ma -= (g_rs * P.rs + g_rt * P.rt) / P.ma;
-#pragma unroll
-  for (int k = 0; k < 3; ++k) {
-    const float g_dn = (g_rs * (float)S[k] + g_rt * (float)T[k]) / P.ma + g_ma * (float)M[k];
-    grad_dir[k] = P.valid ? g_dn / P.length : 0.0f;
-  }
-}
-
-// ---- 2D coordinates, taps and levels ----------------------------------------------------
-
-struct Axis {
-  float x;     // continuous texel coordinate
-  bool bad;    // not finite (then x = 0)
-  bool pass;   // gradient reaches the input coordinate
-};
-
-// coord * size - shift, wrapped or saturated as for the boundary (reference.py:615-633).
-__device__ __forceinline__ Axis texel_axis(float coord, int size, float shift, int boundary) {
-  Axis A;
-  float c = coord;
-  if (boundary == DR_BOUNDARY_WRAP) c = c - floorf(c);
-  A.x = c * (float)size - shift;
-  A.pass = true;
-  if (boundary == DR_BOUNDARY_CLAMP || boundary == DR_BOUNDARY_ZERO) {
-    if (A.x < -1.0f) { A.x = -1.0f; A.pass = false; }
-    if (A.x > (float)size) { A.x = (float)size; A.pass = false; }
-  }
-  A.bad = !isfinite(A.x);
-  if (A.bad) {
-    A.x = 0.0f;
-    A.pass = false;
-  }
-  return A;
-}
-
-// i mod n (non-negative). Tap positions come from coordinates already wrapped into [0, 1], so
-// they lie in [-1, n]: one add or subtract; the division is left for anything else.
-__device__ __forceinline__ int wrap_index(int i, int n) {
-  int r = i < 0 ? i + n : (i >= n ? i - n : i);
-  if (r < 0 || r >= n) {
-    r = i % n;
-    r = r < 0 ? r + n : r;
-  }
-  return r;
-}
-
-// Texel index (in texels from the start of the image's packed buffer) of integer tap
-// (row, col) of a level; false when the tap reads zero (reference.py:636-672).
-__device__ __forceinline__ bool tap(int row, int col, int face, int h, int w, int64_t offset,
-                                    int boundary, int64_t& index) {
-  bool valid = true;
-  if (boundary == DR_BOUNDARY_CUBE) {
-    valid = cube_fold(face, row, col, w);
-  } else if (boundary == DR_BOUNDARY_WRAP) {
-    row = wrap_index(row, h);
-    col = wrap_index(col, w);
-  } else {
-    if (boundary == DR_BOUNDARY_ZERO) valid = row >= 0 && row < h && col >= 0 && col < w;
-    row = min(max(row, 0), h - 1);
-    col = min(max(col, 0), w - 1);
-  }
-  if (face >= 0) row += face * h;
-  index = offset + (int64_t)row * w + col;
-  return valid;
-}
-
-struct Bilinear {
-  int64_t index[4];
-  bool valid[4];
-  float fx, fy;
-  bool bad;
-  bool pass_x, pass_y;
-  float size_x, size_y;
-  // Cube corners: taps beyond two edges count as the mean of the other three.
-  bool cube;
-  float corner[4];  // 1 where (left|right) & (above|below) for taps 00, 01, 10, 11
-};
-
-__device__ __forceinline__ Bilinear bilinear_setup(float s, float t, int face, int h, int w,
-                                                   int64_t offset, int boundary) {
-  Bilinear L;
-  const Axis X = texel_axis(s, w, 0.5f, boundary);
-  const Axis Y = texel_axis(t, h, 0.5f, boundary);
-  const float x0 = floorf(X.x), y0 = floorf(Y.x);
-  L.fx = X.x - x0;
-  L.fy = Y.x - y0;
-  L.bad = X.bad || Y.bad;
-  L.pass_x = X.pass;
-  L.pass_y = Y.pass;
-  L.size_x = (float)w;
-  L.size_y = (float)h;
-  const int col = (int)x0, row = (int)y0;
-  L.valid[0] = tap(row, col, face, h, w, offset, boundary, L.index[0]);
-  L.valid[1] = tap(row, col + 1, face, h, w, offset, boundary, L.index[1]);
-  L.valid[2] = tap(row + 1, col, face, h, w, offset, boundary, L.index[2]);
-  L.valid[3] = tap(row + 1, col + 1, face, h, w, offset, boundary, L.index[3]);
-  L.cube = boundary == DR_BOUNDARY_CUBE;
-  if (L.cube) {
-    const bool left = col < 0, right = col + 1 >= w, above = row < 0, below = row + 1 >= h;
-    L.corner[0] = (left && above) ? 1.0f : 0.0f;
-    L.corner[1] = (right && above) ? 1.0f : 0.0f;
-    L.corner[2] = (left && below) ? 1.0f : 0.0f;
-    L.corner[3] = (right && below) ? 1.0f : 0.0f;
-  }
-  return L;
-}
+using namespace tex;
 
 // Channels [c0, c0 + N) of the four taps (0 past C or for an invalid tap), all loads issued
 // together.
 template <int N>
-__device__ __forceinline__ void fetch_taps(const float* __restrict__ texels, const Bilinear& L,
+__device__ __forceinline__ void fetch_taps(const float* __restrict__ texels, const Bilinear<float>& L,
                                            int C, int c0, float (&t)[4][N]) {
   if constexpr (N == 4) {
     // Four-channel texels on a 16-byte aligned buffer: one 16-byte load per tap.
@@ -307,196 +59,6 @@ __device__ __forceinline__ void tap_column(const float (&t)[4][N], int c, float 
   for (int k = 0; k < 4; ++k) out[k] = t[k][c];
 }
 
-// Value of one channel (reference.py:601-611).
-__device__ __forceinline__ float bilinear_value(const Bilinear& L, const float (&t)[4]) {
-  const float fx = L.fx, fy = L.fy;
-  float out = (1.0f - fy) * ((1.0f - fx) * t[0] + fx * t[1]) +
-              fy * ((1.0f - fx) * t[2] + fx * t[3]);
-  if (L.cube) {
-    const float missing = (1.0f - fy) * ((1.0f - fx) * L.corner[0] + fx * L.corner[1]) +
-                          fy * ((1.0f - fx) * L.corner[2] + fx * L.corner[3]);
-    out = out + missing * (t[0] + t[1] + t[2] + t[3]) / 3.0f;
-  }
-  return out;
-}
-
-// Gradient of one channel's value: texel weights and d/dfx, d/dfy.
-__device__ __forceinline__ void bilinear_grad(const Bilinear& L, const float (&t)[4],
-                                              float (&wgt)[4], float& dfx, float& dfy) {
-  const float fx = L.fx, fy = L.fy;
-  wgt[0] = (1.0f - fy) * (1.0f - fx);
-  wgt[1] = (1.0f - fy) * fx;
-  wgt[2] = fy * (1.0f - fx);
-  wgt[3] = fy * fx;
-  dfx = (1.0f - fy) * (t[1] - t[0]) + fy * (t[3] - t[2]);
-  dfy = ((1.0f - fx) * t[2] + fx * t[3]) - ((1.0f - fx) * t[0] + fx * t[1]);
-  if (L.cube) {
-    const float missing = (1.0f - fy) * ((1.0f - fx) * L.corner[0] + fx * L.corner[1]) +
-                          fy * ((1.0f - fx) * L.corner[2] + fx * L.corner[3]);
-    const float share = (t[0] + t[1] + t[2] + t[3]) / 3.0f;
-    const float dm_dfx = (1.0f - fy) * (L.corner[1] - L.corner[0]) + fy * (L.corner[3] - L.corner[2]);
-    const float dm_dfy = ((1.0f - fx) * L.corner[2] + fx * L.corner[3]) -
-                         ((1.0f - fx) * L.corner[0] + fx * L.corner[1]);
-    dfx += dm_dfx * share;
-    dfy += dm_dfy * share;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) wgt[k] += missing / 3.0f;
-  }
-}
-
-// Level of detail from the footprint (reference.py:491-501). uv_da = (du/dx, du/dy, dv/dx,
-// dv/dy); width and height are those of the base level.
-__device__ __forceinline__ float footprint_lod(const float4& da, int height, int width) {
-  const float W = (float)width, H = (float)height, L = kFootprintLimit;
-  const float cx0 = fminf(fmaxf(da.x * W, -L), L), cy0 = fminf(fmaxf(da.z * H, -L), L);
-  const float cx1 = fminf(fmaxf(da.y * W, -L), L), cy1 = fminf(fmaxf(da.w * H, -L), L);
-  const float len_x = cx0 * cx0 + cy0 * cy0;
-  const float len_y = cx1 * cx1 + cy1 * cy1;
-  if (isnan(da.x) || isnan(da.y) || isnan(da.z) || isnan(da.w))
-    return __int_as_float(0x7fc00000);
-  return 0.5f * log2f(fmaxf(fmaxf(len_x, len_y), kMinFootprint));
-}
-
-__device__ __forceinline__ void footprint_lod_grad(const float4& da, int height, int width,
-                                                   float g, float* grad) {
-  const float W = (float)width, H = (float)height, L = kFootprintLimit;
-  const float v[4] = {da.x * W, da.y * W, da.z * H, da.w * H};  // du/dx, du/dy, dv/dx, dv/dy
-  float c[4];
-  bool pass[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    pass[i] = v[i] >= -L && v[i] <= L;
-    c[i] = fminf(fmaxf(v[i], -L), L);
-  }
-  const float len_x = c[0] * c[0] + c[2] * c[2];
-  const float len_y = c[1] * c[1] + c[3] * c[3];
-  const float m = fmaxf(len_x, len_y);
-  float g_m = m >= kMinFootprint ? g * 0.5f / (m * kLn2) : 0.0f;
-  // torch.maximum splits the gradient evenly between equal arguments.
-  const float share_x = len_x > len_y ? 1.0f : (len_x == len_y ? 0.5f : 0.0f);
-  const float share_y = 1.0f - share_x;
-  const float g_x = g_m * share_x, g_y = g_m * share_y;
-  const float scale[4] = {W, W, H, H};
-  const float gl[4] = {g_x, g_y, g_x, g_y};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) grad[i] = pass[i] ? gl[i] * 2.0f * c[i] * scale[i] : 0.0f;
-}
-
-// Everything a pixel's lookup needs, shared by the forward and backward kernels.
-struct Lookup {
-  bool dir_invalid;  // cube direction that selects nothing: reads zero, no gradient
-  bool bad;          // NaN output, no gradient
-  int face;
-  float s, t;
-  int levels;        // 1 or 2 bilinear lookups (0 for nearest)
-  int level[2];
-  float level_weight[2];
-  bool lod_grad;     // the blend factor passes a gradient to the level of detail
-  float lod_raw;
-  bool mip;
-  CubeProj P;
-};
-
-// CUBE: a.boundary is DR_BOUNDARY_CUBE (the kernels are compiled for both cases, so that the
-// 2D one carries no cube-map state).
-template <bool CUBE>
-__device__ __forceinline__ void lookup_setup(const DrTextureArgs& a, int64_t pixel, Lookup& K) {
-  constexpr bool cube = CUBE;
-  const bool mip = a.filter == DR_FILTER_MIP_NEAREST || a.filter == DR_FILTER_MIP_LINEAR;
-  K.mip = mip;
-  K.dir_invalid = false;
-  K.face = -1;
-  // (du/dx, du/dy, dv/dx, dv/dy), held by value: a pointer that could address either this
-  // thread's registers or global memory would force them into scratch memory.
-  bool has_da = false;
-  float4 da = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (cube) {
-    cube_project(a.uv + 3 * pixel, (mip && a.uv_da) ? a.uv_da + 6 * pixel : nullptr, K.P);
-    K.dir_invalid = !K.P.valid;
-    K.face = K.P.face;
-    K.s = K.P.st[0];
-    K.t = K.P.st[1];
-    if (mip && a.uv_da) {
-      da = make_float4(K.P.st_da[0], K.P.st_da[1], K.P.st_da[2], K.P.st_da[3]);
-      has_da = true;
-    }
-  } else {
-    K.s = a.uv[2 * pixel];
-    K.t = a.uv[2 * pixel + 1];
-    if (mip && a.uv_da) {
-      da = load4(a.uv_da + 4 * pixel);
-      has_da = true;
-    }
-  }
-  K.bad = false;
-  K.lod_grad = false;
-  K.level[0] = K.level[1] = 0;
-  K.level_weight[0] = 1.0f;
-  K.level_weight[1] = 0.0f;
-  if (!mip) {
-    K.levels = a.filter == DR_FILTER_NEAREST ? 0 : 1;
-    return;
-  }
-  float lod = 0.0f;
-  if (has_da) lod = lod + footprint_lod(da, a.level_height[0], a.level_width[0]);
-  if (a.bias) lod = lod + a.bias[pixel];
-  K.lod_raw = lod;
-  const int top = a.num_levels - 1;
-  K.bad = isnan(lod);
-  if (K.bad) lod = 0.0f;
-  const bool inside = lod >= 0.0f && lod <= (float)top;
-  lod = fminf(fmaxf(lod, 0.0f), (float)top);
-  const bool blend = a.filter == DR_FILTER_MIP_LINEAR;
-  const int lower = (int)floorf(lod + (blend ? 0.0f : 0.5f));
-  K.level[0] = lower;
-  if (blend) {
-    K.levels = 2;
-    K.level[1] = min(lower + 1, top);
-    const float frac = lod - (float)lower;
-    K.level_weight[0] = 1.0f - frac;
-    K.level_weight[1] = frac;
-    K.lod_grad = inside && !K.bad;
-  } else {
-    K.levels = 1;
-  }
-}
-
-// Sizes and packed offset of the two levels a lookup may use. The level index differs per lane,
-// so these are memory reads: both levels' are issued together, before either is used.
-struct LevelDims {
-  int h[2], w[2];
-  int64_t off[2];
-};
-
-__device__ __forceinline__ LevelDims lookup_levels(const DrTextureArgs& a, const Lookup& K) {
-  LevelDims D;
-#pragma unroll
-  for (int l = 0; l < 2; ++l) {
-    const int k = K.level[l];
-    D.h[l] = a.level_height[k];
-    D.w[l] = a.level_width[k];
-    D.off[l] = a.level_offset[k];
-  }
-  return D;
-}
-
-__device__ __forceinline__ Bilinear level_setup(const DrTextureArgs& a, const Lookup& K,
-                                                const LevelDims& D, int l) {
-  return bilinear_setup(K.s, K.t, K.face, D.h[l], D.w[l], D.off[l], a.boundary);
-}
-
-// Nearest: the texel containing the coordinate (reference.py:555-573).
-__device__ __forceinline__ bool nearest_setup(const DrTextureArgs& a, const Lookup& K,
-                                              int64_t& index, bool& valid) {
-  const int h = a.level_height[0], w = a.level_width[0];
-  const Axis X = texel_axis(K.s, w, 0.0f, a.boundary);
-  const Axis Y = texel_axis(K.t, h, 0.0f, a.boundary);
-  const int boundary = a.boundary == DR_BOUNDARY_CUBE ? DR_BOUNDARY_CLAMP : a.boundary;
-  valid = tap((int)floorf(Y.x), (int)floorf(X.x), K.face, h, w, a.level_offset[0], boundary,
-              index);
-  return X.bad || Y.bad;
-}
-
 // NC channels per pass (the channel count when it is 1-4; 4 with a loop for more). Every tap
 // of a pass is loaded before its stores.
 template <int NC, bool CUBE>
@@ -505,8 +67,8 @@ __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* __
   if (pixel >= (int64_t)a.batch * a.height * a.width) return;
   const int C = a.channels;
   float* o = out + pixel * C;
-  Lookup K;
-  lookup_setup<CUBE>(a, pixel, K);
+  Lookup<float> K;
+  lookup_setup<float, CUBE>(a, pixel, K);
   if (K.dir_invalid) {
     for (int c = 0; c < C; ++c) o[c] = 0.0f;
     return;
@@ -522,9 +84,9 @@ __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* __
     return;
   }
   const LevelDims D = lookup_levels(a, K);
-  const Bilinear L0 = level_setup(a, K, D, 0);
+  const Bilinear<float> L0 = level_setup(a, K, D, 0);
   const bool two = K.levels == 2;
-  const Bilinear L1 = two ? level_setup(a, K, D, 1) : L0;
+  const Bilinear<float> L1 = two ? level_setup(a, K, D, 1) : L0;
   const bool bad = K.bad || L0.bad || (two && L1.bad);
   const float frac = K.level_weight[1];
   for (int c0 = 0; c0 < C; c0 += NC) {
@@ -559,7 +121,7 @@ __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* __
 // Coordinate-gradient contributions of one level: d/dfx, d/dfy summed over channels with the
 // level weight, and the level's value per channel for the blend-factor gradient.
 template <int N>
-__device__ __forceinline__ void level_coordinate_grads(const Bilinear& L,
+__device__ __forceinline__ void level_coordinate_grads(const Bilinear<float>& L,
                                                        const float* __restrict__ texels,
                                                        const float* __restrict__ g, int C,
                                                        float level_weight, float& g_fx,
@@ -599,7 +161,7 @@ __device__ __forceinline__ void level_coordinate_grads(const Bilinear& L,
 // Table keys (texel rows of the packed buffer, 0xffffffff for none) and weights of a level's
 // taps. A tap of weight 0 (the second level when the blend factor is 0, or an axis with fraction
 // 0) adds nothing and gets no key.
-__device__ __forceinline__ void level_taps(const Bilinear& L, float level_weight,
+__device__ __forceinline__ void level_taps(const Bilinear<float>& L, float level_weight,
                                            int64_t tex_off, uint32_t* key, float* weight) {
   float t0[4] = {0.f, 0.f, 0.f, 0.f}, wgt[4], dfx, dfy;
   bilinear_grad(L, t0, wgt, dfx, dfy);  // the weights do not depend on texel values
@@ -625,7 +187,7 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
   const int64_t tex_off = a.tex_batch > 1 ? (int64_t)tp.b * a.num_texels : 0;
   const float* texels = a.texels + tex_off * C;
 
-  Lookup K;
+  Lookup<float> K;
   // Texel gradient targets: taps 0-3 of the first level, 4-7 of the second.
   uint32_t tap_key[8];
   float tap_weight[8];
@@ -637,7 +199,7 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
   float g_s = 0.0f, g_t = 0.0f, g_lod = 0.0f;
   bool live = false;
   if (tp.inside) {
-    lookup_setup<CUBE>(a, pixel, K);
+    lookup_setup<float, CUBE>(a, pixel, K);
     live = !K.dir_invalid;
   }
   if (live && K.levels == 0) {
@@ -651,8 +213,8 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     live = false;  // no coordinate gradient
   } else if (live) {
     const LevelDims D = lookup_levels(a, K);
-    const Bilinear L0 = level_setup(a, K, D, 0);
-    Bilinear L1 = L0;
+    const Bilinear<float> L0 = level_setup(a, K, D, 0);
+    Bilinear<float> L1 = L0;
     const bool two = K.levels == 2;
     if (two) L1 = level_setup(a, K, D, 1);
     if (K.bad || L0.bad || (two && L1.bad)) {
@@ -677,8 +239,9 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     float g_da[4] = {0.f, 0.f, 0.f, 0.f};
     const bool has_da = K.mip && a.uv_da != nullptr;
     if (live && has_da && g_lod != 0.0f) {
-      const float4 da = cube ? make_float4(K.P.st_da[0], K.P.st_da[1], K.P.st_da[2], K.P.st_da[3])
-                             : load4(a.uv_da + 4 * pixel);
+      const Deriv4<float> da = cube ? Deriv4<float>{K.P.st_da[0], K.P.st_da[1], K.P.st_da[2],
+                                                    K.P.st_da[3]}
+                                    : load_deriv4(a.uv_da + 4 * pixel);
       footprint_lod_grad(da, a.level_height[0], a.level_width[0], g_lod, g_da);
     }
     if (grad_bias) grad_bias[pixel] = live ? g_lod : 0.0f;

@@ -313,6 +313,63 @@ int dr_antialias_backward(const DrAntialiasArgs* a, const void* pairs, size_t pa
                           const float* grad_out, float* grad_color, float* grad_pos,
                           void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * float64 variants, for gradient-check-grade work. The reference's GPU backend accepts float64
+ * tensors at the backend level (its resolve is checked to 1e-12, tests/test_coverage.py:792-808;
+ * interpolate and texture by gradcheck, tests/test_triton.py:234-240, :303-319; antialias to
+ * 1e-9, :408-415) and runs the same entry points: rasterize, interpolate, texture and
+ * antialias of src/diffrast/backends/triton.py:14-92. Here each has a _f64 twin taking the same
+ * argument structs, whose float arrays (pos, attr, rast, rast_db, texels, uv, uv_da, bias, color)
+ * then hold doubles, with strides counted in doubles; outputs and gradients are double. These
+ * kernels are plain (one thread per pixel, float64 atomics). Visibility has no twin: as in the
+ * reference's GPU backend, the keys come from float32 positions, and only the resolve is
+ * float64.
+ * ------------------------------------------------------------------------------------- */
+
+/* dr_resolve_forward / _backward in double (grad_pos accumulated, zeroed by the caller). */
+int dr_resolve_forward_f64(const DrRasterGeometry* g, const uint64_t* keys, double* rast,
+                           double* rast_db, void* stream);
+int dr_resolve_backward_f64(const DrRasterGeometry* g, const uint64_t* keys,
+                            const double* grad_rast, const double* grad_rast_db,
+                            double* grad_pos, void* stream);
+
+/* dr_interpolate_forward / _backward in double (grad_attr accumulated, zeroed by the caller). */
+int dr_interpolate_forward_f64(const DrInterpolateArgs* a, double* out, double* out_da,
+                               void* stream);
+int dr_interpolate_backward_f64(const DrInterpolateArgs* a, const double* grad_out,
+                                const double* grad_out_da, double* grad_attr, double* grad_rast,
+                                double* grad_rast_db, void* stream);
+
+/* dr_texture_forward / _backward and the mip chain in double (grad_texels accumulated, zeroed by
+ * the caller). */
+int dr_texture_forward_f64(const DrTextureArgs* a, double* out, void* stream);
+int dr_texture_backward_f64(const DrTextureArgs* a, const double* grad_out, double* grad_texels,
+                            double* grad_uv, double* grad_uv_da, double* grad_bias,
+                            void* stream);
+int dr_mip_build_f64(double* texels, const double* base, int32_t tex_batch, int32_t channels,
+                     int64_t num_texels, int32_t faces, int32_t num_levels,
+                     const int32_t* level_height, const int32_t* level_width,
+                     const int64_t* level_offset, void* stream);
+int dr_mip_build_backward_f64(double* grad_texels, int32_t tex_batch, int32_t channels,
+                              int64_t num_texels, int32_t faces, int32_t num_levels,
+                              const int32_t* level_height, const int32_t* level_width,
+                              const int64_t* level_offset, void* stream);
+
+/* Silhouette bits of every (pos batch, triangle) from float64 positions (as dr_silhouette_mask
+ * without rast). */
+int dr_silhouette_mask_f64(const double* pos, int64_t pos_batch_stride, int32_t pos_batch,
+                           const int32_t* tri, int32_t num_tri, const int32_t* neighbours,
+                           uint8_t* mask, void* stream);
+
+/* Antialias in double: pair records of 18 bytes per pixel (dr_antialias_workspace_size_f64);
+ * grad_pos accumulated, zeroed by the caller. */
+int dr_antialias_workspace_size_f64(const DrAntialiasArgs* a, size_t* bytes);
+int dr_antialias_forward_f64(const DrAntialiasArgs* a, void* pairs, size_t pairs_bytes,
+                             double* out, void* stream);
+int dr_antialias_backward_f64(const DrAntialiasArgs* a, const void* pairs, size_t pairs_bytes,
+                              const double* grad_out, double* grad_color, double* grad_pos,
+                              void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,6 +82,7 @@ def test_headline_op_bytes():
 
 
 def test_every_entry_point_belongs_to_an_op():
-    compute = {n for n in _lib.EXPORTS if n not in (
+    # (a float64 twin belongs where its float32 entry point does)
+    compute = {n.removesuffix("_f64") for n in _lib.EXPORTS if n not in (
         "dr_error_string", "dr_abi_version", "dr_struct_size") and "size" not in n}
     assert compute <= set(bench.OP_OF)
