@@ -118,6 +118,47 @@ def torus_knot(p: int = 2, q: int = 3, segments: int = 512, sides: int = 32,
     return verts.float(), faces.to(torch.int32)
 
 
+def displaced_grid(num_tri: int) -> tuple[Tensor, Tensor, int]:
+    """The reference's benchmark surface (benchmarks/bench_rasterize.py:19-29): a square grid
+    over [-1, 1]^2 in the x-z plane, n x n cells of two triangles with n = round(sqrt(num_tri /
+    2)), raised to y = 0.1 sin(6x) cos(5z). Vertices row by row ((n + 1) per row, x fastest);
+    triangles as the reference lists them, first (a, b, d) of every cell, then (a, d, c), where
+    a, b are a cell's corners on its first row and c, d those on the next. Returns the vertices
+    [(n + 1)^2, 3], the triangles and n."""
+    n = max(1, round(math.sqrt(num_tri / 2)))
+    line = torch.linspace(-1, 1, n + 1)
+    z, x = (g.reshape(-1) for g in torch.meshgrid(line, line, indexing="ij"))
+    verts = torch.stack([x, 0.1 * torch.sin(6 * x) * torch.cos(5 * z), z], -1)
+    corner = (torch.arange(n)[:, None] * (n + 1) + torch.arange(n)[None, :]).reshape(-1)
+    a, b, c, d = corner, corner + 1, corner + n + 1, corner + n + 2
+    tri = torch.cat([torch.stack([a, b, d], -1), torch.stack([a, d, c], -1)])
+    return verts, tri.to(torch.int32), n
+
+
+def grid_views(verts: Tensor, views: int) -> Tensor:
+    """Clip-space positions [views, vertices, 4] of the grid seen as in the reference's
+    benchmark (benchmarks/bench_rasterize.py:31-52): view i turns the grid by 2 pi i / views
+    about y, moves it by (0, -0.6, 2.2) and projects with focal length 1.5, near 0.1 and far 10,
+    w being the camera-space z (the camera looks along +z)."""
+    focal, near, far = 1.5, 0.1, 10.0
+    out = []
+    for i in range(views):
+        angle = 2 * math.pi * i / max(views, 1)
+        c, s = math.cos(angle), math.sin(angle)
+        x, y, z = verts.unbind(-1)
+        cx, cy, cz = c * x + s * z, y - 0.6, c * z - s * x + 2.2
+        depth = (far + near) / (far - near) * cz - 2 * far * near / (far - near)
+        out.append(torch.stack([focal * cx, focal * cy, depth, cz], -1))
+    return torch.stack(out)
+
+
+def grid_uv(n: int) -> Tensor:
+    """Planar texture coordinates of the grid's vertices [(n + 1)^2, 2]: (column, row) / n."""
+    line = torch.linspace(0, 1, n + 1)
+    v, u = torch.meshgrid(line, line, indexing="ij")
+    return torch.stack([u, v], -1).reshape(-1, 2)
+
+
 def vertex_normals(verts: Tensor, faces: Tensor) -> Tensor:
     """Area-weighted vertex normals."""
     f = faces.long()

@@ -249,11 +249,14 @@ class _Oracle:
     antialias = staticmethod(lambda c, r, p, tri: R.antialias(c, r, p, tri, 1.0))
 
 
-def _one_view(w, ops, device, ids=None):
-    """View 0 of workload ``w`` through ``ops``: the outputs of every stage and the gradients
-    of the MSE loss to every leaf, on the CPU."""
+def _one_view(w, ops, device, ids=None, view=0):
+    """One view of workload ``w`` through ``ops``: the outputs of every stage and the gradients
+    of the loss (MSE against the target, or the sum of the image without one) to every leaf, on
+    the CPU."""
     t = w.tensors
-    one = {"pos": t["pos"][:1], "target": t["target"][:1]}
+    one = {"pos": t["pos"][view:view + 1]}
+    if "target" in t:
+        one["target"] = t["target"][view:view + 1]
     for k in ("tri", "uv", "feat", "tex", "normals", "cube"):
         if k in t:
             one[k] = t[k]
@@ -268,6 +271,9 @@ def _one_view(w, ops, device, ids=None):
         outs["uv"], outs["uv_da"] = ops.interpolate(x["uv"], rast, tri, rast_db, "all")
         mip = ops.construct_mip(x["tex"])
         col = ops.texture(x["tex"], outs["uv"], outs["uv_da"], "wrap", mip=mip)
+    elif w.name == "grid":
+        outs["uv"], outs["uv_da"] = ops.interpolate(x["uv"], rast, tri, rast_db, "all")
+        col = ops.texture(x["tex"], outs["uv"], outs["uv_da"], "wrap")
     elif w.name == "large":
         outs["f"], _ = ops.interpolate(x["feat"], rast, tri)
         outs["st"], outs["st_da"] = ops.interpolate(x["uv"], rast, tri, rast_db, "all")
@@ -280,8 +286,10 @@ def _one_view(w, ops, device, ids=None):
         col = ops.texture(x["cube"], dirs, dirs_da, "cube")
     outs["col"] = col
     outs["aa"] = ops.antialias(col, rast, x["pos"], tri)
-    loss = torch.nn.functional.mse_loss(outs["aa"], x["target"])
-    loss.backward()
+    if "target" in x:
+        torch.nn.functional.mse_loss(outs["aa"], x["target"]).backward()
+    else:
+        outs["aa"].sum().backward()
     grads = {k: v.grad.detach().cpu() for k, v in leaves.items()}
     return {k: v.detach().cpu() for k, v in outs.items()}, grads
 
@@ -307,12 +315,34 @@ def _lod_shifted(ulps):
         R.level_of_detail = original
 
 
-@pytest.mark.parametrize("name", ["textured", "large", "cubemap"])
-def test_one_view_forward_and_backward_in_full(name):
-    """Every output and every gradient of view 0 at the workload's full size, against the
+def _grid_workload(num_tri, views, res):
+    """The reference's published benchmark scene (displaced grid, planar uv, 1024^2 x 3
+    texture) as a workload of this file."""
+    verts, tri, n = workloads.displaced_grid(num_tri)
+    gen = torch.Generator().manual_seed(0)
+    return workloads.Workload("grid", views, (res, res), {
+        "pos": workloads.grid_views(verts, views), "tri": tri, "uv": workloads.grid_uv(n),
+        "tex": torch.rand(1, 1024, 1024, 3, generator=gen)})
+
+
+CASES = [("textured", 0), ("large", 0), ("cubemap", 0), ("grid 10k 512", 0),
+         ("grid 10k 512", 3), ("grid 100k 256", 5)]
+
+
+def _case(name):
+    if name.startswith("grid"):
+        _, count, res = name.split()
+        return _grid_workload(int(count[:-1]) * 1000, 8, int(res))
+    return workloads.build(name)
+
+
+@pytest.mark.parametrize("name,view", CASES)
+def test_one_view_forward_and_backward_in_full(name, view):
+    """Every output and every gradient of one view at the workload's full size, against the
     oracle run from the GPU's triangle ids (the ids themselves are checked against the oracle's
-    brute force at sampled pixels above): values within 1e-5, gradients within 1e-4 of the
-    largest.
+    brute force at sampled pixels, above for the five workloads and here for the grid scene of
+    the reference's published table, with the sum of the image as its loss as there): values
+    within 1e-5, gradients within 1e-4 of the largest.
 
     The level of detail is 0.5 log2 of the footprint, and log2's last bit is not pinned: the
     GPU's and the host's log2 may differ by one unit in the last place. Where the level sits on
@@ -322,11 +352,14 @@ def test_one_view_forward_and_backward_in_full(name):
     moving the oracle's level up by one unit reproduces the GPU's gradient there to 4 digits.
     So each gradient entry must be within tolerance of the oracle's with the level as computed,
     or one unit above, or one below."""
-    w = workloads.build(name)
-    ours, our_grads = _one_view(w, _Gpu(w), "cuda")
+    w = _case(name)
+    ours, our_grads = _one_view(w, _Gpu(w), "cuda", view=view)
     ids = ours["rast"][..., 3].long() - 1
-    ref, ref_grads = _one_view(w, _Oracle(), "cpu", ids)
+    ref, ref_grads = _one_view(w, _Oracle(), "cpu", ids, view=view)
     assert (ids >= 0).any()
+    if w.name == "grid":
+        check_visibility(w.tensors["pos"][view:view + 1], w.tensors["tri"], ours["rast"], [0],
+                         torch.Generator().manual_seed(34 + view))
     assert torch.equal(ours["rast"][..., 3], ref["rast"][..., 3])
     assert (ours["aa"] != ours["col"]).any(), "antialiasing should change silhouette pixels"
     errors = {key: rel_error(ours[key], expect) for key, expect in ref.items()}
@@ -345,7 +378,7 @@ def test_one_view_forward_and_backward_in_full(name):
     if any(e >= GRAD_TOL for e in as_computed.values()):
         for ulps in (1, -1):
             with _lod_shifted(ulps):
-                _, shifted = _one_view(w, _Oracle(), "cpu", ids)
+                _, shifted = _one_view(w, _Oracle(), "cpu", ids, view=view)
             worst = {key: torch.minimum(e, excess(shifted)[key]) for key, e in worst.items()}
     final = {key: e.max().item() for key, e in worst.items()}
     print(name, "values", errors, "gradient excess / max: as computed", as_computed,
