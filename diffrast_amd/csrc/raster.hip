@@ -279,6 +279,18 @@ __device__ __forceinline__ float key_depth(uint64_t key) {
   return __uint_as_float((ordered & 0x80000000u) ? (ordered & 0x7fffffffu) : ~ordered);
 }
 
+// The largest of v over the lanes of each 16-lane row, in the row's last lane.
+__device__ __forceinline__ uint64_t row_max_u64(uint64_t v) {
+  uint64_t o = row_shr64<1>(v);
+  v = o > v ? o : v;
+  o = row_shr64<2>(v);
+  v = o > v ? o : v;
+  o = row_shr64<4>(v);
+  v = o > v ? o : v;
+  o = row_shr64<8>(v);
+  return o > v ? o : v;
+}
+
 // Merges a key into the key buffer, unless the previous layer rules it out. The atomic
 // returns nothing, so a thread never waits on it.
 __device__ __forceinline__ void merge_key(uint64_t* keys, const uint64_t* prev, int64_t pixel,
@@ -1074,9 +1086,10 @@ __global__ __launch_bounds__(256) void raster_tile_place(Workspace ws) {
 // centres may cover (row_span(); the whole row of the box for a triangle without spans). The
 // pixels of all those row spans form one list of work items, which the 256 threads walk in
 // steps of 256, so every lane has a pixel to test whatever the span lengths. The list is mapped
-// kWindow items at a time: each span writes (its first item, its triangle, its first pixel) at
-// its first item of the window, and a max-scan over the window carries that to the span's other
-// items. Hits merge into the keys in LDS (64-bit min). Before each chunk the tile's farthest key
+// kWindow items at a time: each triangle writes (its first item, itself) at its first item of
+// the window, a max-scan over the window carries that to the triangle's other items, and an
+// item finds its pixel by a binary search over its triangle's spans. Hits merge into the keys
+// in LDS (64-bit min). Before each chunk the tile's farthest key
 // bounds what can still win: triangles entirely behind it are skipped, and so are single pixels
 // that already hold a nearer key. The improved keys are stored once at the end.
 template <bool kLoop>
@@ -1089,15 +1102,20 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   __shared__ float4 s_tri[kChunk][3];
   __shared__ float2 s_reach[kChunk];
   __shared__ uint32_t s_row[kChunk];
-  // Per staged triangle and tile row: first column | last column << 4 (0x0f: no pixel).
-  __shared__ uint8_t s_rows[kChunk][kTile];
-  // Work item -> (first item of its span in the window) << 20 | triangle << 12 | pixel offset.
+  // Per staged triangle, its row spans that hold work items, in row order: items before the
+  // span << 8 | first column << 4 | row (a triangle has at most 256 items in a tile, so the
+  // count before a span fits 8 bits); and how many there are.
+  __shared__ uint16_t s_span[kChunk][kTile];
+  __shared__ uint8_t s_spans[kChunk];
+  // Work item -> (first item of its triangle in the window) << 20 | triangle << 12 |
+  // (the triangle's first item - the window's + 2048).
   __shared__ uint2 s_map[kWindow / 2];
   __shared__ int s_wave_sum[256 / DR_WAVE];
   __shared__ uint32_t s_wave_max[256 / DR_WAVE];
   __shared__ unsigned long long s_key[kTile * kTile];
   __shared__ float s_px[kTile], s_py[kTile];
   __shared__ uint64_t s_far[256 / DR_WAVE];
+  __shared__ uint64_t s_row_far[kTile];  // the farthest key of each tile row
   __shared__ float s_bound[kChunk];  // lower bound of each staged triangle's depth
 
   // Workgroups are dispatched round-robin over the 8 XCDs: XCD k runs the busy tiles of share
@@ -1170,7 +1188,10 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     // of the vertex depths z_k / w_k up to a few float32 roundings (~6 * 2^-24 of the largest
     // |z_k / w_k|; the margin is 1e-5 of it), and equal depths are never skipped.
     __syncthreads();  // the previous chunk's merges (and the set-up above) are done
-    uint64_t far_key = wave_max_u64(inside ? s_key[threadIdx.x] : 0ull);
+    const uint64_t own_key = inside ? s_key[threadIdx.x] : 0ull;
+    const uint64_t row_far = row_max_u64(own_key);  // a wave holds four rows of the tile
+    if ((lane & (kTile - 1)) == kTile - 1) s_row_far[threadIdx.x / kTile] = row_far;
+    uint64_t far_key = wave_max_u64(own_key);
     if (lane == 0) s_far[wave] = far_key;
     __syncthreads();
 #pragma unroll
@@ -1178,7 +1199,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     const bool cull = far_key != kEmptyKey;
     const float far_depth = key_depth(far_key);
 
-    int items = 0, row_lo = 0, row_hi = -1;
+    int items = 0;
     if (staged) {
 #pragma unroll
       for (int k = 0; k < 3; ++k) s_tri[threadIdx.x][k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
@@ -1208,18 +1229,19 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
         RowSpans se = {};
         const bool spans =
             span_setup(T.x, T.y, T.w, T.reach_x, T.reach_y, g.width, tile_x0, se);
-        row_lo = by0;
-        row_hi = by1;
+        int held = 0;
         for (int r = by0; r <= by1; ++r) {
           int lo = bx0, hi = bx1;
           if (spans) row_span(se, s_py[r], lo, hi);
-          uint32_t code = 0x0fu;
+          // Every pixel of the row already holds a key nearer than the triangle can reach (an
+          // empty key reads as NaN and never compares greater).
+          if (bound > key_depth(s_row_far[r])) hi = lo - 1;
           if (lo <= hi) {
-            code = (uint32_t)lo | (uint32_t)hi << 4;
+            s_span[threadIdx.x][held++] = (uint16_t)(items << 8 | lo << 4 | r);
             items += hi - lo + 1;
           }
-          s_rows[threadIdx.x][r] = (uint8_t)code;
         }
+        s_spans[threadIdx.x] = (uint8_t)held;
       }
     }
     // Exclusive prefix of the item counts over the workgroup.
@@ -1238,23 +1260,12 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     for (int base = 0; base < total; base += kWindow) {
       s_map[threadIdx.x] = make_uint2(0u, 0u);
       __syncthreads();
-      // Mark the first item in the window of each span that reaches into it.
+      // Mark the first item in the window of each triangle that reaches into it. Its first
+      // item overall is within 256 items of the window (-256 < tri_first - base < 512).
       if (items > 0 && tri_first < base + kWindow && tri_first + items > base) {
-        int first = tri_first;
-        for (int r = row_lo; r <= row_hi && first < base + kWindow; ++r) {
-          const uint32_t code = s_rows[threadIdx.x][r];
-          const int lo = (int)(code & 15u), hi = (int)(code >> 4);
-          if (lo > hi) continue;
-          const int width = hi - lo + 1;
-          if (first + width > base) {
-            const int pos = max(first, base) - base;
-            // Pixel of item i (counted from base) of this span: q - 2048 + i, 0 < q < 4096.
-            const int q = r * kTile + lo - (first - base) + 2048;
-            reinterpret_cast<uint32_t*>(s_map)[pos] =
-                (uint32_t)pos << 20 | threadIdx.x << 12 | (uint32_t)q;
-          }
-          first += width;
-        }
+        const int pos = max(tri_first, base) - base;
+        reinterpret_cast<uint32_t*>(s_map)[pos] =
+            (uint32_t)pos << 20 | threadIdx.x << 12 | (uint32_t)(tri_first - base + 2048);
       }
       __syncthreads();
       // Inclusive max-scan of the window (each mark exceeds every mark before it).
@@ -1276,7 +1287,23 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
       for (int i = threadIdx.x; i < count; i += 256) {
         const uint32_t v = reinterpret_cast<const uint32_t*>(s_map)[i];
         const int j = (int)((v >> 12) & 0xffu);
-        const int p = (int)(v & 0xfffu) - 2048 + i;
+        // The item's place among its triangle's items, then its span: the last one that
+        // starts at or before it (binary search over the triangle's at most 16 spans).
+        const int li = i + 2048 - (int)(v & 0xfffu);
+        const int held = s_spans[j];
+        uint32_t e = s_span[j][0];
+        int at_span = 0;
+#pragma unroll
+        for (int step = kTile / 2; step >= 1; step >>= 1) {
+          if (at_span + step < held) {
+            const uint32_t c = s_span[j][at_span + step];
+            if ((int)(c >> 8) <= li) {
+              at_span += step;
+              e = c;
+            }
+          }
+        }
+        const int p = (int)(e & 15u) * kTile + (int)((e >> 4) & 15u) + li - (int)(e >> 8);
         // Early depth test: the pixel already holds a nearer key (NaN for an empty one).
         if (s_bound[j] > key_depth(s_key[p])) continue;
         const float4 v0 = s_tri[j][0], v1 = s_tri[j][1], v2 = s_tri[j][2];
