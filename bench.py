@@ -291,7 +291,10 @@ class _Shade(torch.autograd.Function):
 
 def make_step(w, device):
     """One forward+backward step of workload ``w`` on the GPU (inputs copied to ``device``)."""
-    t = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in w.tensors.items()}
+    # Range tables stay on the host, as nvdiffrast takes them (reading them needs no device
+    # synchronisation, so the step can be captured in a HIP graph).
+    t = {k: (v.to(device) if isinstance(v, torch.Tensor) and k != "ranges" else v)
+         for k, v in w.tensors.items()}
     ctx = dr.RasterizeContext(device)
     res = w.resolution
     leaves = []
@@ -567,11 +570,44 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int) -> dict:
+def graph_step_ms(step, steps: int) -> float | None:
+    """ms per step when one step, captured in a HIP graph (torch.cuda.graph), is replayed
+    `steps` times back to back: the same kernels with no host work between them. None when the
+    step cannot be captured (the reason goes to stderr)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    try:
+        with torch.cuda.stream(side):  # capture wants its allocations warmed on a side stream
+            for _ in range(2):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+    except RuntimeError as error:
+        print(f"graph capture failed, eager timing only: {error}", file=sys.stderr)
+        torch.cuda.synchronize()
+        return None
+    graph.replay()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - start) * 1e3 / steps
+    del graph
+    torch.cuda.synchronize()
+    return ms
+
+
+def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int,
+        graph: bool = False) -> dict:
     """Warm-up steps (timed per entry point after the first, to find the dominant kernel), then
     exactly `steps` timed steps in which only the dominant entry point carries HIP events (the
     roofline's live launch time; events around every call would add ~0.13 ms per step), then a
-    few more steps with every entry point timed, for the per-kernel and per-op tables."""
+    few more steps with every entry point timed, for the per-kernel and per-op tables. With
+    `graph`, `value` is instead the time per step of a captured step replayed `steps` times
+    (the eager time stays in the line, and the kernel times come from the eager steps)."""
     w = workloads.build(name)
     step = make_step(w, device)
     model = BytesModel(w)
@@ -640,6 +676,11 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     traffic = profiled_traffic(SINGLE_KERNEL[dominant], name)
 
+    eager_ms = ms_per_step
+    replay_ms = graph_step_ms(step, steps) if graph else None
+    if replay_ms is not None:
+        ms_per_step = replay_ms
+
     baseline = None
     if cpu:
         baseline = cpu_baseline(w, sample_tris, first_image_ids(w, device))
@@ -653,6 +694,8 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int)
         "steps": steps,
         "warmup": warmup,
         "ms_per_step": round(ms_per_step, 3),
+        "timing": "HIP graph replay" if replay_ms is not None else "eager",
+        "eager_ms_per_step": round(eager_ms, 3),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -701,6 +744,8 @@ def main():
                         help="one JSON line per workload (the headline first)")
     parser.add_argument("--cpu-sample-tris", type=int, default=4096)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--graph", action="store_true",
+                        help="time a captured step replayed as a HIP graph (eager time kept)")
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="run one copy of this size first (counter calibration)")
     args = parser.parse_args()
@@ -717,7 +762,7 @@ def main():
         else [args.workload]
     for name in names:
         result = run(name, args.steps, args.warmup, device, not args.no_cpu_baseline,
-                     args.cpu_sample_tris)
+                     args.cpu_sample_tris, args.graph)
         print(json.dumps(result), flush=True)
 
 

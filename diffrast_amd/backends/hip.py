@@ -298,6 +298,31 @@ def rasterize_layer(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad_
     return rast, rast_db, keys
 
 
+# Device copies of range tables, by content: a range table drawn again (every DepthPeeler
+# takes its own copy of ``ranges``) is copied to the device once, so that later calls, and a
+# step captured in a HIP graph, make no host-to-device copy.
+_RANGE_COPIES: dict[tuple, tuple[Tensor, Tensor]] = {}
+_RANGE_COPIES_KEPT = 16
+_range_lock = threading.Lock()
+
+
+def _range_tables(table: list[tuple[int, int]], prefix: list[int],
+                  device: torch.device) -> tuple[Tensor, Tensor]:
+    key = (device, tuple(table))
+    with _range_lock:
+        found = _RANGE_COPIES.pop(key, None)
+        if found is not None:
+            _RANGE_COPIES[key] = found  # most recent now
+            return found
+    copies = (torch.tensor(table, dtype=torch.int32).to(device, non_blocking=True),
+              torch.tensor(prefix, dtype=torch.int64).to(device, non_blocking=True))
+    with _range_lock:
+        _RANGE_COPIES[key] = copies
+        while len(_RANGE_COPIES) > _RANGE_COPIES_KEPT:
+            del _RANGE_COPIES[next(iter(_RANGE_COPIES))]
+    return copies
+
+
 def rasterize_ranges(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad_db: bool,
                      ranges: Tensor, previous: Tensor | None = None):
     """Range mode in one launch: image i draws ``tri[start_i : start_i + count_i]`` of the
@@ -316,10 +341,9 @@ def rasterize_ranges(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad
         prefix.append(prefix[-1] + c)
     if prefix[-1] == 0:
         return _empty_layer(pos, batch, resolution)
-    device = pos.device
     pos, tri = pos.contiguous(), tri.contiguous()
-    ranges_dev = torch.tensor(table, dtype=torch.int32).to(device, non_blocking=True)
-    prefix_dev = torch.tensor(prefix, dtype=torch.int64).to(device, non_blocking=True)
+    ranges_dev, prefix_dev = _range_tables(table, prefix, pos.device)
+
     def geometry(p):
         return _Geometry(p, tri, resolution, ranges=ranges_dev, range_prefix=prefix_dev,
                          batch=batch, num_instances=prefix[-1])

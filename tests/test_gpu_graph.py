@@ -49,6 +49,23 @@ def _textured_step(t, ctx, res):
     return body, (pos, tex)
 
 
+def _instances_step(t, ctx, res):
+    # Range mode with depth peeling (a new peeler every step, as an application would make it),
+    # then antialias on the first layer.
+    pos, color, tri, target = t["pos"], t["color"], t["tri"], torch.zeros_like(t["color"])
+    ranges = t["ranges"].cpu()
+
+    def body():
+        with dr.DepthPeeler(ctx, pos, tri, res, ranges=ranges) as peeler:
+            layers = [peeler.rasterize_next_layer()[0] for _ in range(4)]
+        out = dr.antialias(color, layers[0], pos, tri)
+        loss = torch.nn.functional.mse_loss(out, target)
+        loss.backward()
+        return loss, torch.cat([out.flatten(), torch.cat(layers).flatten()])
+
+    return body, (pos, color)
+
+
 def _assert_gradients_equal(got, expected, what):
     # Gradients gather per workgroup in fixed point (exact) and then add to global memory with
     # float atomics, whose order varies from run to run: equal up to that last rounding.
@@ -58,7 +75,8 @@ def _assert_gradients_equal(got, expected, what):
 
 
 @pytest.mark.parametrize("name, make, scale", [("sphere", _sphere_step, 1),
-                                               ("textured", _textured_step, 2)])
+                                               ("textured", _textured_step, 2),
+                                               ("instances", _instances_step, 4)])
 def test_step_captured_in_a_graph_matches_eager(name, make, scale):
     w = workloads.build(name, "cuda", scale=scale)
     ctx = dr.RasterizeContext("cuda")
