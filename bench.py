@@ -13,14 +13,19 @@ of the other four configurations (``make_step`` shows each step) and ``--all-wor
 all five, one JSON line each. Inputs are synthetic and resident on the GPU before timing
 starts. ``--steps`` steps are timed between synchronisations, after ``--warmup`` untimed ones.
 
-Per-kernel time: every C-ABI entry point called in the timed steps is bracketed by HIP events
-on the stream it launches on. ``roofline`` reports the longest-running entry point that
-launches a single kernel (so that its event time is that kernel's duration): its algorithmic
-bytes per launch -- the unique bytes its algorithm must move, from the call's arguments
-(``BytesModel``) -- over its mean duration, against 8 TB/s. ``traffic`` is the HBM bytes per
-launch measured for that kernel with rocprofv3 counters (FETCH_SIZE, WRITE_SIZE, each scaled
-by the counter's reading for a copy of known size), read from the summary under profiles/ when
-one exists for it and the workload.
+Per-kernel time: HIP events around the C-ABI entry points, on the stream they launch on (in the
+timed steps only around the dominant one; every entry point in five further steps for the
+per-kernel table). Algorithmic bytes are the unique-byte model of ``BytesModel``: every input
+read once and every output written once, from each call's own arguments. ``roofline`` reports
+the longest-running entry point that launches a single kernel (so that its event time is that
+kernel's duration): its unique bytes per launch over its mean duration, against 8 TB/s; its
+vector issue against the issue peak (``valu``, from the committed counter summary); each op's
+forward+backward time against the HBM time of its unique bytes (``ops``); and the whole step
+against the four ops' bytes (``step``). ``traffic`` is the HBM bytes per launch measured for
+that kernel with rocprofv3 counters (FETCH_SIZE, WRITE_SIZE, each scaled by the counter's
+reading for a copy of known size), from ``profiles/kernels.<workload>.pmc.txt`` when present.
+``--graph`` times a step captured in a HIP graph and replayed (the eager time stays in the
+line as ``eager_ms_per_step``).
 
 CPU baseline: the oracle (a pure-PyTorch restatement of the reference backend) on the host
 cores, on a bounded sample of the same workload -- one image, its visibility over a subset of
@@ -464,20 +469,17 @@ def cpu_baseline(w, sample_tris: int, ids) -> dict:
 
 
 def profiled_traffic(kernel: str, workload: str) -> dict | None:
-    """HBM bytes per launch of ``kernel`` from its committed rocprofv3 counter summary."""
-    path = ROOT / "profiles" / f"{kernel}.{workload}.pmc.txt"
+    """HBM bytes per launch of ``kernel`` from the workload's committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a copy of known size):
+    lines ``<kernel>.fetch_bytes: N`` and ``<kernel>.write_bytes: N``."""
+    path = ROOT / "profiles" / f"kernels.{workload}.pmc.txt"
     if not path.exists():
         return None
-    fields = {}
-    for line in path.read_text().splitlines():
-        key, sep, value = line.partition(":")
-        if sep and key.strip() in ("fetch_bytes", "write_bytes", "copy_factor_fetch",
-                                   "copy_factor_write"):
-            fields[key.strip()] = float(value)
-    if len(fields) != 4:
+    f = _profile_fields(path)
+    fetch, write = f.get(f"{kernel}.fetch_bytes"), f.get(f"{kernel}.write_bytes")
+    if fetch is None or write is None:
         return None
-    return {"bytes": fields["fetch_bytes"] + fields["write_bytes"], "source": str(
-        path.relative_to(ROOT))}
+    return {"bytes": fetch + write, "source": str(path.relative_to(ROOT))}
 
 
 # Vector issue of the MI355X: 256 CUs x 4 SIMDs, each issuing one wave64 VALU instruction
