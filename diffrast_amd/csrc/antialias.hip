@@ -486,17 +486,34 @@ __device__ __forceinline__ PixelPairs pixel_pairs(const DrAntialiasArgs& a, cons
   return P;
 }
 
+// Channels [c0, c0 + n) of a pixel whose first channel is at p (n <= N; 0 past n): the widest
+// loads the alignment allows, all issued together.
+template <int N>
+__device__ __forceinline__ void load_group(const float* p, int n, float (&v)[N]) {
+  if constexpr (N == 4) {
+    if (n == 4 && load_wide<4>(p, v)) return;
+  } else if constexpr (N == 2) {
+    if (n == 2 && load_wide<2>(p, v)) return;
+  }
+#pragma unroll
+  for (int c = 0; c < N; ++c) v[c] = c < n ? p[c] : 0.0f;
+}
+
+template <int N>
+__device__ __forceinline__ void store_group(float* p, int n, const float (&v)[N]) {
+  if constexpr (N == 4 || N == 2) {
+    if (n == N && store_wide<N>(p, v)) return;
+  }
+#pragma unroll
+  for (int c = 0; c < N; ++c)
+    if (c < n) p[c] = v[c];
+}
+
 // out = colour + |t - 0.5| of the neighbour's colour on the side of each crossing
 // (reference.py:253-264). A pixel takes (0.5 - t) of its pair partner when it is the first
 // pixel and t < 0.5, and (t - 0.5) when it is the second and t >= 0.5.
-// The four channels of a pixel (16-byte loads on an aligned buffer).
-__device__ __forceinline__ void load_px4(const float* p, float (&v)[4]) {
-  if (load_wide<4>(p, v)) return;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) v[c] = p[c];
-}
-
-// NC = 4 for four-channel colours (whole-pixel loads and stores), 0 for any channel count.
+// NC channels per group: the channel count for 1 to 4 channels (whole-pixel loads and stores),
+// 4 with a loop over groups for more.
 template <int NC>
 __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const float2* pair_t,
                                                        const uchar2* pair_bits, float* out) {
@@ -515,44 +532,32 @@ __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const 
   }
   const float* color = a.color + tp.pixel * C;
   float* o = out + tp.pixel * C;
-  if constexpr (NC == 4) {
-    float own[4], v[4];
-    load_px4(color, own);
+  for (int c0 = 0; c0 < C; c0 += NC) {
+    const int n = min(NC, C - c0);
+    float own[NC], v[NC];
+    load_group<NC>(color + c0, n, own);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) v[c] = own[c];
+    for (int c = 0; c < NC; ++c) v[c] = own[c];
     if (any) {
       // Every neighbour that lends colour is read before any is used.
-      float other[4][4];
+      float other[4][NC];
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        if (weight[n] != 0.0f) {
-          load_px4(a.color + P.other[n] * 4, other[n]);
+      for (int k = 0; k < 4; ++k) {
+        if (weight[k] != 0.0f) {
+          load_group<NC>(a.color + P.other[k] * C + c0, n, other[k]);
         } else {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) other[n][c] = own[c];
+          for (int c = 0; c < NC; ++c) other[k][c] = own[c];
         }
       }
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        if (weight[n] == 0.0f) continue;
+      for (int k = 0; k < 4; ++k) {
+        if (weight[k] == 0.0f) continue;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[c] += weight[n] * (other[n][c] - own[c]);
+        for (int c = 0; c < NC; ++c) v[c] += weight[k] * (other[k][c] - own[c]);
       }
     }
-    if (!store_wide<4>(o, v))
-#pragma unroll
-      for (int c = 0; c < 4; ++c) o[c] = v[c];
-    return;
-  }
-  for (int c = 0; c < C; ++c) {
-    const float own = color[c];
-    float v = own;
-    if (any) {
-#pragma unroll
-      for (int n = 0; n < 4; ++n)
-        if (weight[n] != 0.0f) v += weight[n] * (a.color[P.other[n] * C + c] - own);
-    }
-    o[c] = v;
+    store_group<NC>(o + c0, n, v);
   }
 }
 
@@ -577,56 +582,38 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
   if (tp.inside) {
     const PixelPairs P = pixel_pairs(a, tp, pair_t, pair_bits);
     const float* g = grad_out + tp.pixel * C;
-    if (grad_color && NC == 4) {
-      float gv[4], v[4];
-      load_px4(g, gv);
+    if (grad_color) {
+      for (int c0 = 0; c0 < C; c0 += NC) {
+        const int n = min(NC, C - c0);
+        float gv[NC], v[NC];
+        load_group<NC>(g + c0, n, gv);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) v[c] = gv[c];
-      // Every active neighbour's gradient is read before any is used.
-      float g2s[4][4];
+        for (int c = 0; c < NC; ++c) v[c] = gv[c];
+        // Every active neighbour's gradient is read before any is used.
+        float g2s[4][NC];
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        if (P.active[n]) {
-          load_px4(grad_out + P.other[n] * 4, g2s[n]);
-        } else {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) g2s[n][c] = 0.0f;
-        }
-      }
-#pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        if (!P.active[n]) continue;
-        const float t = P.t[n];
-        const float (&g2)[4] = g2s[n];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          if (P.first[n]) {
-            v[c] += t < 0.5f ? -(0.5f - t) * gv[c] : (t - 0.5f) * g2[c];
+        for (int k = 0; k < 4; ++k) {
+          if (P.active[k]) {
+            load_group<NC>(grad_out + P.other[k] * C + c0, n, g2s[k]);
           } else {
-            v[c] += t < 0.5f ? (0.5f - t) * g2[c] : -(t - 0.5f) * gv[c];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) g2s[k][c] = 0.0f;
           }
         }
-      }
-      float* gc = grad_color + tp.pixel * 4;
-      if (!store_wide<4>(gc, v))
 #pragma unroll
-        for (int c = 0; c < 4; ++c) gc[c] = v[c];
-    } else if (grad_color) {
-      float* gc = grad_color + tp.pixel * C;
-      for (int c = 0; c < C; ++c) {
-        float v = g[c];
+        for (int k = 0; k < 4; ++k) {
+          if (!P.active[k]) continue;
+          const float t = P.t[k];
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          if (!P.active[n]) continue;
-          const float t = P.t[n];
-          const float* g2 = grad_out + P.other[n] * C;
-          if (P.first[n]) {
-            v += t < 0.5f ? -(0.5f - t) * g[c] : (t - 0.5f) * g2[c];
-          } else {
-            v += t < 0.5f ? (0.5f - t) * g2[c] : -(t - 0.5f) * g[c];
+          for (int c = 0; c < NC; ++c) {
+            if (P.first[k]) {
+              v[c] += t < 0.5f ? -(0.5f - t) * gv[c] : (t - 0.5f) * g2s[k][c];
+            } else {
+              v[c] += t < 0.5f ? (0.5f - t) * g2s[k][c] : -(t - 0.5f) * gv[c];
+            }
           }
         }
-        gc[c] = v;
+        store_group<NC>(grad_color + tp.pixel * C + c0, n, v);
       }
     }
     if (grad_pos) {
@@ -643,22 +630,19 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
         const float* cQ = a.color + q * C;
         const float* g2 = grad_out + q * C;
         float g_t = 0.0f;
-        if constexpr (NC == 4) {
-          float vP[4], vQ[4], vg[4];
-          load_px4(cP, vP);
-          load_px4(cQ, vQ);
-          load_px4(t < 0.5f ? g : g2, vg);
+        for (int c0 = 0; c0 < C; c0 += NC) {
+          const int m = min(NC, C - c0);
+          float vP[NC], vQ[NC], vg[NC];
+          load_group<NC>(cP + c0, m, vP);
+          load_group<NC>(cQ + c0, m, vQ);
+          load_group<NC>((t < 0.5f ? g : g2) + c0, m, vg);
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
+          for (int c = 0; c < NC; ++c) {
             if (t < 0.5f)
               g_t -= vg[c] * (vQ[c] - vP[c]);
             else
               g_t += vg[c] * (vP[c] - vQ[c]);
           }
-        } else if (t < 0.5f) {
-          for (int c = 0; c < C; ++c) g_t -= g[c] * (cQ[c] - cP[c]);
-        } else {
-          for (int c = 0; c < C; ++c) g_t += g2[c] * (cP[c] - cQ[c]);
         }
         const bool owner_first = info & kOwnerFirst;
         g_t *= owner_first ? a.boost : -a.boost;  // t = 1 - t_q when the second pixel owns it
@@ -783,11 +767,12 @@ extern "C" int dr_antialias_forward(const DrAntialiasArgs* a, void* pairs, size_
   pair_buffers(a, pairs, t, bits);
   const int64_t blocks = tile_blocks(a->batch, a->height, a->width);
   aa_pairs_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits);
-  if (a->channels == 4)
-    aa_blend_kernel<4><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, out);
-  else if (a->channels > 0)
-    aa_blend_kernel<0><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, out);
-  return launch_status();
+  if (a->channels <= 0) return launch_status();
+  return channel_groups(a->channels, [&](auto nc) {
+    constexpr int NC = decltype(nc)::value;
+    aa_blend_kernel<NC><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, out);
+    return launch_status();
+  });
 }
 
 extern "C" int dr_antialias_backward(const DrAntialiasArgs* a, const void* pairs,
@@ -805,11 +790,10 @@ extern "C" int dr_antialias_backward(const DrAntialiasArgs* a, const void* pairs
   uchar2* bits;
   pair_buffers(a, (void*)pairs, t, bits);
   const int64_t blocks = tile_blocks(a->batch, a->height, a->width);
-  if (a->channels == 4)
-    aa_bwd_kernel<4><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, grad_out, grad_color,
-                                                               grad_pos);
-  else
-    aa_bwd_kernel<0><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, grad_out, grad_color,
-                                                               grad_pos);
-  return launch_status();
+  return channel_groups(a->channels, [&](auto nc) {
+    constexpr int NC = decltype(nc)::value;
+    aa_bwd_kernel<NC><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, grad_out,
+                                                                grad_color, grad_pos);
+    return launch_status();
+  });
 }

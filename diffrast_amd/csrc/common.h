@@ -6,6 +6,8 @@
 // (src/diffrast/backends/reference.py) bit for bit.
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -91,6 +93,17 @@ __device__ __forceinline__ bool store_wide(float* p, const float (&v)[N]) {
 }
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Launches of kernels templated on NC channels per group: 1-4 as they are, more in groups of 4.
+template <typename F>
+int channel_groups(int channels, F f) {
+  switch (channels) {
+    case 1: return f(std::integral_constant<int, 1>());
+    case 2: return f(std::integral_constant<int, 2>());
+    case 3: return f(std::integral_constant<int, 3>());
+    default: return f(std::integral_constant<int, 4>());
+  }
+}
 
 // Sum of v over the lanes of the wave whose bit is set in `mask`, valid in every lane.
 __device__ __forceinline__ float wave_masked_sum(float v, uint64_t mask) {

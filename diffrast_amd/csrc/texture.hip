@@ -624,17 +624,6 @@ bool valid_args(const DrTextureArgs* a) {
   return true;
 }
 
-// Kernels templated on NC channels per pass: 1-4 as they are, more in passes of 4.
-template <typename F>
-int dispatch_channels(int channels, F f) {
-  switch (channels) {
-    case 1: return f(std::integral_constant<int, 1>());
-    case 2: return f(std::integral_constant<int, 2>());
-    case 3: return f(std::integral_constant<int, 3>());
-    default: return f(std::integral_constant<int, 4>());
-  }
-}
-
 }  // namespace
 }  // namespace dr
 
@@ -646,7 +635,7 @@ extern "C" int dr_texture_forward(const DrTextureArgs* a, float* out, void* stre
   if (pixels == 0) return DR_OK;
   const DrTextureArgs args = *a;
   const bool cube = args.boundary == DR_BOUNDARY_CUBE;
-  return dispatch_channels(args.channels, [&](auto nc) {
+  return channel_groups(args.channels, [&](auto nc) {
     constexpr int NC = decltype(nc)::value;
     if (cube)
       tex_fwd_kernel<NC, true><<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(args, out);
@@ -668,7 +657,7 @@ extern "C" int dr_texture_backward(const DrTextureArgs* a, const float* grad_out
   const int64_t blocks = tile_blocks(args.batch, args.height, args.width);
   float* g_da = args.uv_da ? grad_uv_da : nullptr;
   float* g_bias = args.bias ? grad_bias : nullptr;
-  return dispatch_channels(args.channels, [&](auto nc) {
+  return channel_groups(args.channels, [&](auto nc) {
     constexpr int NC = decltype(nc)::value;
     if (cube)
       tex_bwd_kernel<NC, true><<<blocks, 256, 0, (hipStream_t)stream>>>(
