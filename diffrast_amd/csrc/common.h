@@ -309,6 +309,68 @@ inline int64_t tile_blocks(int batch, int height, int width) {
   return (int64_t)batch * ((width + 15) / 16) * ((height + 15) / 16);
 }
 
+// The pixels of a thread in the gather kernels (resolve, interpolate forward), in one of two
+// layouts. Rows: PPT pixels 256 apart in pixel order, so every wave reads and writes runs of 64
+// consecutive pixels; best when what the pixels gather (index rows, vertices, attributes) stays
+// in the L2s anyway, or when the pass is bound by its writes. Tiles: a 16 x 16 PPT tile per
+// workgroup, the tiles in XCD order, pixel j at (x, y0 + 16 j); the pixels of a triangle and of
+// its neighbours, which share vertices, then gather into one XCD's L2 rather than one per image
+// row, which pays when the gathered data outgrows an L2.
+template <int PPT>
+struct PixelSlots {
+  int64_t pixel[PPT];
+  int b[PPT], x[PPT], y[PPT];
+  bool inside[PPT];
+};
+
+template <int PPT, bool TILES>
+__device__ __forceinline__ PixelSlots<PPT> pixel_slots(int batch, int height, int width) {
+  PixelSlots<PPT> s;
+  if constexpr (TILES) {
+    const int tiles_x = (width + 15) / 16, tiles_y = (height + 16 * PPT - 1) / (16 * PPT);
+    const int64_t tile = xcd_order(blockIdx.x, (int64_t)batch * tiles_x * tiles_y);
+    const int b = (int)(tile / ((int64_t)tiles_x * tiles_y));
+    const int in_image = (int)(tile - (int64_t)b * tiles_x * tiles_y);
+    const int x = (in_image % tiles_x) * 16 + (int)(threadIdx.x & 15);
+    const int y0 = (in_image / tiles_x) * 16 * PPT + (int)(threadIdx.x >> 4);
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      s.b[j] = b;
+      s.x[j] = x;
+      s.y[j] = y0 + 16 * j;
+      s.inside[j] = x < width && s.y[j] < height;
+      s.pixel[j] = ((int64_t)b * height + s.y[j]) * width + x;
+    }
+  } else {
+    const int64_t image_pixels = (int64_t)height * width;
+    const int64_t total = (int64_t)batch * image_pixels;
+    const int64_t first = (int64_t)blockIdx.x * blockDim.x * PPT + threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int64_t pixel = first + (int64_t)j * blockDim.x;
+      s.pixel[j] = pixel;
+      s.inside[j] = pixel < total;
+      s.b[j] = pixel < 0xffffffffLL && image_pixels < 0xffffffffLL
+                   ? (int)((uint32_t)pixel / (uint32_t)image_pixels)
+                   : (int)(pixel / image_pixels);
+      const int64_t in_image = pixel - (int64_t)s.b[j] * image_pixels;
+      s.y[j] = (int)(in_image / width);
+      s.x[j] = (int)(in_image - (int64_t)s.y[j] * width);
+    }
+  }
+  return s;
+}
+
+template <int PPT, bool TILES>
+inline int64_t pixel_slot_blocks(int batch, int height, int width) {
+  if (TILES) return (int64_t)batch * ((width + 15) / 16) * ((height + 16 * PPT - 1) / (16 * PPT));
+  return blocks_for((int64_t)batch * height * width, 256 * PPT);
+}
+
+// Whether a gather kernel takes the tile layout: when the mesh data one image's pixels gather
+// is larger than an XCD's 4 MiB L2.
+inline bool gather_tiles(int64_t gathered_bytes) { return gathered_bytes > (int64_t)4 << 20; }
+
 // ---- workgroup scatter table --------------------------------------------------------------
 
 // Fixed-point scale of one accumulation pass of a workgroup. LDS float atomics are slow on

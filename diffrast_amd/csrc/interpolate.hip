@@ -102,35 +102,27 @@ __device__ __forceinline__ float pick(const float (&row)[N], int c) {
 // Channels per pass of the generic kernel (any channel count).
 constexpr int kGenericChannels = 4;
 
-// PPT pixels per thread, 256 apart (each load instruction of a wave stays coalesced). The
-// pixels' loads go out level by level -- rast, then the triangles' index rows, then the
-// attribute rows -- so that a thread waits once per level for all its pixels, not once per
-// pixel: the gathers are latency-bound.
-template <int NC, int PPT>
+// PPT pixels per thread, in rows or tiles (pixel_slots). The pixels' loads go out level by
+// level -- rast, then the triangles' index rows, then the attribute rows -- so that a thread
+// waits once per level for all its pixels, not once per pixel: the gathers are latency-bound.
+template <int NC, int PPT, bool TILES>
 __global__ __launch_bounds__(256) void interp_fwd_kernel(DrInterpolateArgs a,
                                                          float* __restrict__ out,
                                                          float* __restrict__ out_da,
                                                          uint32_t rows_per_image) {
-  const int64_t image_pixels = (int64_t)a.height * a.width;
-  const int64_t total = (int64_t)a.batch * image_pixels;
-  const int64_t first = (int64_t)blockIdx.x * blockDim.x * PPT + threadIdx.x;
+  const PixelSlots<PPT> s = pixel_slots<PPT, TILES>(a.batch, a.height, a.width);
   const int C = NC > 0 ? NC : a.channels;
   constexpr int N = NC > 0 ? NC : kGenericChannels;
-  int64_t pixel[PPT];
+  const int64_t* pixel = s.pixel;
   float4 r[PPT];
 #pragma unroll
-  for (int j = 0; j < PPT; ++j) {
-    pixel[j] = first + (int64_t)j * blockDim.x;
-    r[j] = pixel[j] < total ? load4(a.rast + 4 * pixel[j]) : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  for (int j = 0; j < PPT; ++j)
+    r[j] = s.inside[j] ? load4(a.rast + 4 * pixel[j]) : make_float4(0.f, 0.f, 0.f, 0.f);
   Pixel p[PPT];
   float4 db[PPT];
 #pragma unroll
   for (int j = 0; j < PPT; ++j) {
-    const int image = image_pixels < 0x7fffffff && pixel[j] < 0x7fffffff
-                          ? (int)((uint32_t)pixel[j] / (uint32_t)image_pixels)
-                          : (int)(pixel[j] / image_pixels);
-    p[j] = pixel_of(a, r[j], image, rows_per_image);
+    p[j] = pixel_of(a, r[j], s.b[j], rows_per_image);
     db[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (out_da != nullptr && p[j].valid) db[j] = load4(a.rast_db + 4 * pixel[j]);  // du/dx, du/dy, dv/dx, dv/dy
   }
@@ -147,7 +139,7 @@ __global__ __launch_bounds__(256) void interp_fwd_kernel(DrInterpolateArgs a,
     }
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-      if (pixel[j] >= total) continue;
+      if (!s.inside[j]) continue;
       const float u = p[j].u, v = p[j].v, w = 1.0f - u - v;
       float res[N];
 #pragma unroll
@@ -318,11 +310,21 @@ extern "C" int dr_interpolate_forward(const DrInterpolateArgs* a, float* out, fl
   const DrInterpolateArgs args = *a;
   const uint32_t rows_per_image = image_rows(args);
   float* da = args.num_diff > 0 ? out_da : nullptr;
+  // The index rows and attribute rows one image's pixels may gather.
+  const int64_t rows = rows_per_image != 0 ? rows_per_image : args.num_vertices;
+  const bool tiles = gather_tiles(12 * (int64_t)args.num_tri + 4 * rows * args.channels);
   return dispatch_channels(args.channels, [&](auto nc) {
     constexpr int NC = decltype(nc)::value;
     constexpr int PPT = NC > 0 ? 2 : 1;  // pixels per thread
-    interp_fwd_kernel<NC, PPT><<<blocks_for(pixels, 256 * PPT), 256, 0, (hipStream_t)stream>>>(
-        args, out, da, rows_per_image);
+    const hipStream_t st = (hipStream_t)stream;
+    if (tiles)
+      interp_fwd_kernel<NC, PPT, true>
+          <<<pixel_slot_blocks<PPT, true>(args.batch, args.height, args.width), 256, 0, st>>>(
+              args, out, da, rows_per_image);
+    else
+      interp_fwd_kernel<NC, PPT, false>
+          <<<pixel_slot_blocks<PPT, false>(args.batch, args.height, args.width), 256, 0, st>>>(
+              args, out, da, rows_per_image);
     return launch_status();
   });
 }

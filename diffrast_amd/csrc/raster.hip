@@ -1417,22 +1417,19 @@ __device__ __forceinline__ void resolve_pixel(const Tri& T, float px, float py, 
   }
 }
 
-// Two pixels per thread, 256 apart; their loads go out level by level (keys, index rows,
-// vertices) so that a thread waits once per level for both.
+// Two pixels per thread, in rows or tiles (pixel_slots); their loads go out level by level
+// (keys, index rows, vertices) so that a thread waits once per level for both.
+template <bool TILES>
 __global__ __launch_bounds__(256) void resolve_fwd_kernel(DrRasterGeometry g,
-                                                              const uint64_t* keys, float* rast,
-                                                              float* rast_db, float scale_x,
-                                                              float scale_y) {
+                                                          const uint64_t* keys, float* rast,
+                                                          float* rast_db, float scale_x,
+                                                          float scale_y) {
   constexpr int kPixels = 2;
-  const int64_t total = (int64_t)g.batch * g.height * g.width;
-  const int64_t first = (int64_t)blockIdx.x * blockDim.x * kPixels + threadIdx.x;
-  int64_t pixel[kPixels];
+  const PixelSlots<kPixels> s = pixel_slots<kPixels, TILES>(g.batch, g.height, g.width);
+  const int64_t* pixel = s.pixel;
   uint64_t key[kPixels];
 #pragma unroll
-  for (int j = 0; j < kPixels; ++j) {
-    pixel[j] = first + (int64_t)j * blockDim.x;
-    key[j] = pixel[j] < total ? keys[pixel[j]] : kEmptyKey;
-  }
+  for (int j = 0; j < kPixels; ++j) key[j] = s.inside[j] ? keys[pixel[j]] : kEmptyKey;
   // The pixels' index rows, then their vertices, each level's loads issued together: in a wave
   // with any covered pixel every lane reads (triangle 0 of image 0 for an empty one), with no
   // branch between the pixels.
@@ -1443,11 +1440,7 @@ __global__ __launch_bounds__(256) void resolve_fwd_kernel(DrRasterGeometry g,
   for (int j = 0; j < kPixels; ++j) {
     const bool hit = key[j] != kEmptyKey;
     covered = covered || hit;
-    const int64_t image_pixels = (int64_t)g.height * g.width;
-    const int image = pixel[j] < 0xffffffffLL && image_pixels < 0xffffffffLL
-                          ? (int)((uint32_t)pixel[j] / (uint32_t)image_pixels)
-                          : (int)(pixel[j] / image_pixels);
-    b[j] = hit ? image : 0;
+    b[j] = hit ? s.b[j] : 0;
     v[j][0] = v[j][1] = v[j][2] = 0;
   }
   Tri T[kPixels];
@@ -1464,17 +1457,15 @@ __global__ __launch_bounds__(256) void resolve_fwd_kernel(DrRasterGeometry g,
   }
 #pragma unroll
   for (int j = 0; j < kPixels; ++j) {
-    if (pixel[j] >= total) continue;
+    if (!s.inside[j]) continue;
     if (key[j] == kEmptyKey) {
       store4(rast + 4 * pixel[j], make_float4(0.f, 0.f, 0.f, 0.f));
       if (rast_db) store4(rast_db + 4 * pixel[j], make_float4(0.f, 0.f, 0.f, 0.f));
       continue;
     }
     const int t = (int)(uint32_t)key[j];
-    const int64_t in_image = pixel[j] - (int64_t)b[j] * g.height * g.width;
-    const int y = (int)(in_image / g.width), x = (int)(in_image - (int64_t)y * g.width);
     Resolved R;
-    resolve_pixel(T[j], pixel_centre(x, g.width), pixel_centre(y, g.height), R);
+    resolve_pixel(T[j], pixel_centre(s.x[j], g.width), pixel_centre(s.y[j], g.height), R);
     store4(rast + 4 * pixel[j], make_float4(R.b[0], R.b[1], R.depth, (float)(t + 1)));
     if (rast_db)
       store4(rast_db + 4 * pixel[j], make_float4(R.db_dx[0] * scale_x, R.db_dy[0] * scale_y,
@@ -1872,8 +1863,16 @@ extern "C" int dr_resolve_forward(const DrRasterGeometry* g, const uint64_t* key
   if (pixels == 0) return DR_OK;
   float sx, sy;
   resolve_scales(g, sx, sy);
-  resolve_fwd_kernel<<<blocks_for(pixels, 512), 256, 0, (hipStream_t)stream>>>(
-      *g, keys, rast, rast_db, sx, sy);
+  // The index rows and vertices one image's pixels may gather: a range item draws its own
+  // triangles only; a closed mesh has about half a vertex per triangle.
+  const int64_t image_tris = g->ranges != nullptr ? g->num_tri / std::max(g->batch, 1) : g->num_tri;
+  const hipStream_t st = (hipStream_t)stream;
+  if (gather_tiles(20 * image_tris))
+    resolve_fwd_kernel<true><<<pixel_slot_blocks<2, true>(g->batch, g->height, g->width), 256, 0,
+                               st>>>(*g, keys, rast, rast_db, sx, sy);
+  else
+    resolve_fwd_kernel<false><<<pixel_slot_blocks<2, false>(g->batch, g->height, g->width), 256,
+                                0, st>>>(*g, keys, rast, rast_db, sx, sy);
   return launch_status();
 }
 

@@ -155,6 +155,42 @@ def test_subdivided_sphere_in_spatial_order():
     assert_layers_match(pos, tri, (96, 96), count=2)
 
 
+@pytest.mark.parametrize("resolution", [(97, 131), (48, 40)])
+def test_mesh_outgrowing_an_l2_every_pixel_from_ids(resolution):
+    # icosphere(7), 327,680 triangles: the index rows and vertices one image's pixels gather
+    # outgrow an XCD's L2, so resolve and interpolate take their tile layout. At sizes that are
+    # not multiples of the tiles, rast, rast_db and the interpolated attributes of every pixel
+    # must match the oracle run from the GPU's ids (ids bit-exact against brute force at
+    # sampled pixels).
+    from diffrast_amd import workloads as W
+    gen = torch.Generator().manual_seed(31)
+    verts, tri = W.icosphere(7)
+    verts = verts * (1 + 0.02 * torch.randn(verts.shape[0], 1, generator=gen))
+    h, w = resolution
+    pos = W.clip_positions(verts, W.random_eyes(3, 2.5, gen), w / h)
+    rast, db, _ = hip.rasterize_layer(pos.cuda(), tri.cuda(), resolution, True, None)
+    rast, db = rast.cpu(), db.cpu()
+    ids = rast[..., 3].long() - 1
+    assert (ids >= 0).sum() > 0.2 * ids.numel()
+    b = torch.arange(3).repeat_interleave(16)
+    row = torch.randint(0, h, (48,), generator=gen)
+    col = torch.randint(0, w, (48,), generator=gen)
+    _, expect_ids = R.visible_at(pos, tri, h, w, b, row, col)
+    assert torch.equal(ids[b, row, col], expect_ids)
+    ref, ref_db = R.rasterize_from_ids(pos, tri, ids, True)
+    assert torch.equal(rast[..., 3], ref[..., 3])
+    assert rel_error(rast[..., :3], ref[..., :3]) < VALUE_TOL
+    assert rel_error(db, ref_db) < VALUE_TOL
+    attr = torch.randn(verts.shape[0], 8, generator=gen)
+    uv = W.spherical_uv(verts)
+    for a, diff in ((attr, ()), (uv, (0, 1))):
+        out, out_da = hip.interpolate(a.cuda(), rast.cuda(), tri.cuda(), db.cuda(), diff)
+        e_out, e_da = R.interpolate(a, rast, tri, db, list(diff))
+        assert torch.equal(out.cpu(), e_out)
+        if diff:
+            assert rel_error(out_da.cpu(), e_da) < VALUE_TOL
+
+
 @pytest.mark.parametrize("w_range", [(1.0, 2.0), (-1.0, 2.0)])
 def test_every_pixel_of_every_layer(w_range):
     gen = torch.Generator().manual_seed(9)
