@@ -128,6 +128,7 @@ OP_OF = {
     "dr_raster_visibility": "rasterize",
     "dr_raster_visibility_overflow": "rasterize",
     "dr_raster_visibility_static": "rasterize",
+    "dr_raster_order": "rasterize",
     "dr_resolve_forward": "rasterize",
     "dr_resolve_backward": "rasterize",
     "dr_interpolate_forward": "interpolate",

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent.parent / "libdiffrast_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 MAX_LEVELS = 32
 
 c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -35,6 +35,7 @@ class RasterGeometry(ctypes.Structure):
         ("num_instances", ctypes.c_int64),
         ("num_vertices", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("order", c_void_p),
     ]
 
 
@@ -105,6 +106,8 @@ _SIGNATURES = {
     "dr_abi_version": ([], ctypes.c_int),
     "dr_struct_size": ([ctypes.c_int], ctypes.c_int),
     "dr_raster_workspace_size": ([_P, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+    "dr_raster_order_size": ([_P, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+    "dr_raster_order": ([_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P], ctypes.c_int),
     "dr_raster_visibility_begin": (
         [_P, _P, _P, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_uint32), _P], ctypes.c_int),
     "dr_raster_visibility_start": ([_P, _P, _P, _P, ctypes.c_size_t, _P, _P], ctypes.c_int),

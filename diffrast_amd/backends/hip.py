@@ -104,6 +104,7 @@ class _Geometry:
             num_vertices=int(pos.shape[-2]),
         )
         self.shape = (self.batch, int(height), int(width))
+        self.order = None  # the processing order the struct points to, kept alive with it
 
 
 class _Sizes:
@@ -158,6 +159,61 @@ def _remember(key: tuple, sizes: _Sizes) -> None:
         _SIZES[key] = sizes
 
 
+class _Order:
+    """A mesh's processing order on the device and whether a captured graph refers to it."""
+
+    __slots__ = ("tensor", "pinned")
+
+    def __init__(self, tensor: Tensor):
+        self.tensor, self.pinned = tensor, False
+
+
+_ORDERS: dict[tuple, _Order] = {}
+_ORDERS_KEPT = 8
+_orders_lock = threading.Lock()
+
+
+def _order(geo: _Geometry, workspace: Tensor, workspace_bytes: int, capturing: bool) -> None:
+    """Sets geo.struct.order to the processing order of geo's mesh, computed once per tri
+    (its storage, version and size, and the vertex count) and reused: the order is a spatial
+    sort that only the speed of the visibility depends on, so an order computed from earlier
+    positions of the same triangles stays valid. Under graph capture a remembered order is used
+    and then kept for good (the graph refers to it); none is computed there (the captured
+    visibility computes its own into the workspace)."""
+    size = ctypes.c_size_t()
+    call("dr_raster_order_size", ref(geo.struct), ctypes.byref(size))
+    if size.value == 0:
+        return
+    tri, device = geo.tri, geo.pos.device
+    if tri.is_inference():  # no version counter to tell a changed tri: the call orders itself
+        return
+    key = (device.index, tri.data_ptr(), tri._version, geo.struct.num_tri,
+           geo.struct.num_vertices)
+    with _orders_lock:
+        entry = _ORDERS.get(key)
+        if entry is not None and capturing:
+            entry.pinned = True
+    if entry is None:
+        if capturing:
+            return
+        tensor = torch.empty(size.value, dtype=torch.uint8, device=device)
+        call("dr_raster_order", ref(geo.struct), ptr(tensor), size.value, ptr(workspace),
+             workspace_bytes, _lib.stream(device))
+        entry = _Order(tensor)
+        with _orders_lock:
+            if len(_ORDERS) >= _ORDERS_KEPT and key not in _ORDERS:
+                for old in list(_ORDERS):
+                    if not _ORDERS[old].pinned:
+                        _ORDERS.pop(old)
+                        break
+            _ORDERS[key] = entry
+    elif not capturing:
+        # Freed later (once evicted) while this call's kernels may still read it.
+        entry.tensor.record_stream(torch.cuda.current_stream(device))
+    geo.order = entry.tensor
+    geo.struct.order = entry.tensor.data_ptr()
+
+
 def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
     """Visibility keys [batch, height, width] (int64 holding the uint64 key bits).
 
@@ -176,6 +232,7 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
     stream = _lib.stream(device)
     key = (device.index, geo.shape, geo.struct.num_tri, geo.struct.num_instances, prev is None)
     capturing = torch.cuda.is_current_stream_capturing()
+    _order(geo, workspace, size.value, capturing)
     with _sizes_lock:
         sizes = _SIZES.get(key)
     if sizes is None and not capturing:

@@ -15,7 +15,7 @@ extern "C" const char* dr_error_string(int code) {
   }
 }
 
-extern "C" int dr_abi_version(void) { return 12; }
+extern "C" int dr_abi_version(void) { return 13; }
 
 extern "C" int dr_struct_size(int which) {
   switch (which) {

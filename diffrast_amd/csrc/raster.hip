@@ -144,6 +144,7 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
   }
   w.records = (float4*)take(sizeof(float4) * kRecord * 256 * (size_t)w.record_blocks);
   w.bytes = off;
+  if (w.ordered && g.order != nullptr) w.order = (int4*)g.order;
   return w;
 }
 
@@ -1618,6 +1619,42 @@ static int64_t tile_grid_bound(const Workspace& ws) {
                                : kXcdShares * ((ws.tiles + kXcdShares - 1) / kXcdShares);
 }
 
+// The order passes, into ws.order (after raster_prepare has zeroed the bucket counts).
+static void queue_order(const DrRasterGeometry& g, const Workspace& ws, hipStream_t s) {
+  const int tri_blocks = blocks_for(g.num_tri, 256);
+  order_centroids<<<tri_blocks, 256, 0, s>>>(g, ws);
+  order_bounds<<<1, 256, 0, s>>>(ws, tri_blocks);
+  const int bucket_blocks = blocks_for(g.num_tri, 256 * kOrderPerThread);
+  order_count<<<bucket_blocks, 256, 0, s>>>(g, ws);
+  order_scan<<<1, 256, 0, s>>>(ws);
+  order_place<<<bucket_blocks, 256, 0, s>>>(g, ws);
+}
+
+extern "C" int dr_raster_order_size(const DrRasterGeometry* g, size_t* bytes) {
+  if (!valid_geometry(g) || !bytes) return DR_ERR_ARGUMENT;
+  *bytes = use_order(*g) ? sizeof(int4) * (size_t)g->num_tri : 0;
+  return DR_OK;
+}
+
+extern "C" int dr_raster_order(const DrRasterGeometry* g, void* order, size_t order_bytes,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  size_t need = 0;
+  const int status = dr_raster_order_size(g, &need);
+  if (status != DR_OK || need == 0) return status;
+  if (!order || order_bytes < need) return DR_ERR_CAPACITY;
+  DrRasterGeometry own = *g;
+  own.order = nullptr;
+  Workspace ws = layout(own, (char*)workspace);
+  if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
+  ws.order = (int4*)order;
+  hipStream_t s = (hipStream_t)stream;
+  // raster_prepare with no pixels: the bucket counts (and the other counts) zeroed.
+  raster_prepare<<<(int)std::min<int64_t>(blocks_for(ws.lists + 1, 256), 65536), 256, 0, s>>>(
+      nullptr, 0, ws, g->width, g->height);
+  queue_order(own, ws, s);
+  return launch_status();
+}
+
 // Queues the first part of the visibility and the copy of its counts to host_counts.
 static int queue_visibility_start(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                   uint64_t* keys, void* workspace, size_t workspace_bytes,
@@ -1633,15 +1670,7 @@ static int queue_visibility_start(const DrRasterGeometry* g, const uint64_t* pre
   raster_prepare<<<(int)std::min<int64_t>(blocks_for(fill_items, 256), 65536), 256, 0, s>>>(
       keys, pixels, ws, g->width, g->height);
   if (g->num_instances > 0) {
-    if (ws.ordered) {
-      const int tri_blocks = blocks_for(g->num_tri, 256);
-      order_centroids<<<tri_blocks, 256, 0, s>>>(*g, ws);
-      order_bounds<<<1, 256, 0, s>>>(ws, tri_blocks);
-      const int bucket_blocks = blocks_for(g->num_tri, 256 * kOrderPerThread);
-      order_count<<<bucket_blocks, 256, 0, s>>>(*g, ws);
-      order_scan<<<1, 256, 0, s>>>(ws);
-      order_place<<<bucket_blocks, 256, 0, s>>>(*g, ws);
-    }
+    if (ws.ordered && g->order == nullptr) queue_order(*g, ws, s);
     raster_depth_range<<<ws.depth_ranges * kRangeParts, 256, 0, s>>>(*g, ws);
     raster_depth_range_merge<<<ws.depth_ranges, kRangeParts, 0, s>>>(ws);
     raster_setup_kernel<<<blocks_for(g->num_instances, 256), 256, 0, s>>>(*g, prev_keys, keys,

@@ -67,10 +67,26 @@ typedef struct DrRasterGeometry {
   int64_t num_instances;       /* batch * num_tri, or range_prefix[batch] */
   int32_t num_vertices;        /* vertices per image in pos */
   int32_t reserved;            /* 0 */
+  const void* order;           /* NULL, or the processing order dr_raster_order wrote for this
+                                  tri (and num_vertices), reused instead of computed again */
 } DrRasterGeometry;
 
 /* Bytes of the visibility workspace for this geometry. */
 int dr_raster_workspace_size(const DrRasterGeometry* g, size_t* bytes);
+
+/* The processing order of a large mesh, for reuse: its triangles sorted by the Morton code of
+ * their centroid in the first image's clip space (an affine image of world space, so the order
+ * keeps its locality for any camera), each with its three vertex rows. The visibility passes
+ * compute it in every call that gets geometry.order == NULL; a caller that draws one tri many
+ * times computes it once with dr_raster_order and passes it in. The keys do not depend on the
+ * order (only the speed does), so an order computed from other positions of the same tri is
+ * valid; one computed from another tri (or num_vertices) is not. *bytes = 0 when the geometry
+ * keeps the mesh's own order (range mode, or fewer than 8192 triangles). workspace is a
+ * visibility workspace (dr_raster_workspace_size). No counterpart in the reference: its Triton
+ * rasterizer bins triangles in index order (_triton_rasterize.py:371-424). */
+int dr_raster_order_size(const DrRasterGeometry* g, size_t* bytes);
+int dr_raster_order(const DrRasterGeometry* g, void* order, size_t order_bytes, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 /* Visibility, first part: clears keys, orders the triangles of a large mesh spatially,
  * rasterizes triangles with a small bounding box directly, bins the others into 16x16 tiles

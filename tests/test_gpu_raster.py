@@ -191,6 +191,36 @@ def test_mesh_outgrowing_an_l2_every_pixel_from_ids(resolution):
             assert rel_error(out_da.cpu(), e_da) < VALUE_TOL
 
 
+def test_processing_order_is_reused_per_tri_and_recomputed_when_tri_changes():
+    # A large mesh's processing order is computed once per tri and reused with other
+    # positions (the keys do not depend on it); an in-place change of tri makes a new one.
+    from diffrast_amd import workloads as W
+    gen = torch.Generator().manual_seed(23)
+    verts, tri = W.icosphere(5)
+    tri_dev = tri.cuda()
+    hip._ORDERS.clear()
+    for eyes_seed in (1, 2):
+        eyes = W.random_eyes(2, 3.0, torch.Generator().manual_seed(eyes_seed))
+        pos = W.clip_positions(verts * (1 + 0.02 * torch.randn(verts.shape[0], 1, generator=gen)),
+                               eyes, 1.0)
+        rast, db, _ = hip.rasterize_layer(pos.cuda(), tri_dev, (64, 80), True, None)
+        (er, ed), = oracle_layers(pos, tri, (64, 80), 1)
+        assert torch.equal(rast[..., 3].cpu(), er[..., 3])
+        assert rel_error(rast[..., :3].cpu(), er[..., :3]) < VALUE_TOL
+        assert len(hip._ORDERS) == 1
+    order = next(iter(hip._ORDERS.values())).tensor
+    # Reverse every triangle's winding in place: a new tri, a new order.
+    tri_dev[:, [1, 2]] = tri_dev[:, [2, 1]]
+    flipped = tri[:, [0, 2, 1]].contiguous()
+    rast, db, _ = hip.rasterize_layer(pos.cuda(), tri_dev, (64, 80), True, None)
+    (er, ed), = oracle_layers(pos, flipped, (64, 80), 1)
+    assert torch.equal(rast[..., 3].cpu(), er[..., 3])
+    assert rel_error(db.cpu(), ed) < VALUE_TOL
+    assert len(hip._ORDERS) == 2
+    assert all(e.tensor.data_ptr() != order.data_ptr() or e.tensor is order
+               for e in hip._ORDERS.values())
+
+
 @pytest.mark.parametrize("w_range", [(1.0, 2.0), (-1.0, 2.0)])
 def test_every_pixel_of_every_layer(w_range):
     gen = torch.Generator().manual_seed(9)
