@@ -1116,7 +1116,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   __shared__ unsigned long long s_key[kTile * kTile];
   __shared__ float s_px[kTile], s_py[kTile];
   __shared__ uint64_t s_far[256 / DR_WAVE];
-  __shared__ uint64_t s_row_far[kTile];  // the farthest key of each tile row
+  __shared__ float s_row_far[kTile];  // the depth of the farthest key of each tile row (NaN: empty)
   __shared__ float s_bound[kChunk];  // lower bound of each staged triangle's depth
 
   // Workgroups are dispatched round-robin over the 8 XCDs: XCD k runs the busy tiles of share
@@ -1191,7 +1191,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     __syncthreads();  // the previous chunk's merges (and the set-up above) are done
     const uint64_t own_key = inside ? s_key[threadIdx.x] : 0ull;
     const uint64_t row_far = row_max_u64(own_key);  // a wave holds four rows of the tile
-    if ((lane & (kTile - 1)) == kTile - 1) s_row_far[threadIdx.x / kTile] = row_far;
+    if ((lane & (kTile - 1)) == kTile - 1) s_row_far[threadIdx.x / kTile] = key_depth(row_far);
     uint64_t far_key = wave_max_u64(own_key);
     if (lane == 0) s_far[wave] = far_key;
     __syncthreads();
@@ -1236,7 +1236,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
           if (spans) row_span(se, s_py[r], lo, hi);
           // Every pixel of the row already holds a key nearer than the triangle can reach (an
           // empty key reads as NaN and never compares greater).
-          if (bound > key_depth(s_row_far[r])) hi = lo - 1;
+          if (bound > s_row_far[r]) hi = lo - 1;
           if (lo <= hi) {
             s_span[threadIdx.x][held++] = (uint16_t)(items << 8 | lo << 4 | r);
             items += hi - lo + 1;
