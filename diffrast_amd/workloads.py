@@ -247,12 +247,11 @@ def reflect(view: Tensor, view_da: Tensor, n: Tensor, n_da: Tensor) -> tuple[Ten
     (layouts of interpolate's ``out_da``: (d/dx, d/dy) per component)."""
     d = (view * n).sum(-1, keepdim=True)
     dirs = view - 2 * d * n
-    parts = []
-    for axis in (0, 1):
-        dv, dn = view_da[..., axis::2], n_da[..., axis::2]
-        dd = (dv * n).sum(-1, keepdim=True) + (view * dn).sum(-1, keepdim=True)
-        parts.append(dv - 2 * (dd * n + d * dn))
-    return dirs, torch.stack(parts, -1).reshape(*dirs.shape[:-1], 6)
+    # The derivatives as [..., component, axis], both axes at once (no strided slices).
+    dv, dn = view_da.unflatten(-1, (3, 2)), n_da.unflatten(-1, (3, 2))
+    dd = (dv * n[..., None]).sum(-2) + (view[..., None] * dn).sum(-2)  # [..., axis]
+    dirs_da = dv - 2 * (dd[..., None, :] * n[..., None] + d[..., None] * dn)
+    return dirs, dirs_da.flatten(-2)
 
 
 # ---------------------------------------------------------------------------------------------

@@ -1,6 +1,7 @@
-"""The reference's published benchmark scene (displaced grid) and the chart of its sweep, on the
-CPU: the scene against closed forms of its construction (benchmarks/bench_rasterize.py:19-52,
-bench_pipeline.py:24-28), the chart as well-formed SVG whose points follow the values."""
+"""Benchmark scenes on the CPU: the reference's published one (displaced grid) against closed
+forms of its construction (benchmarks/bench_rasterize.py:19-52, bench_pipeline.py:24-28), the
+chart of its sweep as well-formed SVG whose points follow the values, and the cube-map
+workload's reflected rays against forward-mode derivatives."""
 
 import json
 import math
@@ -113,3 +114,23 @@ def test_published_figures_are_looked_up_by_requested_count_and_views():
     assert pipeline_bench.published(1_000_000, 1024, 8) == (27.32, 57.88)
     assert pipeline_bench.published(1_000_000, 1024, 1) is None
     assert pipeline_bench.published(50_000, 1024, 8) is None
+
+
+def test_reflection_and_its_screen_space_derivatives():
+    # The cube-map workload's directions: r = v - 2 (n . v) n, and per screen axis the
+    # derivative of r along (v + t dv, n + t dn) at t = 0 (forward mode in float64), in
+    # interpolate's out_da layout (d/dx, d/dy of each component in turn).
+    gen = torch.Generator().manual_seed(3)
+    view = torch.randn(2, 5, 7, 3, dtype=torch.float64, generator=gen)
+    n = torch.randn(2, 5, 7, 3, dtype=torch.float64, generator=gen)
+    view_da = torch.randn(2, 5, 7, 6, dtype=torch.float64, generator=gen)
+    n_da = torch.randn(2, 5, 7, 6, dtype=torch.float64, generator=gen)
+    dirs, dirs_da = workloads.reflect(view, view_da, n, n_da)
+
+    def r(v, m):
+        return v - 2 * (v * m).sum(-1, keepdim=True) * m
+
+    torch.testing.assert_close(dirs, r(view, n), atol=1e-14, rtol=0)
+    for axis in (0, 1):
+        _, jvp = torch.func.jvp(r, (view, n), (view_da[..., axis::2], n_da[..., axis::2]))
+        torch.testing.assert_close(dirs_da[..., axis::2], jvp, atol=1e-12, rtol=0)
