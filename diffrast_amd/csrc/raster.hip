@@ -13,7 +13,7 @@
 //    patch of the screen, which makes the binning below aggregate well.
 // 2. Setup: one thread per triangle instance culls it (a non-finite coordinate, or every w <= 0:
 //    the interpolated w is then never positive) and bounds its pixels. Boxes of at most
-//    kSmallPixels pixel centres are rasterized right away (64-bit atomic min per covered
+//    small_pixels() pixel centres are rasterized right away (64-bit atomic min per covered
 //    pixel); the others are binned into 16x16 tiles. Per-tile counts gather in an LDS table of
 //    the workgroup before one global atomic per distinct tile.
 // 3. A three-phase scan turns tile counts into list offsets; the bin pass reserves each
@@ -44,7 +44,14 @@ constexpr int kChunk = 256;          // triangles per tile work item
 constexpr int kWorkClasses = 128;    // tile work classes: none, then 32 entries each (heavy-first order)
 constexpr int kWindow = 512;         // work items per map of the tile kernel (256 threads x 2)
 static_assert(kWindow == 2 * 256, "the map scan gives each thread two entries");
-constexpr int kSmallPixels = 16;     // bounding boxes up to this many pixels skip binning
+// Bounding boxes up to this many pixel centres skip binning: a device atomic per covered pixel
+// against a record, tile entries and the tile pass's per-tile work. Many views of one dense
+// mesh keep few (1.31 M triangles, 8 x 1024^2: 8 is best, 16 costs 26 us, 64 far more in
+// atomics); range mode, where every image draws its own small item and most tiles hold few
+// triangles, keeps many (256 items of 5120 triangles at 512^2, 4 layers: visibility 3.08 ms
+// with 16, 2.38 with 64).
+constexpr int kSmallPixelsDense = 8;
+constexpr int kSmallPixelsRanges = 64;
 constexpr int kScanBlock = 1024;     // elements per scan block (256 threads x 4)
 constexpr int kOrderBuckets = 4096;  // Morton buckets (12 bits of a 30-bit code)
 constexpr int kOrderMinTris = 8192;  // smaller meshes keep their own order
@@ -97,6 +104,10 @@ struct Workspace {
 };
 
 size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
+
+int small_pixels(const DrRasterGeometry& g) {
+  return g.ranges != nullptr ? kSmallPixelsRanges : kSmallPixelsDense;
+}
 
 bool use_order(const DrRasterGeometry& g) {
   return g.ranges == nullptr && g.num_tri >= kOrderMinTris;
@@ -663,9 +674,9 @@ __device__ __forceinline__ int depth_slab(uint2 span, const Tri& T) {
 
 // ---- kernels: setup, scan, bin, tiles -----------------------------------------------------
 
-// Splits work item p of a box bw pixels wide (bw <= 16, p < 256) into (dx, dy). The float
-// quotient (p + 1/2) / bw lies at least 1/32 away from an integer, far more than the error of
-// the approximate reciprocal, so the truncation is exact.
+// Splits work item p of a box bw pixels wide (bw <= 64, p < 64) into (dx, dy). The float
+// quotient (p + 1/2) / bw lies at least 1/128 away from an integer, far more than the error of
+// the approximate reciprocal (2^-22 relative, below 2^-15 here), so the truncation is exact.
 __device__ __forceinline__ void box_cell(int p, int bw, int& dx, int& dy) {
   dy = (int)(((float)p + 0.5f) * __builtin_amdgcn_rcpf((float)bw));
   dx = p - dy * bw;
@@ -680,7 +691,7 @@ __device__ __forceinline__ uint32_t pack_box(int x0, int w, int y0, int h) {
 // Small triangles of a workgroup staged for the wave that rasterizes them.
 struct SmallStage {
   float4 tri[256][4];  // the three vertices, then (reach_x, reach_y, row bits, image bits)
-  uint2 box[256];      // (x0 | (w - 1) << 20, y0 | (h - 1) << 20), w * h <= kSmallPixels
+  uint2 box[256];      // (x0 | (w - 1) << 20, y0 | (h - 1) << 20), w * h <= small_pixels()
   int start[256];      // first work item of each lane's triangle within its wave
 };
 
@@ -689,7 +700,7 @@ struct SmallStage {
 // the others are binned, their per-tile counts gathered in the workgroup's tile table.
 __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
                                                            const uint64_t* prev, uint64_t* keys,
-                                                           Workspace ws) {
+                                                           Workspace ws, int small_limit) {
   __shared__ union {
     SmallStage small;
     TileTable table;
@@ -721,7 +732,7 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
     candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
     if (x_lo <= x_hi && y_lo <= y_hi) {
       const int64_t count = (int64_t)(x_hi - x_lo + 1) * (y_hi - y_lo + 1);
-      if (count <= kSmallPixels) {
+      if (count <= small_limit) {
         area = (int)count;
         SmallStage& st = lds.small;
 #pragma unroll
@@ -1674,7 +1685,7 @@ static int queue_visibility_start(const DrRasterGeometry* g, const uint64_t* pre
     raster_depth_range<<<ws.depth_ranges * kRangeParts, 256, 0, s>>>(*g, ws);
     raster_depth_range_merge<<<ws.depth_ranges, kRangeParts, 0, s>>>(ws);
     raster_setup_kernel<<<blocks_for(g->num_instances, 256), 256, 0, s>>>(*g, prev_keys, keys,
-                                                                          ws);
+                                                                          ws, small_pixels(*g));
     raster_scan_reduce<<<ws.scan_blocks, 256, 0, s>>>(ws.list_counts, ws.lists, ws.block_sums);
     raster_scan_blocks<<<1, 256, 0, s>>>(ws.block_sums, ws.scan_blocks, ws.counters);
     raster_scan_apply<<<ws.scan_blocks, 256, 0, s>>>(ws.list_counts, ws.lists, ws.block_sums,
