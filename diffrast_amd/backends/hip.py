@@ -300,6 +300,8 @@ class _Resolve(torch.autograd.Function):
         ctx.save_for_backward(_saveable(pos), keys)
         if not grad_db:
             ctx.mark_non_differentiable(rast_db)
+        # Outputs that no gradient reaches arrive as None, not as zeros to walk through.
+        ctx.set_materialize_grads(False)
         return rast, rast_db
 
     @staticmethod
@@ -310,9 +312,15 @@ class _Resolve(torch.autograd.Function):
             return None, None, None, None
         geo = ctx.geo
         grad_pos = torch.zeros_like(pos, memory_format=torch.contiguous_format)
+        use_db = ctx.grad_db and grad_rast_db is not None
+        if grad_rast is None and not use_db:
+            # Neither output carries a gradient (rast only fed antialias, say, which has none
+            # for it): the positions' gradient through here is zero, as the reference's
+            # resolve backward computes from zero gradients.
+            return grad_pos, None, None, None
         if grad_rast is None:
             grad_rast = pos.new_zeros(*geo.shape, 4)
-        grad_db = _dense(grad_rast_db) if ctx.grad_db else None
+        grad_db = _dense(grad_rast_db) if use_db else None
         # The geometry points at the forward's tensors, which are still alive (saved).
         struct = _lib.RasterGeometry.from_buffer_copy(geo.struct)
         struct.pos = ptr(pos)
@@ -459,6 +467,7 @@ class _Interpolate(torch.autograd.Function):
                               diff_dev)
         if not diff:
             ctx.mark_non_differentiable(out_da)
+        ctx.set_materialize_grads(False)  # unreached outputs arrive as None
         return out, out_da
 
     @staticmethod
@@ -469,6 +478,10 @@ class _Interpolate(torch.autograd.Function):
         if not (need_attr or need_rast or need_db):
             return None, None, None, None, None
         diff = ctx.diff
+        if grad_out is None and (grad_out_da is None or not diff):
+            # No gradient reaches either output: zero for the attributes, and none to pass on
+            # to rast (whose own backward then has nothing to add).
+            return torch.zeros_like(attr) if need_attr else None, None, None, None, None
         if grad_out is None:
             grad_out = attr.new_zeros(*rast.shape[:3], attr.shape[-1])
         grad_out = grad_out.contiguous()

@@ -440,6 +440,44 @@ def test_public_api_and_double_backward_guard():
         torch.autograd.grad(rast[..., :3].square().sum(), pos, create_graph=True)
 
 
+def test_outputs_no_gradient_reaches_add_zero_gradient():
+    # rast that only feeds antialias (which has no gradient for it) and an interpolate whose
+    # derivative output is unused: the positions' and attributes' gradients are those of the
+    # paths that do carry one, and a leaf reached only through such outputs gets zeros.
+    ctx = dr.RasterizeContext("cuda")
+    gen = torch.Generator().manual_seed(17)
+    pos0, tri = random_mesh(60, gen, batch=2)
+    pos0, tri = pos0.cuda(), tri.cuda()
+    color = torch.rand(2, 40, 48, 3, generator=gen).cuda()
+    pos = pos0.clone().requires_grad_(True)
+    rast, _ = dr.rasterize(ctx, pos, tri, (40, 48))
+    dr.antialias(color, rast, pos, tri).square().sum().backward()
+    expected = pos0.clone().requires_grad_(True)
+    dr.antialias(color, rast.detach(), expected, tri).square().sum().backward()
+    torch.testing.assert_close(pos.grad, expected.grad, rtol=1e-6,
+                               atol=1e-6 * expected.grad.abs().max().item())
+    # Only the derivative-free output used, against the same loss with the derivatives given a
+    # zero weight.
+    attr0 = torch.randn(pos0.shape[1], 3, generator=gen).cuda()
+    grads = []
+    for weigh_da in (False, True):
+        p, attr = pos0.clone().requires_grad_(True), attr0.clone().requires_grad_(True)
+        r, db = dr.rasterize(ctx, p, tri, (40, 48))
+        out, out_da = dr.interpolate(attr, r, tri, db, diff_attrs="all")
+        loss = out.square().sum() + (0.0 * out_da.sum() if weigh_da else 0.0)
+        loss.backward()
+        grads.append((p.grad, attr.grad))
+    for a, b in zip(*grads):
+        torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-6 * b.abs().max().item())
+    # A leaf reached only through an output without gradient still gets a (zero) gradient, as
+    # from the reference's resolve backward run on zeros.
+    p = pos0.clone().requires_grad_(True)
+    c = color.clone().requires_grad_(True)
+    r, _ = dr.rasterize(ctx, p, tri, (40, 48))
+    dr.antialias(c, r, pos0, tri).square().sum().backward()
+    assert c.grad is not None and p.grad is not None and not p.grad.any()
+
+
 def test_depth_peeler_range_mode_through_public_api():
     ctx = dr.RasterizeContext("cuda")
     gen = torch.Generator().manual_seed(13)
