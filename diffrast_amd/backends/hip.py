@@ -826,6 +826,12 @@ def antialias(color: Tensor, rast: Tensor, pos: Tensor, tri: Tensor, pos_gradien
     if neighbours is None:
         neighbours = edge_neighbours(tri)
     neighbours = neighbours.to(torch.int32).contiguous()
+    # Antialiasing reads the silhouette bits of the triangles rast shows only. Finding those
+    # takes a pass over rast (16 bytes per pixel); classifying a triangle, some 100 bytes of
+    # gathers: when the (pos batch, triangle) pairs are fewer than a sixth of the pixels, all
+    # are classified and rast is not read (range mode, small meshes at large images).
+    pairs = (pos.shape[0] if pos.ndim == 3 else 1) * tri.shape[0]
+    shown = rast.detach() if 6 * pairs > rast.shape[0] * rast.shape[1] * rast.shape[2] else None
     with torch.no_grad():
-        mask = silhouette_mask(pos.detach(), tri, neighbours, rast.detach())
+        mask = silhouette_mask(pos.detach(), tri, neighbours, shown)
     return _Antialias.apply(color, rast, pos, tri, mask, float(pos_gradient_boost))
