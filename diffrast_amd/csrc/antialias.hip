@@ -386,16 +386,32 @@ __device__ __forceinline__ int zw_tri(const DrAntialiasArgs& a, float2 zw, float
   return (id >= 1.0f && id <= (float)a.num_tri) ? (int)id - 1 : -1;
 }
 
+// The 16 x 16 tile of a pixel, numbered as tile_pixel() numbers workgroups before xcd_order.
+__device__ __forceinline__ int64_t tile_of(const DrAntialiasArgs& a, const TilePixel& tp) {
+  const int tiles_x = (a.width + 15) / 16, tiles_y = (a.height + 15) / 16;
+  return ((int64_t)tp.b * tiles_y + tp.y / 16) * tiles_x + tp.x / 16;
+}
+
+// Whether any pair record that the pixels of tp's tile read is active: its own records and
+// the last column and row of the tiles to its left and above (a tile's flag covers all its
+// records), as aa_pairs_kernel flagged them. Uniform over the workgroup.
+__device__ __forceinline__ bool tile_reads_active(const DrAntialiasArgs& a, const TilePixel& tp,
+                                                  const uint8_t* tile_active) {
+  const int tiles_x = (a.width + 15) / 16;
+  const int tx = tp.x / 16, ty = tp.y / 16;
+  const int64_t t = tile_of(a, tp);
+  return tile_active[t] || (tx > 0 && tile_active[t - 1]) || (ty > 0 && tile_active[t - tiles_x]);
+}
+
 // Every pixel evaluates the pairs it forms with its right and lower neighbours, once. The
 // loads go level by level over the (at most three) triangles involved -- ids, silhouette bits,
 // index rows, vertices -- so that each level's loads are in flight together: a wave where any
 // pixel needs a triangle reads all three for every lane, lanes that need fewer reading
 // triangle 0 in their place (one cached line). A pair of pixels showing one triangle, or two
 // triangles without silhouette edges, is inactive.
-__global__ __launch_bounds__(256) void aa_pairs_kernel(DrAntialiasArgs a, float2* pair_t,
-                                                       uchar2* pair_bits) {
-  const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
-  if (!tp.inside) return;
+// Sets `active` when either pair is.
+__device__ __forceinline__ void pixel_pairs_of(const DrAntialiasArgs& a, const TilePixel& tp,
+                                               float2* pair_t, uchar2* pair_bits, int& active) {
   const bool has_right = tp.x + 1 < a.width, has_down = tp.y + 1 < a.height;
   const float* zw = a.rast + 4 * tp.pixel + 2;
   const float2 zw_p = *reinterpret_cast<const float2*>(zw);
@@ -445,6 +461,22 @@ __global__ __launch_bounds__(256) void aa_pairs_kernel(DrAntialiasArgs a, float2
   }
   pair_t[tp.pixel] = make_float2(t_right, t_down);
   pair_bits[tp.pixel] = make_uchar2(right, down);
+  if ((right | down) & kActive) active = 1;  // any order: every writer stores 1
+}
+
+// One workgroup per tile: every pixel's pair records, and the tile's flag (any active record),
+// which lets the blend and the backward pass of a tile with no active record near it copy
+// instead of reading records.
+__global__ __launch_bounds__(256) void aa_pairs_kernel(DrAntialiasArgs a, float2* pair_t,
+                                                       uchar2* pair_bits,
+                                                       uint8_t* tile_active) {
+  __shared__ int s_active;
+  if (threadIdx.x == 0) s_active = 0;
+  __syncthreads();
+  const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
+  if (tp.inside) pixel_pairs_of(a, tp, pair_t, pair_bits, s_active);
+  __syncthreads();
+  if (threadIdx.x == 0) tile_active[tile_of(a, tp)] = (uint8_t)(s_active != 0);
 }
 
 // The four pairs of a pixel as (active, t, other pixel, this pixel is the first).
@@ -516,10 +548,21 @@ __device__ __forceinline__ void store_group(float* p, int n, const float (&v)[N]
 // 4 with a loop over groups for more.
 template <int NC>
 __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const float2* pair_t,
-                                                       const uchar2* pair_bits, float* out) {
+                                                       const uchar2* pair_bits,
+                                                       const uint8_t* tile_active, float* out) {
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   if (!tp.inside) return;
   const int C = a.channels;
+  if (!tile_reads_active(a, tp, tile_active)) {  // uniform: no pair moves colour here
+    const float* color = a.color + tp.pixel * C;
+    for (int c0 = 0; c0 < C; c0 += NC) {
+      const int n = min(NC, C - c0);
+      float v[NC];
+      load_group<NC>(color + c0, n, v);
+      store_group<NC>(out + tp.pixel * C + c0, n, v);
+    }
+    return;
+  }
   const PixelPairs P = pixel_pairs(a, tp, pair_t, pair_bits);
   float weight[4];
   bool any = false;
@@ -566,13 +609,25 @@ __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const 
 template <int NC>
 __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const float2* pair_t,
                                                      const uchar2* pair_bits,
+                                                     const uint8_t* tile_active,
                                                      const float* grad_out, float* grad_color,
                                                      float* grad_pos) {
   using Table = RowTable<512, 4>;
   __shared__ Table table;
-  table.init();
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   const int C = a.channels;
+  if (!tile_reads_active(a, tp, tile_active)) {  // uniform: the gradient passes through
+    if (tp.inside && grad_color) {
+      for (int c0 = 0; c0 < C; c0 += NC) {
+        const int n = min(NC, C - c0);
+        float v[NC];
+        load_group<NC>(grad_out + tp.pixel * C + c0, n, v);
+        store_group<NC>(grad_color + tp.pixel * C + c0, n, v);
+      }
+    }
+    return;
+  }
+  table.init();
   uint32_t rows[4] = {Table::kEmpty, Table::kEmpty, Table::kEmpty, Table::kEmpty};
   float vals[4][4];
 #pragma unroll
@@ -744,14 +799,18 @@ extern "C" int dr_silhouette_mask(const float* pos, int64_t pos_batch_stride, in
 extern "C" int dr_antialias_workspace_size(const DrAntialiasArgs* a, size_t* bytes) {
   if (!valid_args(a) || !bytes) return DR_ERR_ARGUMENT;
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
-  *bytes = (size_t)pixels * (sizeof(float2) + sizeof(uchar2));
+  *bytes = (size_t)pixels * (sizeof(float2) + sizeof(uchar2)) +
+           (size_t)tile_blocks(a->batch, a->height, a->width);
   return DR_OK;
 }
 
-static void pair_buffers(const DrAntialiasArgs* a, void* pairs, float2*& t, uchar2*& bits) {
+// The pair records: crossings, then bits, then one activity flag per 16 x 16 tile.
+static void pair_buffers(const DrAntialiasArgs* a, void* pairs, float2*& t, uchar2*& bits,
+                         uint8_t*& tiles) {
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   t = (float2*)pairs;
   bits = (uchar2*)((char*)pairs + pixels * sizeof(float2));
+  tiles = (uint8_t*)((char*)pairs + pixels * (sizeof(float2) + sizeof(uchar2)));
 }
 
 extern "C" int dr_antialias_forward(const DrAntialiasArgs* a, void* pairs, size_t pairs_bytes,
@@ -764,13 +823,14 @@ extern "C" int dr_antialias_forward(const DrAntialiasArgs* a, void* pairs, size_
   if (!pairs || pairs_bytes < need) return DR_ERR_CAPACITY;
   float2* t;
   uchar2* bits;
-  pair_buffers(a, pairs, t, bits);
+  uint8_t* tiles;
+  pair_buffers(a, pairs, t, bits, tiles);
   const int64_t blocks = tile_blocks(a->batch, a->height, a->width);
-  aa_pairs_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits);
+  aa_pairs_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, tiles);
   if (a->channels <= 0) return launch_status();
   return channel_groups(a->channels, [&](auto nc) {
     constexpr int NC = decltype(nc)::value;
-    aa_blend_kernel<NC><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, out);
+    aa_blend_kernel<NC><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, tiles, out);
     return launch_status();
   });
 }
@@ -788,11 +848,12 @@ extern "C" int dr_antialias_backward(const DrAntialiasArgs* a, const void* pairs
     return DR_ERR_ARGUMENT;
   float2* t;
   uchar2* bits;
-  pair_buffers(a, (void*)pairs, t, bits);
+  uint8_t* tiles;
+  pair_buffers(a, (void*)pairs, t, bits, tiles);
   const int64_t blocks = tile_blocks(a->batch, a->height, a->width);
   return channel_groups(a->channels, [&](auto nc) {
     constexpr int NC = decltype(nc)::value;
-    aa_bwd_kernel<NC><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, grad_out,
+    aa_bwd_kernel<NC><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, tiles, grad_out,
                                                                 grad_color, grad_pos);
     return launch_status();
   });

@@ -315,7 +315,7 @@ typedef struct DrAntialiasArgs {
 } DrAntialiasArgs;
 
 /* Bytes of the pair records that dr_antialias_forward writes and dr_antialias_backward
- * reads (10 per pixel). */
+ * reads (10 per pixel and one per 16x16 tile). */
 int dr_antialias_workspace_size(const DrAntialiasArgs* a, size_t* bytes);
 
 /* out [batch, h, w, channels] = color blended across silhouette edges; also fills the pair

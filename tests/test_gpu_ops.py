@@ -12,7 +12,7 @@ import torch
 
 import diffrast_amd as dr
 from diffrast_amd.backends import hip
-from helpers import random_mesh, rel_error
+from helpers import random_mesh, rel_error, tiny_mesh
 from oracle import reference as R
 
 pytestmark = pytest.mark.gpu
@@ -336,6 +336,25 @@ def test_antialias_matches_oracle(channels, mesh):
     assert rel_error(ours[1][0], ref[1][0]) < VALUE_TOL
     # Position gradients: vertices near the camera plane have huge gradients whose float32
     # rounding differs between implementations; 1e-4 of the largest one.
+    assert_grads_close([ours[1][1]], [ref[1][1]])
+
+
+@pytest.mark.parametrize("channels", [3, 4])
+def test_antialias_small_objects_in_large_images(channels):
+    # A few small triangles in 100 x 120 images: most 16 x 16 tiles hold no active pair and copy
+    # colour and gradient without reading pair records; the active ones sit next to them, with
+    # pairs across tile borders (a tile's left and upper neighbours' records).
+    gen = torch.Generator().manual_seed(41)
+    pos, tri = tiny_mesh(12, gen, 0.18, batch=3)
+    rast, _ = R.rasterize(pos, tri, (100, 120), True)
+    color = torch.rand(3, 100, 120, channels, generator=gen)
+    weights = torch.randn(3, 100, 120, channels, generator=gen)
+    ref = grads_of(lambda c, p: R.antialias(c, rast, p, tri, 1.0), [color, pos], [weights], "cpu")
+    ours = grads_of(lambda c, p: hip.antialias(c, rast.cuda(), p, tri.cuda(), 1.0),
+                    [color, pos], [weights], "cuda")
+    assert (ref[0][0] != color).any() and (rast[..., 3] == 0).float().mean() > 0.5
+    assert rel_error(ours[0][0], ref[0][0]) < VALUE_TOL
+    assert rel_error(ours[1][0], ref[1][0]) < VALUE_TOL
     assert_grads_close([ours[1][1]], [ref[1][1]])
 
 
