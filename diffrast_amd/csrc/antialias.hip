@@ -392,15 +392,23 @@ __device__ __forceinline__ int64_t tile_of(const DrAntialiasArgs& a, const TileP
   return ((int64_t)tp.b * tiles_y + tp.y / 16) * tiles_x + tp.x / 16;
 }
 
-// Whether any pair record that the pixels of tp's tile read is active: its own records and
-// the last column and row of the tiles to its left and above (a tile's flag covers all its
-// records), as aa_pairs_kernel flagged them. Uniform over the workgroup.
-__device__ __forceinline__ bool tile_reads_active(const DrAntialiasArgs& a, const TilePixel& tp,
-                                                  const uint8_t* tile_active) {
+// The activity flags (aa_pairs_kernel) of tp's tile and of the tiles to its left and above,
+// whose last column and row hold records that its pixels read. A tile without an active pair
+// has no records written: its pixels' pairs are all inactive. Uniform over the workgroup.
+struct TileFlags {
+  bool own, left, up;
+  __device__ __forceinline__ bool any() const { return own || left || up; }
+};
+
+__device__ __forceinline__ TileFlags tile_flags(const DrAntialiasArgs& a, const TilePixel& tp,
+                                                const uint8_t* tile_active) {
   const int tiles_x = (a.width + 15) / 16;
-  const int tx = tp.x / 16, ty = tp.y / 16;
   const int64_t t = tile_of(a, tp);
-  return tile_active[t] || (tx > 0 && tile_active[t - 1]) || (ty > 0 && tile_active[t - tiles_x]);
+  TileFlags f;
+  f.own = tile_active[t] != 0;
+  f.left = tp.x >= 16 && tile_active[t - 1] != 0;
+  f.up = tp.y >= 16 && tile_active[t - tiles_x] != 0;
+  return f;
 }
 
 // Every pixel evaluates the pairs it forms with its right and lower neighbours, once. The
@@ -409,9 +417,9 @@ __device__ __forceinline__ bool tile_reads_active(const DrAntialiasArgs& a, cons
 // pixel needs a triangle reads all three for every lane, lanes that need fewer reading
 // triangle 0 in their place (one cached line). A pair of pixels showing one triangle, or two
 // triangles without silhouette edges, is inactive.
-// Sets `active` when either pair is.
+// The pixel's records: crossings (t_right, t_down) and bits (right, down).
 __device__ __forceinline__ void pixel_pairs_of(const DrAntialiasArgs& a, const TilePixel& tp,
-                                               float2* pair_t, uchar2* pair_bits, int& active) {
+                                               float2& pair_t, uchar2& pair_bits) {
   const bool has_right = tp.x + 1 < a.width, has_down = tp.y + 1 < a.height;
   const float* zw = a.rast + 4 * tp.pixel + 2;
   const float2 zw_p = *reinterpret_cast<const float2*>(zw);
@@ -459,14 +467,14 @@ __device__ __forceinline__ void pixel_pairs_of(const DrAntialiasArgs& a, const T
       down = pair_record(from_p, from_q, depth, depth_d, t_down);
     }
   }
-  pair_t[tp.pixel] = make_float2(t_right, t_down);
-  pair_bits[tp.pixel] = make_uchar2(right, down);
-  if ((right | down) & kActive) active = 1;  // any order: every writer stores 1
+  pair_t = make_float2(t_right, t_down);
+  pair_bits = make_uchar2(right, down);
 }
 
-// One workgroup per tile: every pixel's pair records, and the tile's flag (any active record),
-// which lets the blend and the backward pass of a tile with no active record near it copy
-// instead of reading records.
+// One workgroup per tile: the tile's flag (any active pair) and, only in a flagged tile, every
+// pixel's pair records. The blend and the backward pass treat the records of unflagged tiles as
+// inactive without reading them, and copy colour and gradient where no record they read is
+// active.
 __global__ __launch_bounds__(256) void aa_pairs_kernel(DrAntialiasArgs a, float2* pair_t,
                                                        uchar2* pair_bits,
                                                        uint8_t* tile_active) {
@@ -474,9 +482,17 @@ __global__ __launch_bounds__(256) void aa_pairs_kernel(DrAntialiasArgs a, float2
   if (threadIdx.x == 0) s_active = 0;
   __syncthreads();
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
-  if (tp.inside) pixel_pairs_of(a, tp, pair_t, pair_bits, s_active);
+  float2 t = make_float2(0.f, 0.f);
+  uchar2 bits = make_uchar2(0, 0);
+  if (tp.inside) pixel_pairs_of(a, tp, t, bits);
+  if ((bits.x | bits.y) & kActive) s_active = 1;  // any order: every writer stores 1
   __syncthreads();
-  if (threadIdx.x == 0) tile_active[tile_of(a, tp)] = (uint8_t)(s_active != 0);
+  const bool active = s_active != 0;
+  if (threadIdx.x == 0) tile_active[tile_of(a, tp)] = (uint8_t)active;
+  if (active && tp.inside) {
+    pair_t[tp.pixel] = t;
+    pair_bits[tp.pixel] = bits;
+  }
 }
 
 // The four pairs of a pixel as (active, t, other pixel, this pixel is the first).
@@ -489,15 +505,17 @@ struct PixelPairs {
 
 __device__ __forceinline__ PixelPairs pixel_pairs(const DrAntialiasArgs& a, const TilePixel& tp,
                                                   const float2* pair_t,
-                                                  const uchar2* pair_bits) {
+                                                  const uchar2* pair_bits, TileFlags f) {
   PixelPairs P;
   const float2 own_t = pair_t[tp.pixel];
   const uchar2 own_b = pair_bits[tp.pixel];
-  P.active[0] = own_b.x & kActive;
+  // Records of an unflagged tile were never written (whatever they read is ignored).
+  const bool left_ok = (tp.x & 15) ? f.own : f.left, up_ok = (tp.y & 15) ? f.own : f.up;
+  P.active[0] = f.own && (own_b.x & kActive);
   P.t[0] = own_t.x;
   P.other[0] = tp.pixel + 1;
   P.first[0] = true;
-  P.active[1] = own_b.y & kActive;
+  P.active[1] = f.own && (own_b.y & kActive);
   P.t[1] = own_t.y;
   P.other[1] = tp.pixel + a.width;
   P.first[1] = true;
@@ -507,11 +525,11 @@ __device__ __forceinline__ PixelPairs pixel_pairs(const DrAntialiasArgs& a, cons
   const int64_t up = tp.y > 0 ? tp.pixel - a.width : tp.pixel;
   const uchar2 left_b = pair_bits[left], up_b = pair_bits[up];
   const float2 left_t = pair_t[left], up_t = pair_t[up];
-  P.active[2] = tp.x > 0 && (left_b.x & kActive);
+  P.active[2] = tp.x > 0 && left_ok && (left_b.x & kActive);
   P.t[2] = left_t.x;
   P.other[2] = tp.pixel - 1;
   P.first[2] = false;
-  P.active[3] = tp.y > 0 && (up_b.y & kActive);
+  P.active[3] = tp.y > 0 && up_ok && (up_b.y & kActive);
   P.t[3] = up_t.y;
   P.other[3] = tp.pixel - a.width;
   P.first[3] = false;
@@ -553,7 +571,8 @@ __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const 
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   if (!tp.inside) return;
   const int C = a.channels;
-  if (!tile_reads_active(a, tp, tile_active)) {  // uniform: no pair moves colour here
+  const TileFlags flags = tile_flags(a, tp, tile_active);
+  if (!flags.any()) {  // uniform: no pair moves colour here
     const float* color = a.color + tp.pixel * C;
     for (int c0 = 0; c0 < C; c0 += NC) {
       const int n = min(NC, C - c0);
@@ -563,7 +582,7 @@ __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const 
     }
     return;
   }
-  const PixelPairs P = pixel_pairs(a, tp, pair_t, pair_bits);
+  const PixelPairs P = pixel_pairs(a, tp, pair_t, pair_bits, flags);
   float weight[4];
   bool any = false;
 #pragma unroll
@@ -616,7 +635,8 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
   __shared__ Table table;
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   const int C = a.channels;
-  if (!tile_reads_active(a, tp, tile_active)) {  // uniform: the gradient passes through
+  const TileFlags flags = tile_flags(a, tp, tile_active);
+  if (!flags.any()) {  // uniform: the gradient passes through
     if (tp.inside && grad_color) {
       for (int c0 = 0; c0 < C; c0 += NC) {
         const int n = min(NC, C - c0);
@@ -635,7 +655,7 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
 #pragma unroll
     for (int c = 0; c < 4; ++c) vals[k][c] = 0.0f;
   if (tp.inside) {
-    const PixelPairs P = pixel_pairs(a, tp, pair_t, pair_bits);
+    const PixelPairs P = pixel_pairs(a, tp, pair_t, pair_bits, flags);
     const float* g = grad_out + tp.pixel * C;
     if (grad_color) {
       for (int c0 = 0; c0 < C; c0 += NC) {
@@ -672,7 +692,7 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
       }
     }
     if (grad_pos) {
-      const uchar2 bits = pair_bits[tp.pixel];
+      const uchar2 bits = flags.own ? pair_bits[tp.pixel] : make_uchar2(0, 0);
       const int pos_b = a.pos_batch_stride != 0 ? tp.b : 0;
       const int64_t row0 = (int64_t)pos_b * (a.pos_batch_stride / 4);
 #pragma unroll
