@@ -402,6 +402,7 @@ struct TileFlags {
 
 __device__ __forceinline__ TileFlags tile_flags(const DrAntialiasArgs& a, const TilePixel& tp,
                                                 const uint8_t* tile_active) {
+  if (tile_active == nullptr) return {true, true, true};  // dense: every record written
   const int tiles_x = (a.width + 15) / 16;
   const int64_t t = tile_of(a, tp);
   TileFlags f;
@@ -474,7 +475,8 @@ __device__ __forceinline__ void pixel_pairs_of(const DrAntialiasArgs& a, const T
 // One workgroup per tile: the tile's flag (any active pair) and, only in a flagged tile, every
 // pixel's pair records. The blend and the backward pass treat the records of unflagged tiles as
 // inactive without reading them, and copy colour and gradient where no record they read is
-// active.
+// active. Without flags (tile_active NULL: dense images, where nearly every tile has an active
+// pair and the flags' loads would only add a round trip) every record is written.
 __global__ __launch_bounds__(256) void aa_pairs_kernel(DrAntialiasArgs a, float2* pair_t,
                                                        uchar2* pair_bits,
                                                        uint8_t* tile_active) {
@@ -487,8 +489,8 @@ __global__ __launch_bounds__(256) void aa_pairs_kernel(DrAntialiasArgs a, float2
   if (tp.inside) pixel_pairs_of(a, tp, t, bits);
   if ((bits.x | bits.y) & kActive) s_active = 1;  // any order: every writer stores 1
   __syncthreads();
-  const bool active = s_active != 0;
-  if (threadIdx.x == 0) tile_active[tile_of(a, tp)] = (uint8_t)active;
+  const bool active = tile_active == nullptr || s_active != 0;
+  if (threadIdx.x == 0 && tile_active != nullptr) tile_active[tile_of(a, tp)] = (uint8_t)active;
   if (active && tp.inside) {
     pair_t[tp.pixel] = t;
     pair_bits[tp.pixel] = bits;
@@ -564,15 +566,15 @@ __device__ __forceinline__ void store_group(float* p, int n, const float (&v)[N]
 // pixel and t < 0.5, and (t - 0.5) when it is the second and t >= 0.5.
 // NC channels per group: the channel count for 1 to 4 channels (whole-pixel loads and stores),
 // 4 with a loop over groups for more.
-template <int NC>
+template <int NC, bool SPARSE>
 __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const float2* pair_t,
                                                        const uchar2* pair_bits,
                                                        const uint8_t* tile_active, float* out) {
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   if (!tp.inside) return;
   const int C = a.channels;
-  const TileFlags flags = tile_flags(a, tp, tile_active);
-  if (!flags.any()) {  // uniform: no pair moves colour here
+  const TileFlags flags = SPARSE ? tile_flags(a, tp, tile_active) : TileFlags{true, true, true};
+  if (SPARSE && !flags.any()) {  // uniform: no pair moves colour here
     const float* color = a.color + tp.pixel * C;
     for (int c0 = 0; c0 < C; c0 += NC) {
       const int n = min(NC, C - c0);
@@ -625,7 +627,7 @@ __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const 
 
 // Colour gradient (a gather over the same pairs) and position gradient of each active pair,
 // written by its first pixel through the workgroup's scatter table (rows of pos: x, y, z, w).
-template <int NC>
+template <int NC, bool SPARSE>
 __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const float2* pair_t,
                                                      const uchar2* pair_bits,
                                                      const uint8_t* tile_active,
@@ -633,10 +635,11 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
                                                      float* grad_pos) {
   using Table = RowTable<512, 4>;
   __shared__ Table table;
+  if (!SPARSE) table.init();
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   const int C = a.channels;
-  const TileFlags flags = tile_flags(a, tp, tile_active);
-  if (!flags.any()) {  // uniform: the gradient passes through
+  const TileFlags flags = SPARSE ? tile_flags(a, tp, tile_active) : TileFlags{true, true, true};
+  if (SPARSE && !flags.any()) {  // uniform: the gradient passes through
     if (tp.inside && grad_color) {
       for (int c0 = 0; c0 < C; c0 += NC) {
         const int n = min(NC, C - c0);
@@ -647,7 +650,7 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
     }
     return;
   }
-  table.init();
+  if (SPARSE) table.init();
   uint32_t rows[4] = {Table::kEmpty, Table::kEmpty, Table::kEmpty, Table::kEmpty};
   float vals[4][4];
 #pragma unroll
@@ -824,6 +827,14 @@ extern "C" int dr_antialias_workspace_size(const DrAntialiasArgs* a, size_t* byt
   return DR_OK;
 }
 
+// Whether the pair records are sparse enough for tile flags: as for the silhouettes, when
+// the (pos batch, triangle) pairs are fewer than a sixth of the pixels (small meshes in large
+// images, range mode); dense views of one mesh fill nearly every tile with active pairs.
+static bool sparse_pairs(const DrAntialiasArgs* a) {
+  const int64_t pos_batch = a->pos_batch_stride != 0 ? a->batch : 1;
+  return 6 * pos_batch * (int64_t)a->num_tri <= (int64_t)a->batch * a->height * a->width;
+}
+
 // The pair records: crossings, then bits, then one activity flag per 16 x 16 tile.
 static void pair_buffers(const DrAntialiasArgs* a, void* pairs, float2*& t, uchar2*& bits,
                          uint8_t*& tiles) {
@@ -845,12 +856,17 @@ extern "C" int dr_antialias_forward(const DrAntialiasArgs* a, void* pairs, size_
   uchar2* bits;
   uint8_t* tiles;
   pair_buffers(a, pairs, t, bits, tiles);
+  const bool sparse = sparse_pairs(a);
+  if (!sparse) tiles = nullptr;
   const int64_t blocks = tile_blocks(a->batch, a->height, a->width);
   aa_pairs_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, tiles);
   if (a->channels <= 0) return launch_status();
   return channel_groups(a->channels, [&](auto nc) {
     constexpr int NC = decltype(nc)::value;
-    aa_blend_kernel<NC><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, tiles, out);
+    if (sparse)
+      aa_blend_kernel<NC, true><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, tiles, out);
+    else
+      aa_blend_kernel<NC, false><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, tiles, out);
     return launch_status();
   });
 }
@@ -870,11 +886,17 @@ extern "C" int dr_antialias_backward(const DrAntialiasArgs* a, const void* pairs
   uchar2* bits;
   uint8_t* tiles;
   pair_buffers(a, (void*)pairs, t, bits, tiles);
+  const bool sparse = sparse_pairs(a);
+  if (!sparse) tiles = nullptr;
   const int64_t blocks = tile_blocks(a->batch, a->height, a->width);
   return channel_groups(a->channels, [&](auto nc) {
     constexpr int NC = decltype(nc)::value;
-    aa_bwd_kernel<NC><<<blocks, 256, 0, (hipStream_t)stream>>>(*a, t, bits, tiles, grad_out,
-                                                                grad_color, grad_pos);
+    if (sparse)
+      aa_bwd_kernel<NC, true><<<blocks, 256, 0, (hipStream_t)stream>>>(
+          *a, t, bits, tiles, grad_out, grad_color, grad_pos);
+    else
+      aa_bwd_kernel<NC, false><<<blocks, 256, 0, (hipStream_t)stream>>>(
+          *a, t, bits, tiles, grad_out, grad_color, grad_pos);
     return launch_status();
   });
 }
