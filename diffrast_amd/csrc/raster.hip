@@ -1396,8 +1396,13 @@ __global__ __launch_bounds__(256) void raster_overflow_kernel(DrRasterGeometry g
 struct Resolved {
   float a[3], c[3], e[3], area, b[3], num, den, depth, dex[3], dey[3], sum_dx, sum_dy;
   float db_dx[3], db_dy[3];
+  float inv_area, inv_den;  // 1 / area and 1 / den (the backward pass's quotients)
 };
 
+// With kExact (the forward pass) every quotient is the reference's correctly rounded division;
+// otherwise (the backward pass, whose gradients are compared to 1e-4) the quotients by area and
+// depth denominator multiply by their reciprocals, within 2 ulp.
+template <bool kExact = true>
 __device__ __forceinline__ void resolve_pixel(const Tri& T, float px, float py, Resolved& R) {
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
@@ -1408,11 +1413,13 @@ __device__ __forceinline__ void resolve_pixel(const Tri& T, float px, float py, 
   R.e[1] = R.a[2] * R.c[0] - R.a[0] * R.c[2];
   R.e[2] = R.a[0] * R.c[1] - R.a[1] * R.c[0];
   R.area = R.e[0] + R.e[1] + R.e[2];
+  R.inv_area = 1.0f / R.area;
 #pragma unroll
-  for (int k = 0; k < 3; ++k) R.b[k] = R.e[k] / R.area;
+  for (int k = 0; k < 3; ++k) R.b[k] = kExact ? R.e[k] / R.area : R.e[k] * R.inv_area;
   R.num = R.b[0] * T.z[0] + R.b[1] * T.z[1] + R.b[2] * T.z[2];
   R.den = R.b[0] * T.w[0] + R.b[1] * T.w[1] + R.b[2] * T.w[2];
-  R.depth = R.num / R.den;
+  R.inv_den = 1.0f / R.den;
+  R.depth = kExact ? R.num / R.den : R.num * R.inv_den;
   // d e / d px = c x w and d e / d py = w x a.
   R.dex[0] = R.c[1] * T.w[2] - R.c[2] * T.w[1];
   R.dex[1] = R.c[2] * T.w[0] - R.c[0] * T.w[2];
@@ -1424,8 +1431,9 @@ __device__ __forceinline__ void resolve_pixel(const Tri& T, float px, float py, 
   R.sum_dy = R.dey[0] + R.dey[1] + R.dey[2];
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
-    R.db_dx[k] = (R.dex[k] - R.b[k] * R.sum_dx) / R.area;
-    R.db_dy[k] = (R.dey[k] - R.b[k] * R.sum_dy) / R.area;
+    const float nx = R.dex[k] - R.b[k] * R.sum_dx, ny = R.dey[k] - R.b[k] * R.sum_dy;
+    R.db_dx[k] = kExact ? nx / R.area : nx * R.inv_area;
+    R.db_dy[k] = kExact ? ny / R.area : ny * R.inv_area;
   }
 }
 
@@ -1517,13 +1525,13 @@ __global__ __launch_bounds__(256) void resolve_bwd_kernel(
     load_tri(g, b, t, T, v);
     const float px = pixel_centre(tp.x, g.width), py = pixel_centre(tp.y, g.height);
     Resolved R;
-    resolve_pixel(T, px, py, R);
+    resolve_pixel<false>(T, px, py, R);
     const float4 gr = load4(grad_rast + 4 * pixel);
     float gb[3] = {gr.x, gr.y, 0.0f};
     float gw[3] = {0.f, 0.f, 0.f}, gz[3];
     // depth = num / den
-    const float g_num = gr.z / R.den;
-    const float g_den = -gr.z * R.depth / R.den;
+    const float g_num = gr.z * R.inv_den;
+    const float g_den = -gr.z * R.depth * R.inv_den;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
       gb[k] += g_num * T.z[k] + g_den * T.w[k];
@@ -1542,23 +1550,23 @@ __global__ __launch_bounds__(256) void resolve_bwd_kernel(
       for (int k = 0; k < 3; ++k) {
         dot_x += gx[k] * R.b[k];
         dot_y += gy[k] * R.b[k];
-        gb[k] -= (gx[k] * R.sum_dx + gy[k] * R.sum_dy) / R.area;
-        g_area -= (gx[k] * R.db_dx[k] + gy[k] * R.db_dy[k]) / R.area;
+        gb[k] -= (gx[k] * R.sum_dx + gy[k] * R.sum_dy) * R.inv_area;
+        g_area -= (gx[k] * R.db_dx[k] + gy[k] * R.db_dy[k]) * R.inv_area;
       }
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
-        g_dex[k] = (gx[k] - dot_x) / R.area;
-        g_dey[k] = (gy[k] - dot_y) / R.area;
+        g_dex[k] = (gx[k] - dot_x) * R.inv_area;
+        g_dey[k] = (gy[k] - dot_y) * R.inv_area;
       }
     }
     // b_k = e_k / area
     float dot_b = 0.f;
 #pragma unroll
     for (int k = 0; k < 3; ++k) dot_b += gb[k] * R.b[k];
-    g_area -= dot_b / R.area;
+    g_area -= dot_b * R.inv_area;
     float ge[3];
 #pragma unroll
-    for (int k = 0; k < 3; ++k) ge[k] = gb[k] / R.area + g_area;
+    for (int k = 0; k < 3; ++k) ge[k] = gb[k] * R.inv_area + g_area;
     // e = a x c; dex = c x w; dey = w x a.
     float ga[3], gc[3], tmp[3];
     cross3(R.c, ge, ga);
