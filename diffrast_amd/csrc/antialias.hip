@@ -310,8 +310,9 @@ __device__ __forceinline__ void crossing_grad(const Triangle& T, int edge, float
   const float es = asi * csj - asj * csi;
   const float ed = adi * cdj - adj * cdi;
   const float span = es - ed;
-  const float dt_des = -ed / (span * span);
-  const float dt_ded = es / (span * span);
+  const float inv = 1.0f / (span * span);  // one division (the quotients within two ulp)
+  const float dt_des = -ed * inv;
+  const float dt_ded = es * inv;
   // d e / d(x_i, y_i, w_i, x_j, y_j, w_j) at a centre (px, py) with a, c there.
   auto de = [](float ai, float ci, float aj, float cj, float px, float py, float (&d)[6]) {
     d[0] = cj;
@@ -734,10 +735,8 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
         load_triangle(a, tp.b, owner, T);
         const int edge = info & 3;
         float d[6];
-        if (owner_first)
-          crossing_grad(T, edge, px, py, qcx, qcy, d);
-        else
-          crossing_grad(T, edge, qcx, qcy, px, py, d);
+        crossing_grad(T, edge, owner_first ? px : qcx, owner_first ? py : qcy,
+                      owner_first ? qcx : px, owner_first ? qcy : py, d);
         const int vi = pick3(T.v, (edge + 1) % 3), vj = pick3(T.v, (edge + 2) % 3);
         rows[2 * n] = (uint32_t)(row0 + vi);
         rows[2 * n + 1] = (uint32_t)(row0 + vj);

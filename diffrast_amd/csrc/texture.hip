@@ -147,13 +147,13 @@ __device__ __forceinline__ void level_coordinate_grads(const Bilinear<float>& L,
 #pragma unroll
     for (int c = 0; c < N; ++c) {
       if (c0 + c >= C) continue;
-      float tc[4], wgt[4], dfx, dfy;
+      float tc[4], dfx, dfy;
       tap_column(t, c, tc);
-      bilinear_grad(L, tc, wgt, dfx, dfy);
+      const float value = bilinear_grad_value(L, tc, dfx, dfy);
       const float gl = gc[c] * level_weight;
       g_fx += gl * dfx;
       g_fy += gl * dfy;
-      if (want_value) g_value += gc[c] * bilinear_value(L, tc);
+      if (want_value) g_value += gc[c] * value;
     }
   }
 }

@@ -179,6 +179,9 @@ __device__ __forceinline__ void cube_project_backward(const CubeProj<S>& P, S g_
   const int* M = kMajor[P.face];
   const int* A = kSAxis[P.face];
   const int* T = kTAxis[P.face];
+  // Gradient only: multiplies by the reciprocals (two divisions instead of 25; each product
+  // is within two ulp of the quotient).
+  const S inv_ma = S(1) / P.ma, inv_length = S(1) / P.length;
   S g_rs = S(0.5) * g_s, g_rt = S(0.5) * g_t, g_ma = S(0);
   S g_dsc[2] = {S(0), S(0)}, g_dtc[2] = {S(0), S(0)}, g_dma[2] = {S(0), S(0)};
   if (use_sda && !P.undefined) {
@@ -186,12 +189,12 @@ __device__ __forceinline__ void cube_project_backward(const CubeProj<S>& P, S g_
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const S ds = P.st_da[j], dt = P.st_da[2 + j];
-      g_rs += gds[j] * (S(-0.5) * P.d_ma[j] / P.ma);
-      g_rt += gdt[j] * (S(-0.5) * P.d_ma[j] / P.ma);
-      g_ma -= (gds[j] * ds + gdt[j] * dt) / P.ma;
-      g_dsc[j] = S(0.5) * gds[j] / P.ma;
-      g_dtc[j] = S(0.5) * gdt[j] / P.ma;
-      g_dma[j] = S(-0.5) * (gds[j] * P.rs + gdt[j] * P.rt) / P.ma;
+      g_rs += gds[j] * (S(-0.5) * P.d_ma[j] * inv_ma);
+      g_rt += gdt[j] * (S(-0.5) * P.d_ma[j] * inv_ma);
+      g_ma -= (gds[j] * ds + gdt[j] * dt) * inv_ma;
+      g_dsc[j] = S(0.5) * gds[j] * inv_ma;
+      g_dtc[j] = S(0.5) * gdt[j] * inv_ma;
+      g_dma[j] = S(-0.5) * (gds[j] * P.rs + gdt[j] * P.rt) * inv_ma;
     }
   }
 #pragma unroll
@@ -199,14 +202,14 @@ __device__ __forceinline__ void cube_project_backward(const CubeProj<S>& P, S g_
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       S g = g_dsc[j] * (S)A[k] + g_dtc[j] * (S)T[k] + g_dma[j] * (S)M[k];
-      g = (P.valid && !P.undefined && P.da_pass[k][j]) ? g / P.length : S(0);
+      g = (P.valid && !P.undefined && P.da_pass[k][j]) ? g * inv_length : S(0);
       grad_dir_da[2 * k + j] = g;
     }
-  g_ma -= (g_rs * P.rs + g_rt * P.rt) / P.ma;
+  g_ma -= (g_rs * P.rs + g_rt * P.rt) * inv_ma;
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
-    const S g_dn = (g_rs * (S)A[k] + g_rt * (S)T[k]) / P.ma + g_ma * (S)M[k];
-    grad_dir[k] = P.valid ? g_dn / P.length : S(0);
+    const S g_dn = (g_rs * (S)A[k] + g_rt * (S)T[k]) * inv_ma + g_ma * (S)M[k];
+    grad_dir[k] = P.valid ? g_dn * inv_length : S(0);
   }
 }
 
@@ -349,6 +352,31 @@ __device__ __forceinline__ void bilinear_grad(const Bilinear<S>& L, const S (&t)
 #pragma unroll
     for (int k = 0; k < 4; ++k) wgt[k] += missing / S(3);
   }
+}
+
+// bilinear_grad and bilinear_value of one channel in one pass, for the backward kernels: the
+// cube-corner mean is the tap sum times 1/3 (within an ulp of the quotient), shared by the
+// value and the derivatives.
+template <class S>
+__device__ __forceinline__ S bilinear_grad_value(const Bilinear<S>& L, const S (&t)[4],
+                                                 S& dfx, S& dfy) {
+  const S fx = L.fx, fy = L.fy;
+  const S top = (S(1) - fx) * t[0] + fx * t[1], bottom = (S(1) - fx) * t[2] + fx * t[3];
+  S value = (S(1) - fy) * top + fy * bottom;
+  dfx = (S(1) - fy) * (t[1] - t[0]) + fy * (t[3] - t[2]);
+  dfy = bottom - top;
+  if (L.cube) {
+    const S missing = (S(1) - fy) * ((S(1) - fx) * L.corner[0] + fx * L.corner[1]) +
+                      fy * ((S(1) - fx) * L.corner[2] + fx * L.corner[3]);
+    const S share = (t[0] + t[1] + t[2] + t[3]) * S(1.0 / 3.0);
+    const S dm_dfx = (S(1) - fy) * (L.corner[1] - L.corner[0]) + fy * (L.corner[3] - L.corner[2]);
+    const S dm_dfy = ((S(1) - fx) * L.corner[2] + fx * L.corner[3]) -
+                     ((S(1) - fx) * L.corner[0] + fx * L.corner[1]);
+    dfx += dm_dfx * share;
+    dfy += dm_dfy * share;
+    value = value + missing * share;
+  }
+  return value;
 }
 
 // (du/dx, du/dy, dv/dx, dv/dy) of a pixel.
