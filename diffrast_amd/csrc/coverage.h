@@ -41,7 +41,9 @@ DR_HD bool inside_edge(float e, float ai, float ci, float wi, float aj, float cj
     float gy = aj * wi - ai * wj;
     q = (gx == 0.0f) ? gy : gx;
   }
-  return positive ? (q > 0.0f) : (q < 0.0f);
+  // q > 0 for a positive orientation, q < 0 otherwise, as one comparison (negation is exact;
+  // a zero or NaN q fails either way).
+  return (positive ? q : -q) > 0.0f;
 }
 
 // Coverage of pixel centre (px, py) and depth there: the reference's operations in its order
@@ -59,15 +61,17 @@ DR_HD bool covers(const float* x, const float* y, const float* z, const float* w
   const float e2 = a0 * c1 - a1 * c0;
   const float s = e0 + e1 + e2;
   const bool positive = s > 0.0f;
-  if (!inside_edge(e0, a1, c1, w[1], a2, c2, w[2], positive)) return false;
-  if (!inside_edge(e1, a2, c2, w[2], a0, c0, w[0], positive)) return false;
-  if (!inside_edge(e2, a0, c0, w[0], a1, c1, w[1], positive)) return false;
+  // All three edges, then one branch (their tests have no side effects).
+  const bool in0 = inside_edge(e0, a1, c1, w[1], a2, c2, w[2], positive);
+  const bool in1 = inside_edge(e1, a2, c2, w[2], a0, c0, w[0], positive);
+  const bool in2 = inside_edge(e2, a0, c0, w[0], a1, c1, w[1], positive);
+  if (!(in0 & in1 & in2)) return false;
   const float span_x = fabsf(a0) + fabsf(a1) + fabsf(a2);
   const float span_y = fabsf(c0) + fabsf(c1) + fabsf(c2);
   if (!(fabsf(s) > (reach_x * span_y + span_x * (reach_y + span_y)) * kAreaTolerance))
     return false;
   const float ew = e0 * w[0] + e1 * w[1] + e2 * w[2];
-  if (positive ? !(ew > 0.0f) : !(ew < 0.0f)) return false;
+  if (!((positive ? ew : -ew) > 0.0f)) return false;
   depth = (e0 * z[0] + e1 * z[1] + e2 * z[2]) / ew;
   return depth >= -1.0f && depth <= 1.0f;
 }
