@@ -32,18 +32,13 @@ DR_HD float reach(const float* a, const float* w) {
                fabsf(a[2]) + fabsf(w[2]));
 }
 
-// Fill-rule test of one edge (reference.py:338-365).
-DR_HD bool inside_edge(float e, float ai, float ci, float wi, float aj, float cj, float wj,
-                       bool positive) {
-  float q = e;
-  if (e == 0.0f) {
-    float gx = ci * wj - cj * wi;
-    float gy = aj * wi - ai * wj;
-    q = (gx == 0.0f) ? gy : gx;
-  }
-  // q > 0 for a positive orientation, q < 0 otherwise, as one comparison (negation is exact;
-  // a zero or NaN q fails either way).
-  return (positive ? q : -q) > 0.0f;
+// Fill rule of one edge (reference.py:338-365): the value whose sign decides, e itself unless it
+// is 0, then the tie-break gx, or gy when gx is 0 too.
+DR_HD float tie_broken(float e, float ai, float ci, float wi, float aj, float cj, float wj) {
+  if (e != 0.0f) return e;
+  const float gx = ci * wj - cj * wi;
+  const float gy = aj * wi - ai * wj;
+  return (gx == 0.0f) ? gy : gx;
 }
 
 // Coverage of pixel centre (px, py) and depth there: the reference's operations in its order
@@ -61,10 +56,18 @@ DR_HD bool covers(const float* x, const float* y, const float* z, const float* w
   const float e2 = a0 * c1 - a1 * c0;
   const float s = e0 + e1 + e2;
   const bool positive = s > 0.0f;
-  // All three edges, then one branch (their tests have no side effects).
-  const bool in0 = inside_edge(e0, a1, c1, w[1], a2, c2, w[2], positive);
-  const bool in1 = inside_edge(e1, a2, c2, w[2], a0, c0, w[0], positive);
-  const bool in2 = inside_edge(e2, a0, c0, w[0], a1, c1, w[1], positive);
+  // An edge passes when its value has the orientation's sign (q > 0 for a positive one, q < 0
+  // otherwise: one comparison of q or -q, negation being exact; a zero or NaN q fails). The
+  // tie-breaks of edges through the centre are rare: one branch for all three.
+  float q0 = e0, q1 = e1, q2 = e2;
+  if (e0 == 0.0f || e1 == 0.0f || e2 == 0.0f) {
+    q0 = tie_broken(e0, a1, c1, w[1], a2, c2, w[2]);
+    q1 = tie_broken(e1, a2, c2, w[2], a0, c0, w[0]);
+    q2 = tie_broken(e2, a0, c0, w[0], a1, c1, w[1]);
+  }
+  const bool in0 = (positive ? q0 : -q0) > 0.0f;
+  const bool in1 = (positive ? q1 : -q1) > 0.0f;
+  const bool in2 = (positive ? q2 : -q2) > 0.0f;
   if (!(in0 & in1 & in2)) return false;
   const float span_x = fabsf(a0) + fabsf(a1) + fabsf(a2);
   const float span_y = fabsf(c0) + fabsf(c1) + fabsf(c2);
