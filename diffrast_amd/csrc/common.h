@@ -249,9 +249,19 @@ __device__ __forceinline__ bool row_run_sums(uint32_t key, float (&v)[N]) {
   const bool last = (pos == 15) | (right != key);
   const uint64_t heads = __ballot(head);
   const int start = 63 - __clzll(heads & ((2ull << lane) - 1ull));  // first lane of the run
+  // A step adds nothing unless some lane sits at least that far into its run: the lanes at
+  // position >= 1, 2, 4 and 8, as masks of the wave (runs never cross a row: its first lane is
+  // a head), end the scan early where the runs are short.
+  const uint64_t at1 = ~heads;
+  if (at1 == 0) return last;
   run_step<1>(v, lane - 1 >= start);
+  const uint64_t at2 = at1 & (at1 << 1);
+  if (at2 == 0) return last;
   run_step<2>(v, lane - 2 >= start);
+  const uint64_t at4 = at2 & (at2 << 2);
+  if (at4 == 0) return last;
   run_step<4>(v, lane - 4 >= start);
+  if ((at4 & (at4 << 4)) == 0) return last;
   run_step<8>(v, lane - 8 >= start);
   return last;
 }
