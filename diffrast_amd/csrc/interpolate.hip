@@ -174,7 +174,8 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
                                                          uint32_t rows_per_image) {
   using Table = RowTable<256, 8>;
   __shared__ Table table;
-  table.init();  // the first pass's barriers order it before any add
+  const bool scatter = grad_attr != nullptr && a.channels > 0;  // uniform over the workgroup
+  if (scatter) table.init();  // the first pass's barriers order it before any add
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   const int64_t pixel = tp.pixel;
   const int C = NC > 0 ? NC : a.channels;
@@ -192,7 +193,6 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
   const float w = 1.0f - p.u - p.v;
   const float* g = grad_out + (tp.inside ? pixel * C : 0);
   const float* gd = (D > 0 && tp.inside) ? grad_da + pixel * 2 * D : nullptr;
-  const bool scatter = grad_attr != nullptr && C > 0;  // uniform over the workgroup
   const uint32_t run_key = p.valid ? (uint32_t)p.t : 0xffffffffu;
   float gu = 0.f, gv = 0.f, g_dudx = 0.f, g_dudy = 0.f, g_dvdx = 0.f, g_dvdy = 0.f;
 
