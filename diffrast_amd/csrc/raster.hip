@@ -42,8 +42,8 @@ namespace {
 constexpr int kTile = 16;            // tile edge in pixels; a tile is one 256-thread workgroup
 constexpr int kChunk = 256;          // triangles per tile work item
 constexpr int kWorkClasses = 128;    // tile work classes: none, then 32 entries each (heavy-first order)
-constexpr int kWindow = 512;         // work items per map of the tile kernel (256 threads x 2)
-static_assert(kWindow == 2 * 256, "the map scan gives each thread two entries");
+constexpr int kWindow = 1024;        // work items per map of the tile kernel (256 threads x 4)
+static_assert(kWindow == 4 * 256, "the map scan gives each thread four entries");
 // Bounding boxes up to this many pixel centres skip binning: a device atomic per covered pixel
 // against a record, tile entries and the tile pass's per-tile work. Many views of one dense
 // mesh keep few (1.31 M triangles, 8 x 1024^2: 8 is best, 16 costs 26 us, 64 far more in
@@ -1121,7 +1121,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   __shared__ uint8_t s_spans[kChunk];
   // Work item -> (first item of its triangle in the window) << 20 | triangle << 12 |
   // (the triangle's first item - the window's + 2048).
-  __shared__ uint2 s_map[kWindow / 2];
+  __shared__ uint4 s_map[kWindow / 4];
   __shared__ int s_wave_sum[256 / DR_WAVE];
   __shared__ uint32_t s_wave_max[256 / DR_WAVE];
   __shared__ unsigned long long s_key[kTile * kTile];
@@ -1270,10 +1270,10 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     const int tri_first = before + incl - items;
 
     for (int base = 0; base < total; base += kWindow) {
-      s_map[threadIdx.x] = make_uint2(0u, 0u);
+      s_map[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
       __syncthreads();
       // Mark the first item in the window of each triangle that reaches into it. Its first
-      // item overall is within 256 items of the window (-256 < tri_first - base < 512).
+      // item overall is within 256 items of the window (-256 < tri_first - base < kWindow).
       if (items > 0 && tri_first < base + kWindow && tri_first + items > base) {
         const int pos = max(tri_first, base) - base;
         reinterpret_cast<uint32_t*>(s_map)[pos] =
@@ -1281,9 +1281,11 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
       }
       __syncthreads();
       // Inclusive max-scan of the window (each mark exceeds every mark before it).
-      uint2 m = s_map[threadIdx.x];
+      uint4 m = s_map[threadIdx.x];
       m.y = max(m.y, m.x);
-      const uint32_t run = wave_inclusive_max(m.y);
+      m.z = max(m.z, m.y);
+      m.w = max(m.w, m.z);
+      const uint32_t run = wave_inclusive_max(m.w);
       if (lane == DR_WAVE - 1) s_wave_max[wave] = run;
       uint32_t carry = wave_shr1(run);
       __syncthreads();
@@ -1292,6 +1294,8 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
         carry = w < wave ? max(carry, s_wave_max[w]) : carry;
       m.x = max(m.x, carry);
       m.y = max(m.y, carry);
+      m.z = max(m.z, carry);
+      m.w = max(m.w, carry);
       s_map[threadIdx.x] = m;
       __syncthreads();
 
