@@ -58,6 +58,7 @@ constexpr int kOrderMinTris = 8192;  // smaller meshes keep their own order
 constexpr int kTileSlots = 1024;     // LDS table of a workgroup's tiles
 constexpr int kRecord = 4;           // float4 per binned triangle record (one 64-byte line)
 constexpr int kDepthSlabs = 16;      // tile lists per tile, by the triangle's nearest depth
+                                     // (dense views; range mode keeps one list per tile)
 constexpr int kRangeParts = 64;      // workgroups per image in the depth span reduction
 constexpr int kXcdShares = 8;        // XCDs of an MI355X: workgroup b runs on XCD b mod 8
 
@@ -65,7 +66,7 @@ struct Workspace {
   float4* records;           // binned triangles, kRecord float4 each: the three clip-space
                              // vertices, then the bits of (image, row, tx0 | tx1 << 16,
                              // ty0 | ty1 << 16)
-  // Tile lists: list tile * kDepthSlabs + slab holds the binned triangles of that tile whose
+  // Tile lists: list tile * slabs + slab holds the binned triangles of that tile whose
   // nearest depth falls in depth slab `slab` of their image, so a tile's entries are one range
   // that runs near to far.
   uint32_t* list_counts;     // [lists + 1]
@@ -100,6 +101,7 @@ struct Workspace {
   int depth_ranges;
   int scan_blocks;
   int record_blocks;          // setup workgroups; each owns 256 record slots
+  int slabs;                  // tile lists per tile: kDepthSlabs, or 1 in range mode
   size_t bytes;
 };
 
@@ -118,7 +120,11 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
   w.tiles_x = (g.width + kTile - 1) / kTile;
   w.tiles_y = (g.height + kTile - 1) / kTile;
   w.tiles = (int64_t)g.batch * w.tiles_x * w.tiles_y;
-  w.lists = w.tiles * kDepthSlabs;
+  // Range mode keeps one list per tile: its items' triangles mostly take the small-triangle path,
+  // so the near-to-far slabs gain its tile pass nothing, while their lists (clears, scans) and
+  // the depth span they need cost 0.2 ms per step of four layers of 256 items at 512 x 512.
+  w.slabs = g.ranges != nullptr ? 1 : kDepthSlabs;
+  w.lists = w.tiles * w.slabs;
   w.scan_blocks = (int)((w.lists + 1 + kScanBlock - 1) / kScanBlock);
   w.depth_ranges = (g.ranges == nullptr && g.pos_batch_stride != 0) ? std::max(g.batch, 1) : 1;
   w.ordered = use_order(g);
@@ -660,16 +666,16 @@ __global__ __launch_bounds__(kRangeParts) void raster_depth_range_merge(Workspac
 // Depth slab of a binned triangle: its nearest vertex depth's place in the image's depth span
 // (order-preserving bits of its nearest and farthest depth, from ws.depth_range). Triangles that
 // cross the camera plane go first (slab 0).
-__device__ __forceinline__ int depth_slab(uint2 span, const Tri& T) {
-  if (!(T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f)) return 0;
+__device__ __forceinline__ int depth_slab(uint2 span, const Tri& T, int slabs) {
+  if (slabs == 1 || !(T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f)) return 0;
   float d[3];
   vertex_depths(T, d);
   const float nearest = fminf(fminf(d[0], d[1]), d[2]);
   const float lo = from_ordered_bits(span.x);
   const float hi = from_ordered_bits(span.y);
-  const float f = (nearest - lo) / (hi - lo) * (float)kDepthSlabs;
+  const float f = (nearest - lo) / (hi - lo) * (float)slabs;
   if (!(hi > lo) || !isfinite(f)) return 0;
-  return min(max((int)f, 0), kDepthSlabs - 1);
+  return min(max((int)f, 0), slabs - 1);
 }
 
 // ---- kernels: setup, scan, bin, tiles -----------------------------------------------------
@@ -728,7 +734,7 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
       load_tri(g, b, t, T, v);
     }
     // Loaded now and used after the small triangles' work, which hides the load's latency.
-    span = reinterpret_cast<const uint2*>(ws.depth_range)[ws.depth_ranges > 1 ? b : 0];
+    if (ws.slabs > 1) span = reinterpret_cast<const uint2*>(ws.depth_range)[ws.depth_ranges > 1 ? b : 0];
     candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
     if (x_lo <= x_hi && y_lo <= y_hi) {
       const int64_t count = (int64_t)(x_hi - x_lo + 1) * (y_hi - y_lo + 1);
@@ -801,7 +807,7 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
       const uint32_t rec = (uint32_t)(block * 256 + before) +
                            (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
       const int tx0 = x_lo / kTile, tx1 = x_hi / kTile, ty0 = y_lo / kTile, ty1 = y_hi / kTile;
-      const int slab = depth_slab(span, T);
+      const int slab = depth_slab(span, T, ws.slabs);
       float4* out = ws.records + (size_t)rec * kRecord;
 #pragma unroll
       for (int k = 0; k < 3; ++k) out[k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
@@ -812,7 +818,7 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
       for (int ty = ty0; ty <= ty1; ++ty)
         for (int tx = tx0; tx <= tx1; ++tx) {
           const uint32_t list =
-              (image_tiles + ty * ws.tiles_x + tx) * kDepthSlabs + (uint32_t)slab;
+              (image_tiles + ty * ws.tiles_x + tx) * ws.slabs + (uint32_t)slab;
           const int slot = table.insert(list);
           if (slot >= 0)
             atomicAdd(table.count + slot, 1u);
@@ -946,7 +952,7 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint32_t*
   }
   for (int ty = ty0; ty <= ty1; ++ty)
     for (int tx = tx0; tx <= tx1; ++tx) {
-      const int slot = table.insert((image_tiles + ty * ws.tiles_x + tx) * kDepthSlabs + slab);
+      const int slot = table.insert((image_tiles + ty * ws.tiles_x + tx) * ws.slabs + slab);
       if (slot >= 0) atomicAdd(table.count + slot, 1u);
     }
   __syncthreads();
@@ -969,7 +975,7 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint32_t*
   __syncthreads();
   for (int ty = ty0; ty <= ty1; ++ty)
     for (int tx = tx0; tx <= tx1; ++tx) {
-      const uint32_t list = (image_tiles + ty * ws.tiles_x + tx) * kDepthSlabs + slab;
+      const uint32_t list = (image_tiles + ty * ws.tiles_x + tx) * ws.slabs + slab;
       const int slot = table.find(list);
       const uint32_t at = slot >= 0 ? table.base[slot] + atomicAdd(table.count + slot, 1u)
                                     : atomicAdd(ws.list_cursor + list, 1u);
@@ -1012,7 +1018,7 @@ __global__ __launch_bounds__(256) void raster_tile_classes(Workspace ws) {
   bool has = false;
   if (tile < ws.tiles) {
     const uint32_t n =
-        ws.list_offsets[(tile + 1) * kDepthSlabs] - ws.list_offsets[tile * kDepthSlabs];
+        ws.list_offsets[(tile + 1) * ws.slabs] - ws.list_offsets[tile * ws.slabs];
     // Class 0: no entries; then one class per 32 entries, the last one open-ended.
     const int c = n == 0 ? 0 : (int)min((n >> 5) + 1, (uint32_t)(kWorkClasses - 1));
     ws.tile_class[tile] = (uint8_t)c;
@@ -1144,8 +1150,8 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   const uint32_t stride = gridDim.x / kXcdShares;
   for (uint32_t slot = blockIdx.x / kXcdShares; slot < busy; slot += stride) {
   const uint32_t tile = ws.tile_order[ws.share_info[kXcdShares + share] + slot];
-  const uint32_t begin = ws.list_offsets[(size_t)tile * kDepthSlabs];
-  const uint32_t end = ws.list_offsets[(size_t)(tile + 1) * kDepthSlabs];
+  const uint32_t begin = ws.list_offsets[(size_t)tile * ws.slabs];
+  const uint32_t end = ws.list_offsets[(size_t)(tile + 1) * ws.slabs];
   if (begin == end) {  // uniform over the workgroup
     if (!kLoop) break;
     continue;
@@ -1694,8 +1700,10 @@ static int queue_visibility_start(const DrRasterGeometry* g, const uint64_t* pre
       keys, pixels, ws, g->width, g->height);
   if (g->num_instances > 0) {
     if (ws.ordered && g->order == nullptr) queue_order(*g, ws, s);
-    raster_depth_range<<<ws.depth_ranges * kRangeParts, 256, 0, s>>>(*g, ws);
-    raster_depth_range_merge<<<ws.depth_ranges, kRangeParts, 0, s>>>(ws);
+    if (ws.slabs > 1) {  // the depth span places binned triangles in slabs
+      raster_depth_range<<<ws.depth_ranges * kRangeParts, 256, 0, s>>>(*g, ws);
+      raster_depth_range_merge<<<ws.depth_ranges, kRangeParts, 0, s>>>(ws);
+    }
     raster_setup_kernel<<<blocks_for(g->num_instances, 256), 256, 0, s>>>(*g, prev_keys, keys,
                                                                           ws, small_pixels(*g));
     raster_scan_reduce<<<ws.scan_blocks, 256, 0, s>>>(ws.list_counts, ws.lists, ws.block_sums);
