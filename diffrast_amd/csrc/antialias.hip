@@ -413,6 +413,35 @@ __device__ __forceinline__ TileFlags tile_flags(const DrAntialiasArgs& a, const 
   return f;
 }
 
+// Copies the workgroup's 16 x 16 tile of [.., C] values from src to dst, row by row, 16 bytes
+// per thread where the rows allow (a tile row is 16 C consecutive floats): every thread of the
+// workgroup takes part, inside the image or not.
+__device__ __forceinline__ void copy_tile(const DrAntialiasArgs& a, const TilePixel& tp,
+                                          const float* __restrict__ src,
+                                          float* __restrict__ dst) {
+  const int C = a.channels;
+  const int x0 = tp.x & ~15, y0 = tp.y & ~15;
+  const int rows = min(16, a.height - y0), row_floats = min(16, a.width - x0) * C;
+  const int64_t first = (((int64_t)tp.b * a.height + y0) * a.width + x0) * C;
+  const int64_t stride = (int64_t)a.width * C;
+  const bool wide = row_floats % 4 == 0 && stride % 4 == 0 && first % 4 == 0 &&
+                    ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) == 0;
+  if (wide) {  // uniform
+    const int per_row = row_floats / 4;
+    for (int i = threadIdx.x; i < rows * per_row; i += blockDim.x) {
+      const int r = i / per_row;
+      const int64_t at = first + r * stride + 4 * (i - r * per_row);
+      store4(dst + at, load4(src + at));
+    }
+  } else {
+    for (int i = threadIdx.x; i < rows * row_floats; i += blockDim.x) {
+      const int r = i / row_floats;
+      const int64_t at = first + r * stride + (i - r * row_floats);
+      dst[at] = src[at];
+    }
+  }
+}
+
 // Every pixel evaluates the pairs it forms with its right and lower neighbours, once. The
 // loads go level by level over the (at most three) triangles involved -- ids, silhouette bits,
 // index rows, vertices -- so that each level's loads are in flight together: a wave where any
@@ -572,19 +601,13 @@ __global__ __launch_bounds__(256) void aa_blend_kernel(DrAntialiasArgs a, const 
                                                        const uchar2* pair_bits,
                                                        const uint8_t* tile_active, float* out) {
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
-  if (!tp.inside) return;
   const int C = a.channels;
   const TileFlags flags = SPARSE ? tile_flags(a, tp, tile_active) : TileFlags{true, true, true};
   if (SPARSE && !flags.any()) {  // uniform: no pair moves colour here
-    const float* color = a.color + tp.pixel * C;
-    for (int c0 = 0; c0 < C; c0 += NC) {
-      const int n = min(NC, C - c0);
-      float v[NC];
-      load_group<NC>(color + c0, n, v);
-      store_group<NC>(out + tp.pixel * C + c0, n, v);
-    }
+    copy_tile(a, tp, a.color, out);
     return;
   }
+  if (!tp.inside) return;
   const PixelPairs P = pixel_pairs(a, tp, pair_t, pair_bits, flags);
   float weight[4];
   bool any = false;
@@ -641,14 +664,7 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
   const int C = a.channels;
   const TileFlags flags = SPARSE ? tile_flags(a, tp, tile_active) : TileFlags{true, true, true};
   if (SPARSE && !flags.any()) {  // uniform: the gradient passes through
-    if (tp.inside && grad_color) {
-      for (int c0 = 0; c0 < C; c0 += NC) {
-        const int n = min(NC, C - c0);
-        float v[NC];
-        load_group<NC>(grad_out + tp.pixel * C + c0, n, v);
-        store_group<NC>(grad_color + tp.pixel * C + c0, n, v);
-      }
-    }
+    if (grad_color) copy_tile(a, tp, grad_out, grad_color);
     return;
   }
   if (SPARSE) table.init();
