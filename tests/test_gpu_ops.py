@@ -339,16 +339,17 @@ def test_antialias_matches_oracle(channels, mesh):
     assert_grads_close([ours[1][1]], [ref[1][1]])
 
 
-@pytest.mark.parametrize("channels", [3, 4])
-def test_antialias_small_objects_in_large_images(channels):
+@pytest.mark.parametrize("channels,size", [(3, (100, 120)), (4, (100, 120)), (3, (75, 101))])
+def test_antialias_small_objects_in_large_images(channels, size):
     # A few small triangles in 100 x 120 images: most 16 x 16 tiles hold no active pair and copy
-    # colour and gradient without reading pair records; the active ones sit next to them, with
-    # pairs across tile borders (a tile's left and upper neighbours' records).
+    # colour and gradient as whole tiles without reading pair records; the active ones sit next
+    # to them, with pairs across tile borders (a tile's left and upper neighbours' records). At
+    # 75 x 101 with 3 channels the tiles' rows are not 16-byte aligned (the per-float copy).
     gen = torch.Generator().manual_seed(41)
     pos, tri = tiny_mesh(12, gen, 0.18, batch=3)
-    rast, _ = R.rasterize(pos, tri, (100, 120), True)
-    color = torch.rand(3, 100, 120, channels, generator=gen)
-    weights = torch.randn(3, 100, 120, channels, generator=gen)
+    rast, _ = R.rasterize(pos, tri, size, True)
+    color = torch.rand(3, *size, channels, generator=gen)
+    weights = torch.randn(3, *size, channels, generator=gen)
     ref = grads_of(lambda c, p: R.antialias(c, rast, p, tri, 1.0), [color, pos], [weights], "cpu")
     ours = grads_of(lambda c, p: hip.antialias(c, rast.cuda(), p, tri.cuda(), 1.0),
                     [color, pos], [weights], "cuda")
