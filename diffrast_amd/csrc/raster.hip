@@ -1447,14 +1447,14 @@ __device__ __forceinline__ void resolve_pixel(const Tri& T, float px, float py, 
   }
 }
 
-// Two pixels per thread, in rows or tiles (pixel_slots); their loads go out level by level
-// (keys, index rows, vertices) so that a thread waits once per level for both.
+// Four pixels per thread, in rows or tiles (pixel_slots); their loads go out level by level
+// (keys, index rows, vertices) so that a thread waits once per level for all four.
 template <bool TILES>
 __global__ __launch_bounds__(256) void resolve_fwd_kernel(DrRasterGeometry g,
                                                           const uint64_t* keys, float* rast,
                                                           float* rast_db, float scale_x,
                                                           float scale_y) {
-  constexpr int kPixels = 2;
+  constexpr int kPixels = 4;
   const PixelSlots<kPixels> s = pixel_slots<kPixels, TILES>(g.batch, g.height, g.width);
   const int64_t* pixel = s.pixel;
   uint64_t key[kPixels];
@@ -1928,10 +1928,10 @@ extern "C" int dr_resolve_forward(const DrRasterGeometry* g, const uint64_t* key
   const int64_t image_tris = g->ranges != nullptr ? g->num_tri / std::max(g->batch, 1) : g->num_tri;
   const hipStream_t st = (hipStream_t)stream;
   if (gather_tiles(20 * image_tris))
-    resolve_fwd_kernel<true><<<pixel_slot_blocks<2, true>(g->batch, g->height, g->width), 256, 0,
+    resolve_fwd_kernel<true><<<pixel_slot_blocks<4, true>(g->batch, g->height, g->width), 256, 0,
                                st>>>(*g, keys, rast, rast_db, sx, sy);
   else
-    resolve_fwd_kernel<false><<<pixel_slot_blocks<2, false>(g->batch, g->height, g->width), 256,
+    resolve_fwd_kernel<false><<<pixel_slot_blocks<4, false>(g->batch, g->height, g->width), 256,
                                 0, st>>>(*g, keys, rast, rast_db, sx, sy);
   return launch_status();
 }
