@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
+import weakref
 from collections.abc import Sequence
 
 import torch
@@ -139,6 +140,20 @@ def _entry_capacity(count: int) -> int:
     return min(count + count // 8 + 4096, 0xffffffff)
 
 
+# The tile pass runs one workgroup per 16x16 tile when that grid is at most this many
+# workgroups and none smaller is asked for (dr_raster_visibility_tiles).
+_PLAIN_TILE_GRID = 1 << 16
+
+
+def _tile_grid(geo: _Geometry, groups: int) -> int:
+    """The tile pass's grid to ask for: none (one workgroup per tile) while that grid is small
+    enough for the kernel without the tile loop, which keeps fewer registers; else ``groups``
+    (a smaller grid runs the looping kernel, which covers every tile for any grid)."""
+    batch, height, width = geo.shape
+    tiles = batch * (-(-height // 16)) * (-(-width // 16))
+    return 0 if tiles <= _PLAIN_TILE_GRID else groups
+
+
 def _host_counts(device: torch.device) -> tuple[Tensor, torch.cuda.Event]:
     """Pinned memory for the counts of a first call and the event that marks their arrival
     (one pair per host thread and device: such a call waits for its counts)."""
@@ -160,26 +175,43 @@ def _remember(key: tuple, sizes: _Sizes) -> None:
 
 
 class _Order:
-    """A mesh's processing order on the device and whether a captured graph refers to it."""
+    """A mesh's processing order on the device, the tri it was computed from (a weak
+    reference: the order is valid for that tensor only) and whether a captured graph refers
+    to it."""
 
-    __slots__ = ("tensor", "pinned")
+    __slots__ = ("tensor", "ref", "pinned")
 
-    def __init__(self, tensor: Tensor):
-        self.tensor, self.pinned = tensor, False
+    def __init__(self, tensor: Tensor, ref: weakref.ref):
+        self.tensor, self.ref, self.pinned = tensor, ref, False
 
 
 _ORDERS: dict[tuple, _Order] = {}
 _ORDERS_KEPT = 8
-_orders_lock = threading.Lock()
+# Re-entrant: a tri freed by the garbage collector while this thread holds the lock calls
+# _forget_order.
+_orders_lock = threading.RLock()
+
+
+def _forget_order(key: tuple, dead: weakref.ref) -> None:
+    # A freed tri frees its order, pinned or not: a graph that drew it reads tri's memory too,
+    # so it cannot be replayed once tri is gone. The key may already name a newer tensor's
+    # entry (same address and version): only the dead tensor's own entry goes.
+    with _orders_lock:
+        entry = _ORDERS.get(key)
+        if entry is not None and entry.ref is dead:
+            del _ORDERS[key]
 
 
 def _order(geo: _Geometry, workspace: Tensor, workspace_bytes: int, capturing: bool) -> None:
     """Sets geo.struct.order to the processing order of geo's mesh, computed once per tri
-    (its storage, version and size, and the vertex count) and reused: the order is a spatial
-    sort that only the speed of the visibility depends on, so an order computed from earlier
-    positions of the same triangles stays valid. Under graph capture a remembered order is used
-    and then kept for good (the graph refers to it); none is computed there (the captured
-    visibility computes its own into the workspace)."""
+    tensor and reused while that tensor lives and is unchanged (its version counter): the
+    order is a spatial sort that only the speed of the visibility depends on, so an order
+    computed from earlier positions of the same triangles stays valid. An entry is found by
+    the tensor's address, version and sizes and accepted only for the very tensor it was
+    computed from (a new tri at a freed tri's address, with the same sizes and a fresh version
+    counter, gets its own). Under graph capture a remembered order is used and then kept while
+    its tri lives (the graph refers to it); none is computed there (the captured visibility
+    computes its own into the workspace)."""
     size = ctypes.c_size_t()
     call("dr_raster_order_size", ref(geo.struct), ctypes.byref(size))
     if size.value == 0:
@@ -191,6 +223,8 @@ def _order(geo: _Geometry, workspace: Tensor, workspace_bytes: int, capturing: b
            geo.struct.num_vertices)
     with _orders_lock:
         entry = _ORDERS.get(key)
+        if entry is not None and entry.ref() is not tri:
+            entry = None  # another tensor's order at a reused address
         if entry is not None and capturing:
             entry.pinned = True
     if entry is None:
@@ -199,9 +233,10 @@ def _order(geo: _Geometry, workspace: Tensor, workspace_bytes: int, capturing: b
         tensor = torch.empty(size.value, dtype=torch.uint8, device=device)
         call("dr_raster_order", ref(geo.struct), ptr(tensor), size.value, ptr(workspace),
              workspace_bytes, _lib.stream(device))
-        entry = _Order(tensor)
+        entry = _Order(tensor, weakref.ref(tri, lambda dead, key=key: _forget_order(key, dead)))
         with _orders_lock:
-            if len(_ORDERS) >= _ORDERS_KEPT and key not in _ORDERS:
+            _ORDERS.pop(key, None)
+            if len(_ORDERS) >= _ORDERS_KEPT:
                 for old in list(_ORDERS):
                     if not _ORDERS[old].pinned:
                         _ORDERS.pop(old)
@@ -242,7 +277,7 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
         arrived.record(torch.cuda.current_stream(device))
         arrived.synchronize()
         found = [v & 0xFFFFFFFF for v in host.tolist()]
-        counts = (ctypes.c_uint32 * 4)(*found)
+        counts = (ctypes.c_uint32 * 4)(found[0], found[1], _tile_grid(geo, found[2]), found[3])
         entries = torch.empty(max(found[1], 1), dtype=torch.int32, device=device)
         call("dr_raster_visibility_bin", ref(geo.struct), ptr(workspace), size.value,
              ptr(entries), counts, stream)
@@ -261,7 +296,7 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
     entries = torch.empty(capacity, dtype=torch.int32, device=device)
     # The four passes of dr_raster_visibility, queued one call each (so that each can be timed
     # on its own): start, bin and tiles into the buffer, overflow when it was too small.
-    spec = (ctypes.c_uint32 * 4)(0, capacity, groups, 0)
+    spec = (ctypes.c_uint32 * 4)(0, capacity, _tile_grid(geo, groups), 0)
 
     def passes(readback):
         call("dr_raster_visibility_start", ref(geo.struct), ptr(prev), ptr(keys), ptr(workspace),
@@ -365,27 +400,33 @@ def rasterize_layer(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad_
 
 # Device copies of range tables, by content: a range table drawn again (every DepthPeeler
 # takes its own copy of ``ranges``) is copied to the device once, so that later calls, and a
-# step captured in a HIP graph, make no host-to-device copy.
-_RANGE_COPIES: dict[tuple, tuple[Tensor, Tensor]] = {}
+# step captured in a HIP graph, make no host-to-device copy. A captured graph keeps the
+# copies' addresses in its kernel arguments and no reference to them, so a copy used under
+# capture is pinned: never evicted, for the life of the process.
+_RANGE_COPIES: dict[tuple, list] = {}  # key -> [ranges, prefix, pinned]; order = recency
 _RANGE_COPIES_KEPT = 16
 _range_lock = threading.Lock()
 
 
-def _range_tables(table: list[tuple[int, int]], prefix: list[int],
-                  device: torch.device) -> tuple[Tensor, Tensor]:
+def _range_tables(table: list[tuple[int, int]], prefix: list[int], device: torch.device,
+                  capturing: bool | None = None) -> tuple[Tensor, Tensor]:
+    if capturing is None:
+        capturing = device.type == "cuda" and torch.cuda.is_current_stream_capturing()
     key = (device, tuple(table))
     with _range_lock:
         found = _RANGE_COPIES.pop(key, None)
         if found is not None:
+            found[2] = found[2] or capturing
             _RANGE_COPIES[key] = found  # most recent now
-            return found
-    copies = (torch.tensor(table, dtype=torch.int32).to(device, non_blocking=True),
-              torch.tensor(prefix, dtype=torch.int64).to(device, non_blocking=True))
+            return found[0], found[1]
+    copies = [torch.tensor(table, dtype=torch.int32).to(device, non_blocking=True),
+              torch.tensor(prefix, dtype=torch.int64).to(device, non_blocking=True), capturing]
     with _range_lock:
         _RANGE_COPIES[key] = copies
-        while len(_RANGE_COPIES) > _RANGE_COPIES_KEPT:
-            del _RANGE_COPIES[next(iter(_RANGE_COPIES))]
-    return copies
+        unpinned = [k for k, v in _RANGE_COPIES.items() if not v[2]]
+        for old in unpinned[:max(0, len(_RANGE_COPIES) - _RANGE_COPIES_KEPT)]:
+            del _RANGE_COPIES[old]  # least recent unpinned first
+    return copies[0], copies[1]
 
 
 def rasterize_ranges(pos: Tensor, tri: Tensor, resolution: tuple[int, int], grad_db: bool,

@@ -1725,27 +1725,27 @@ static int queue_visibility_start(const DrRasterGeometry* g, const uint64_t* pre
   return DR_OK;
 }
 
-// Up to this many workgroups, a tile pass whose busy tiles are not known launches one per tile
-// (the idle ones return at once, ~0.2 us per thousand) rather than the looping kernel.
+// Up to this many workgroups, a tile pass without a requested grid launches one workgroup per
+// tile (the idle ones return at once, ~0.2 us per thousand) rather than the looping kernel.
 constexpr int64_t kPlainTileGrid = 1 << 16;
 
-// Launches the tile pass. exact: `requested` is the grid this call's counts give (8 x the busy
-// tiles of the largest share), so one workgroup per busy tile. Otherwise it is a guess (0: none)
-// and the grid is one workgroup per tile up to kPlainTileGrid tiles, else the guess (at least
-// 8, a multiple of 8, below 2^24) with the looping kernel, which covers every tile whatever
-// the grid.
+// Launches the tile pass so that it covers every busy tile whatever `requested` is. A grid of
+// at least one workgroup per tile (`requested` 0 or at least that, and then at most
+// kPlainTileGrid workgroups) runs the plain kernel, one tile per workgroup. Any smaller grid
+// runs the looping kernel: `requested` workgroups (0: one per tile), rounded up to a multiple
+// of 8 and kept below 2^24, each taking every (grid / 8)-th busy tile of its XCD share. So a
+// grid sized before the busy tiles were known, or sized wrongly by a caller, loses no tile.
 static void launch_tile_pass(const DrRasterGeometry& g, const uint64_t* prev, uint64_t* keys,
                              const Workspace& ws, const uint32_t* entries, uint32_t capacity,
-                             uint32_t requested, bool exact, hipStream_t s) {
+                             uint32_t requested, hipStream_t s) {
   const int64_t bound = tile_grid_bound(ws);
   const int64_t limit = ((int64_t)1 << 24) - kXcdShares;
-  if ((exact && requested > 0 && requested <= limit) || (!exact && bound <= kPlainTileGrid)) {
-    const int64_t grid = exact ? (int64_t)requested : bound;
-    raster_tile_kernel<false><<<(int)grid, 256, 0, s>>>(g, prev, keys, ws, entries, capacity);
+  const bool full = requested == 0 || (int64_t)requested >= bound;
+  if (full && bound <= kPlainTileGrid) {
+    raster_tile_kernel<false><<<(int)bound, 256, 0, s>>>(g, prev, keys, ws, entries, capacity);
     return;
   }
-  int64_t grid = requested == 0 ? bound : ((int64_t)requested + kXcdShares - 1) / kXcdShares *
-                                              kXcdShares;
+  int64_t grid = full ? bound : ((int64_t)requested + kXcdShares - 1) / kXcdShares * kXcdShares;
   grid = std::min(std::min(std::max<int64_t>(grid, kXcdShares), bound), limit);
   raster_tile_kernel<true><<<(int)grid, 256, 0, s>>>(g, prev, keys, ws, entries, capacity);
 }
@@ -1769,7 +1769,7 @@ static int queue_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys
   Workspace ws = layout(*g, (char*)workspace);
   if (capacity > 0) {
     raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, entries, capacity);
-    launch_tile_pass(*g, prev_keys, keys, ws, entries, capacity, tile_groups, false, s);
+    launch_tile_pass(*g, prev_keys, keys, ws, entries, capacity, tile_groups, s);
   }
   raster_overflow_kernel<<<overflow_grid(ws), 256, 0, s>>>(*g, prev_keys, keys, ws, capacity);
   return launch_status();
@@ -1904,9 +1904,7 @@ extern "C" int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint6
   if (!entries || !keys) return DR_ERR_ARGUMENT;
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
-  // counts[3] (busy tiles) is known only with this call's own counts: then counts[2] is exact.
-  launch_tile_pass(*g, prev_keys, keys, ws, entries, counts[1], counts[2], counts[3] != 0,
-                   (hipStream_t)stream);
+  launch_tile_pass(*g, prev_keys, keys, ws, entries, counts[1], counts[2], (hipStream_t)stream);
   return launch_status();
 }
 

@@ -5,10 +5,13 @@
  *
  * Every entry point takes plain device pointers, sizes and a hipStream_t (passed as void*),
  * enqueues its kernels on that stream and returns 0 or an error code (dr_error_string).
- * The library allocates no device memory and keeps no mutable global state: the caller
+ * Apart from dr_raster_visibility_static, the library allocates no device memory: the caller
  * allocates every output, gradient and workspace buffer (the *_workspace_size queries give
- * sizes) and zeroes the targets of gradient accumulation. Calls are re-entrant and ordered
- * by their stream. All float data is float32; every array is dense (C-contiguous).
+ * sizes) and zeroes the targets of gradient accumulation. Its mutable global state is small
+ * and named where it lives: the static 64 MiB device buffer of dr_raster_visibility_static
+ * (one per device, created when the library's code is loaded on it) with that buffer's
+ * device addresses, and the per-host-thread pinned buffer of dr_raster_visibility_begin.
+ * Calls are re-entrant and ordered by their stream (dr_raster_visibility_static: see there). All float data is float32; every array is dense (C-contiguous).
  *
  * Each entry point cites the interface of the reference diffrast (github.com/sennecools/
  * diffrast) that it replaces. The reference's GPU path is Python: its backend modules
@@ -124,9 +127,12 @@ int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspace, size_t 
 
 /* Visibility, third part: rasterizes the binned triangles tile by tile into keys, after
  * dr_raster_visibility_bin with the same entries and counts. Nothing to do when
- * counts[1] == 0. The pass runs counts[2] workgroups (rounded up to a multiple of 8; 0: one per
- * tile of the largest XCD share, 8 x); each takes every (grid / 8)-th busy tile of its share,
- * so any grid covers all tiles. */
+ * counts[1] == 0. counts[2] is the pass's grid: 0, or at least one workgroup per 16x16 tile,
+ * runs one workgroup per tile when that is at most 65536 workgroups; any smaller grid (rounded
+ * up to a multiple of 8) runs a looping kernel in which each workgroup takes every
+ * (grid / 8)-th busy tile of its XCD share. Either way every tile is covered, whatever
+ * counts[2] and counts[3] hold; counts[2] as dr_raster_visibility_begin returns it is the
+ * smallest grid that gives each busy tile its own workgroup. counts[3] is not read. */
 int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                uint64_t* keys, void* workspace, size_t workspace_bytes,
                                const uint32_t* entries, const uint32_t counts[4], void* stream);
@@ -166,8 +172,9 @@ int dr_raster_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys, u
  * (dr_raster_workspace_size) must leave room for 4096 tile entries, i.e. be at most
  * 64 MiB - 16 KiB (DR_ERR_SCRATCH otherwise: about 690K triangle instances at 512x512, 870K
  * at 4 x 1024^2); tile lists beyond the rest of the buffer go through the overflow pass.
- * Each GPU holds its own copy of the buffer from the first call on it (the device current at
- * the call) until the process ends. Every call on a GPU shares that GPU's buffer: calls that
+ * The buffer is part of the library's device code: each GPU on which the library's code is
+ * loaded (the first launch of any of its kernels there, whichever entry point) holds its own
+ * 64 MiB copy until the process ends, also in processes that never call this entry point. Every call on a GPU shares that GPU's buffer: calls that
  * overlap on one GPU (other streams, other threads) race and must be serialised by the caller.
  * Each call prepares what it reads, so what an earlier call left there does not matter. */
 int dr_raster_visibility_static(const DrRasterGeometry* g, const uint64_t* prev_keys,

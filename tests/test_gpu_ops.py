@@ -216,6 +216,28 @@ def test_texture_max_mip_level(max_mip_level):
     assert rel_error(out, ref) < VALUE_TOL
 
 
+@pytest.mark.parametrize("max_mip_level", [0, 1, 2, 9])
+@pytest.mark.parametrize("filter_mode", ["linear-mipmap-linear", "linear-mipmap-nearest"])
+def test_cube_texture_max_mip_level(max_mip_level, filter_mode):
+    # A limited chain on a cube map (each face 16x16, so 9 is past the 1x1 level), with a bias:
+    # values and every gradient against the oracle.
+    gen = torch.Generator().manual_seed(11 + max_mip_level)
+    tex = torch.rand(1, 6, 16, 16, 3, generator=gen)
+    dirs = torch.randn(2, 9, 11, 3, generator=gen)
+    dirs_da = torch.randn(2, 9, 11, 6, generator=gen) * 0.3
+    bias = torch.rand(2, 9, 11, generator=gen) * 2.5
+    weights = torch.randn(2, 9, 11, 3, generator=gen)
+
+    def run(fn):
+        return lambda t, d, dd, b: fn(t, d, dd, filter_mode, "cube", max_mip_level,
+                                      mip_level_bias=b)
+
+    outs, grads = grads_of(run(hip.texture), [tex, dirs, dirs_da, bias], [weights], "cuda")
+    e_outs, e_grads = grads_of(run(R.texture), [tex, dirs, dirs_da, bias], [weights], "cpu")
+    assert rel_error(outs[0], e_outs[0]) < VALUE_TOL
+    assert_grads_close(grads, e_grads)
+
+
 @pytest.mark.parametrize("size", [(16, 16), (5, 7), (1, 13), (37, 50)])
 def test_mip_chain_matches_oracle(size):
     tex = torch.randn(2, *size, 3, generator=torch.Generator().manual_seed(3))

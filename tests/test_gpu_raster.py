@@ -555,8 +555,9 @@ def _keys_one_call(pos, tri, res, capacity, groups, prev=None):
     return keys, [v & 0xFFFFFFFF for v in host.tolist()]
 
 
-def _keys_waiting(pos, tri, res, prev=None):
-    """Keys from dr_raster_visibility_begin (which waits for the counts), bin and tiles."""
+def _keys_waiting(pos, tri, res, prev=None, groups=None):
+    """Keys from dr_raster_visibility_begin (which waits for the counts), bin and tiles (with
+    a tile pass of ``groups`` workgroups instead of the counted grid, if given)."""
     import ctypes
 
     from diffrast_amd.backends import _lib
@@ -574,11 +575,103 @@ def _keys_waiting(pos, tri, res, prev=None):
         entries = torch.empty(counts[1], dtype=torch.int32, device=pos.device)
         _lib.call("dr_raster_visibility_bin", _lib.ref(geo.struct), _lib.ptr(workspace),
                   size.value, _lib.ptr(entries), counts, stream)
+        grid = counts if groups is None else (ctypes.c_uint32 * 4)(
+            counts[0], counts[1], groups, counts[3])
         _lib.call("dr_raster_visibility_tiles", _lib.ref(geo.struct), _lib.ptr(prev),
-                  _lib.ptr(keys), _lib.ptr(workspace), size.value, _lib.ptr(entries), counts,
+                  _lib.ptr(keys), _lib.ptr(workspace), size.value, _lib.ptr(entries), grid,
                   stream)
     torch.cuda.synchronize()
     return keys, list(counts)
+
+
+def _ids_of(keys):
+    """Triangle ids (-1: none) of visibility keys."""
+    return torch.where(keys == -1, torch.full_like(keys, -1), keys & 0xFFFFFFFF)
+
+
+def _native_layers(pos, tri, res, count):
+    """Ids of ``count`` peel layers from the oracle's brute force at every pixel."""
+    from oracle import native
+    h, w = res
+    batch = pos.shape[0]
+    b, row, col = (t.reshape(-1) for t in torch.meshgrid(
+        torch.arange(batch), torch.arange(h), torch.arange(w), indexing="ij"))
+    previous, out = None, []
+    for _ in range(count):
+        previous = native.visible_at(pos, tri, h, w, b, row, col, previous)
+        out.append(previous[1].view(batch, h, w))
+    return out
+
+
+@pytest.mark.parametrize("groups", [8, 24])
+def test_tile_pass_with_a_short_grid_covers_every_tile(groups):
+    # dr_raster_visibility_tiles with the call's own counts but a grid smaller than one
+    # workgroup per busy tile: every tile must still be rasterized (every pixel against the
+    # oracle, two layers).
+    pos, tri = mixed_mesh(torch.Generator().manual_seed(12), batch=3)
+    res = (96, 80)
+    expect = _native_layers(pos, tri, res, 2)
+    pos, tri = pos.cuda().contiguous(), tri.cuda().int().contiguous()
+    prev = None
+    for layer in range(2):
+        keys, counts = _keys_waiting(pos, tri, res, prev, groups=groups)
+        assert counts[3] > 0 and counts[2] > groups
+        assert torch.equal(_ids_of(keys).cpu(), expect[layer]), layer
+        prev = keys
+
+
+def test_looping_tile_pass_beyond_the_plain_grid():
+    # 1040 images of 128 x 128 are 66,560 tiles, more than the tile pass launches one
+    # workgroup each for: the backend and the one-call entry point with grids of 8 and 24
+    # run the looping kernel. Every pixel of two layers against the oracle.
+    gen = torch.Generator().manual_seed(13)
+    pos, tri = random_mesh(6, gen, batch=1040)
+    res = (128, 128)
+    expect = _native_layers(pos, tri, res, 2)
+    assert (expect[1] >= 0).any()
+    pos_dev, tri_dev = pos.cuda().contiguous(), tri.cuda().contiguous()
+    hip._SIZES.clear()
+    for repeat in range(2):  # the first call learns the sizes, the second queues at once
+        state = None
+        for layer in range(2):
+            rast, _, state = hip.rasterize_layer(pos_dev, tri_dev, res, False, state)
+            assert torch.equal(rast[..., 3].long().cpu() - 1, expect[layer]), (repeat, layer)
+    for groups in (8, 24):
+        prev = None
+        for layer in range(2):
+            keys, _ = _keys_one_call(pos_dev, tri_dev, res, 1 << 22, groups, prev)
+            assert torch.equal(_ids_of(keys).cpu(), expect[layer]), (groups, layer)
+            prev = keys
+
+
+def test_processing_order_of_a_freed_tri_is_not_taken_by_a_new_one():
+    # A tri freed and a different tri of the same shape allocated at its address, with a
+    # fresh version counter: the new one must get its own processing order (the old one
+    # carries the old triangles' vertex rows and ids).
+    from diffrast_amd import workloads as W
+    gen = torch.Generator().manual_seed(24)
+    verts, tri = W.icosphere(5)
+    pos = W.clip_positions(verts, W.random_eyes(2, 3.0, gen), 1.0)
+    res = (64, 80)
+    hip._ORDERS.clear()
+    first = tri.cuda()
+    address = first.data_ptr()
+    hip.rasterize_layer(pos.cuda(), first, res, True, None)
+    assert len(hip._ORDERS) == 1
+    del first
+    torch.cuda.synchronize()
+    other_cpu = tri[torch.randperm(tri.shape[0], generator=gen)].contiguous()
+    held = []
+    other = other_cpu.cuda()
+    while other.data_ptr() != address and len(held) < 64:
+        held.append(other)
+        other = other_cpu.cuda()
+    assert other.data_ptr() == address and other._version == 0
+    rast, db, _ = hip.rasterize_layer(pos.cuda(), other, res, True, None)
+    (er, ed), = oracle_layers(pos, other_cpu, res, 1)
+    assert torch.equal(rast[..., 3].cpu(), er[..., 3])
+    assert rel_error(db.cpu(), ed) < VALUE_TOL
+    del held
 
 
 @pytest.mark.parametrize("resolution", [(96, 80), (40, 24), (300, 17)])

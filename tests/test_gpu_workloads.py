@@ -1,12 +1,15 @@
-"""The five benchmark workloads at their full sizes, checked at sampled pixels.
+"""The five benchmark workloads at their full sizes, ids checked by brute force at thousands of
+pixels per image.
 
 The oracle cannot rasterize a 1.3M-triangle mesh at 8 x 1024^2 in a test, but its brute-force
-visibility at a list of pixels (``visible_at``) goes through the same arithmetic for every
-(triangle, pixel) pair, so ids must be bit-exact there; rast values come from the oracle's
-resolve of those ids. Interpolate and texture are per-pixel operations: the oracle runs on the
-GPU's own inputs at the sampled pixels (packed into a one-row image) and must agree to the
-stated tolerance (interpolate bit-exact). Gradients are checked at the small sizes of the other
-test files.
+visibility at a list of pixels goes through the same arithmetic for every (triangle, pixel)
+pair, so ids must be bit-exact there. The list is mostly pixels where the GPU's id differs
+from a 4-neighbour's -- silhouettes and triangle edges, where the fill rule and depth ties
+decide -- plus pixels anywhere; every triangle of the mesh is tested at each of them, by the
+oracle's C restatement (oracle/visible.c, pinned to the PyTorch oracle on the CPU). rast values
+come from the oracle's resolve of those ids. Interpolate and texture are per-pixel operations:
+the oracle runs on the GPU's own inputs at the sampled pixels (packed into a one-row image) and
+must agree to the stated tolerance (interpolate bit-exact).
 """
 
 import contextlib
@@ -18,28 +21,48 @@ import torch
 import diffrast_amd as dr
 from diffrast_amd import workloads
 from helpers import rel_error
+from oracle import native
 from oracle import reference as R
 
 pytestmark = pytest.mark.gpu
 
 VALUE_TOL = 1e-5
 GRAD_TOL = 1e-4
-SAMPLES = 48  # pixels per checked image: half covered (by the GPU result), half anywhere
+EDGE_SAMPLES = 4096  # per checked image: pixels whose id differs from a 4-neighbour's
+OTHER_SAMPLES = 512  # per checked image: anywhere
+# Gradient entries per view that may need the oracle's level of detail moved by one unit in the
+# last place to come within tolerance (log2's last bit is unpinned; see the one-view test).
+MAX_LOD_SHIFTED = 64
 
 
-def sample_pixels(ids, image, gen):
-    """(row, col) of SAMPLES pixels of ``image``: half where ids shows a triangle."""
-    covered = (ids[image] >= 0).nonzero()
-    anywhere = torch.stack([torch.randint(0, ids.shape[1], (SAMPLES // 2,), generator=gen),
-                            torch.randint(0, ids.shape[2], (SAMPLES // 2,), generator=gen)], 1)
-    pick = covered[torch.randperm(covered.shape[0], generator=gen)[:SAMPLES // 2]]
-    rc = torch.cat([pick, anywhere])
+def edge_mask(ids):
+    """Pixels of ids [B, H, W] whose id differs from one of their 4-neighbours'."""
+    edge = torch.zeros_like(ids, dtype=torch.bool)
+    right = ids[:, :, 1:] != ids[:, :, :-1]
+    down = ids[:, 1:, :] != ids[:, :-1, :]
+    edge[:, :, 1:] |= right
+    edge[:, :, :-1] |= right
+    edge[:, 1:, :] |= down
+    edge[:, :-1, :] |= down
+    return edge
+
+
+def sample_pixels(ids, image, gen, edges=EDGE_SAMPLES, anywhere=OTHER_SAMPLES,
+                  mask=None):
+    """(row, col) of up to ``edges`` pixels of ``image`` on an id edge (of ``mask`` if given)
+    and ``anywhere`` more anywhere."""
+    on_edge = (edge_mask(ids[image:image + 1])[0] if mask is None else mask).nonzero()
+    pick = on_edge[torch.randperm(on_edge.shape[0], generator=gen)[:edges]]
+    rand = torch.stack([torch.randint(0, ids.shape[1], (anywhere,), generator=gen),
+                        torch.randint(0, ids.shape[2], (anywhere,), generator=gen)], 1)
+    rc = torch.cat([pick, rand])
     return rc[:, 0], rc[:, 1]
 
 
 def check_visibility(pos, tri, rast, images, gen, offset=0, previous=None):
-    """Ids bit-exact and rast within VALUE_TOL at sampled pixels of ``images``; returns the
-    sampled (b, row, col) and the oracle's (depth, id) there."""
+    """Ids bit-exact against brute force and rast within VALUE_TOL at sampled pixels of
+    ``images`` (mostly id edges); returns the sampled (b, row, col) and the oracle's (depth, id)
+    there."""
     H, W = rast.shape[1:3]
     gpu_ids = rast[..., 3].long() - 1
     bs, rows, cols = [], [], []
@@ -49,18 +72,21 @@ def check_visibility(pos, tri, rast, images, gen, offset=0, previous=None):
         rows.append(r)
         cols.append(c)
     b, row, col = torch.cat(bs), torch.cat(rows), torch.cat(cols)
-    depth, ids = R.visible_at(pos, tri, H, W, b if pos.shape[0] > 1 else torch.zeros_like(b),
-                              row, col, previous)
+    edges = edge_mask(gpu_ids)[b, row, col].sum().item()
+    assert edges >= min(EDGE_SAMPLES, 1000) * len(images), edges
+    image_of = b if pos.shape[0] > 1 else torch.zeros_like(b)
+    depth, ids = native.visible_at(pos, tri, H, W, image_of, row, col, previous)
     ids = torch.where(ids >= 0, ids + offset, ids)
-    assert torch.equal(gpu_ids[b, row, col], ids), "ids differ at sampled pixels"
+    differ = (gpu_ids[b, row, col] != ids).sum().item()
+    assert differ == 0, f"ids differ at {differ} of {b.numel()} sampled pixels"
+    print(f"ids bit-exact at {b.numel()} pixels ({edges} on id edges) of images {list(images)}")
     # rast there, from the oracle's resolve of those ids (one image per checked pixel).
-    full_tri = tri if offset == 0 else None
-    if full_tri is not None:
+    if offset == 0:
         tri_id = torch.full((pos.shape[0],) + tuple(rast.shape[1:3]), -1, dtype=torch.long)
-        tri_id[b if pos.shape[0] > 1 else torch.zeros_like(b), row, col] = ids
+        tri_id[image_of, row, col] = ids
         ref, _ = R.rasterize_from_ids(pos, tri, tri_id, False)
         ours = rast[b, row, col]
-        expect = ref[b if pos.shape[0] > 1 else torch.zeros_like(b), row, col]
+        expect = ref[image_of, row, col]
         assert rel_error(ours[:, :3], expect[:, :3]) < VALUE_TOL
     return (b, row, col), (depth, ids)
 
@@ -176,7 +202,8 @@ def test_cubemap_workload_at_sampled_pixels():
 
 def test_instances_workload_layers_at_sampled_pixels():
     # Range mode with depth peeling: item i draws triangles [start, start + count); each of
-    # the four layers must match the oracle's peel of that item alone.
+    # the four layers must match the oracle's peel of that item alone, at pixels on the id
+    # edges of any layer and anywhere, for 16 items.
     w = workloads.build("instances")
     t = w.tensors
     dev = torch.device("cuda", 0)
@@ -186,22 +213,29 @@ def test_instances_workload_layers_at_sampled_pixels():
                         ranges=ranges) as peeler:
         for _ in range(4):
             layers.append(peeler.rasterize_next_layer()[0].cpu())
+    gpu_ids = [rast[..., 3].long() - 1 for rast in layers]
     gen = torch.Generator().manual_seed(33)
-    for item in (0, 97, 255):
+    items = sorted({0, 97, 255} | set(torch.randperm(256, generator=gen)[:13].tolist()))
+    checked = edges = 0
+    for item in items:
         start, count = (int(v) for v in ranges[item])
         own = tri[start:start + count]
+        mask = torch.zeros(w.resolution, dtype=torch.bool)
+        for ids in gpu_ids:
+            mask |= edge_mask(ids[item:item + 1])[0]
+        row, col = sample_pixels(gpu_ids[0], item, gen, edges=1024, anywhere=128, mask=mask)
+        b = torch.zeros_like(row)
         previous = None
-        where = None
-        for rast in layers:
-            one = rast[item:item + 1]
-            gpu_ids = one[..., 3].long() - 1
-            if where is None:
-                r, c = sample_pixels(gpu_ids, 0, gen)
-                where = (torch.zeros_like(r), r, c)
-            b, row, col = where
-            depth, ids = R.visible_at(pos[None], own, *w.resolution, b, row, col, previous)
-            assert torch.equal(gpu_ids[b, row, col], torch.where(ids >= 0, ids + start, ids))
-            previous = (depth, ids)
+        for layer, ids in enumerate(gpu_ids):
+            depth, expect = native.visible_at(pos, own, *w.resolution, b, row, col, previous)
+            expect = torch.where(expect >= 0, expect + start, expect)
+            got = ids[item, row, col]
+            assert torch.equal(got, expect), (item, layer, (got != expect).sum().item())
+            previous = (depth, expect - start * (expect >= 0))
+            checked += row.numel()
+        edges += mask[row, col].sum().item()
+    print(f"{len(items)} items x 4 layers: ids bit-exact at {checked} pixel-layers "
+          f"({edges} pixels on an id edge of some layer)")
 
 
 # ---- one view of each textured workload, forward and backward in full ------------------------
@@ -357,9 +391,8 @@ def test_one_view_forward_and_backward_in_full(name, view):
     ids = ours["rast"][..., 3].long() - 1
     ref, ref_grads = _one_view(w, _Oracle(), "cpu", ids, view=view)
     assert (ids >= 0).any()
-    if w.name == "grid":
-        check_visibility(w.tensors["pos"][view:view + 1], w.tensors["tri"], ours["rast"], [0],
-                         torch.Generator().manual_seed(34 + view))
+    check_visibility(w.tensors["pos"][view:view + 1], w.tensors["tri"], ours["rast"], [0],
+                     torch.Generator().manual_seed(34 + view))
     assert torch.equal(ours["rast"][..., 3], ref["rast"][..., 3])
     assert (ours["aa"] != ours["col"]).any(), "antialiasing should change silhouette pixels"
     errors = {key: rel_error(ours[key], expect) for key, expect in ref.items()}
@@ -375,15 +408,20 @@ def test_one_view_forward_and_backward_in_full(name, view):
 
     worst = excess(ref_grads)
     as_computed = {key: e.max().item() for key, e in worst.items()}
-    if any(e >= GRAD_TOL for e in as_computed.values()):
+    # Entries outside the tolerance of the oracle with its level as computed: each must come
+    # within it with the level one unit up or down, and they must stay few.
+    outside = {key: (e >= GRAD_TOL).sum().item() for key, e in worst.items()}
+    if any(outside.values()):
         for ulps in (1, -1):
             with _lod_shifted(ulps):
                 _, shifted = _one_view(w, _Oracle(), "cpu", ids, view=view)
             worst = {key: torch.minimum(e, excess(shifted)[key]) for key, e in worst.items()}
     final = {key: e.max().item() for key, e in worst.items()}
     print(name, "values", errors, "gradient excess / max: as computed", as_computed,
-          "within one unit of the level", final)
+          "within one unit of the level", final, "entries that needed the level shifted",
+          outside, "of", {key: g.numel() for key, g in ref_grads.items()})
     assert all(e < GRAD_TOL for e in final.values()), final
+    assert all(n <= MAX_LOD_SHIFTED for n in outside.values()), outside
 
 
 def test_instances_antialias_on_layer_zero():

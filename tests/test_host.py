@@ -289,3 +289,31 @@ def test_log_levels_and_compat_aliases():
 
     assert dt.rasterize is dr.rasterize and diffrast.ops is ops
     assert compat._displaced == {}
+
+
+def test_range_tables_used_under_capture_are_never_evicted():
+    # A captured graph keeps the device range tables' addresses, so a table used while a stream
+    # is captured stays for good; beyond 16 tables the others are evicted, least recent first.
+    from diffrast_amd.backends import hip
+
+    cpu = torch.device("cpu")
+    hip._RANGE_COPIES.clear()
+    try:
+        pinned = hip._range_tables([(0, 3), (3, 3)], [0, 3, 6], cpu, capturing=True)
+        for i in range(40):
+            hip._range_tables([(i, 1)], [0, 1], cpu, capturing=False)
+        assert len(hip._RANGE_COPIES) == hip._RANGE_COPIES_KEPT
+        again = hip._range_tables([(0, 3), (3, 3)], [0, 3, 6], cpu, capturing=False)
+        assert again[0] is pinned[0] and again[1] is pinned[1]
+        assert torch.equal(pinned[1], torch.tensor([0, 3, 6]))
+        # A table first drawn eagerly and then under capture becomes pinned too.
+        hip._range_tables([(7, 2)], [0, 2], cpu, capturing=False)
+        hip._range_tables([(7, 2)], [0, 2], cpu, capturing=True)
+        for i in range(40, 80):
+            hip._range_tables([(i, 1)], [0, 1], cpu, capturing=False)
+        keys = {key[1] for key in hip._RANGE_COPIES}
+        assert ((0, 3), (3, 3)) in keys and ((7, 2),) in keys
+        assert ((40, 1),) not in keys and ((79, 1),) in keys
+        assert len(hip._RANGE_COPIES) == hip._RANGE_COPIES_KEPT
+    finally:
+        hip._RANGE_COPIES.clear()

@@ -387,6 +387,79 @@ def test_mip_chain_equals_exact_area_weights(size):
         torch.testing.assert_close(level, expected, rtol=1e-12, atol=1e-12)
 
 
+def box_chain(tex, count):
+    """The first ``count`` levels of a power-of-two texture (``[..., h, w, c]``: 2D or cube),
+    each the mean of 2x2 blocks of the one before, built here independently of the oracle."""
+    levels = [tex]
+    while len(levels) < count:
+        t = levels[-1]
+        levels.append((t[..., 0::2, 0::2, :] + t[..., 1::2, 0::2, :] + t[..., 0::2, 1::2, :]
+                       + t[..., 1::2, 1::2, :]) / 4)
+    return levels
+
+
+def mip_scene(cube, seed):
+    gen = torch.Generator().manual_seed(seed)
+    shape = (1, 6, 16, 16, 3) if cube else (1, 16, 16, 3)
+    tex = torch.rand(*shape, generator=gen, dtype=torch.float64)
+    if cube:
+        uv = torch.randn(1, 6, 7, 3, generator=gen, dtype=torch.float64)
+        uv_da = torch.randn(1, 6, 7, 6, generator=gen, dtype=torch.float64) * 0.4
+    else:
+        uv = torch.rand(1, 6, 7, 2, generator=gen, dtype=torch.float64)
+        uv_da = torch.randn(1, 6, 7, 4, generator=gen, dtype=torch.float64) * 0.3
+    bias = torch.rand(1, 6, 7, generator=gen, dtype=torch.float64) * 3
+    return tex, uv, uv_da, bias, "cube" if cube else "wrap"
+
+
+@pytest.mark.parametrize("cube", [False, True])
+def test_max_mip_level_zero_is_the_plain_linear_lookup(cube):
+    # With the chain stopped at level 0 the level of detail is clamped to 0: both taps read
+    # level 0 and the blend weight is 0, so the result is the non-mipmapped bilinear lookup,
+    # whatever the footprint and the bias (reference tests/test_cube.py:354-368).
+    tex, uv, uv_da, bias, boundary = mip_scene(cube, 20)
+    linear = R.texture(tex, uv, None, "linear", boundary, None)
+    for da, b in ((uv_da, None), (uv_da * 50, bias), (None, bias * 4)):
+        out = R.texture(tex, uv, da, "linear-mipmap-linear", boundary, 0, mip_level_bias=b)
+        assert torch.equal(out, linear)
+        nearest_level = R.texture(tex, uv, da, "linear-mipmap-nearest", boundary, 0,
+                                  mip_level_bias=b)
+        assert torch.equal(nearest_level, linear)
+
+
+@pytest.mark.parametrize("cube", [False, True])
+@pytest.mark.parametrize("k", [1, 2, 3, 9])
+def test_max_mip_level_limits_the_chain_to_its_first_levels(cube, k):
+    # A chain limited to k holds levels 0..k (fewer when the texture runs out: 16x16 has five),
+    # equal to an explicit list of the first k box-filtered levels; a bias far past the top
+    # reads the top level alone (reference tests/test_mip.py:119-130, tests/test_cube.py:
+    # 354-398).
+    tex, uv, uv_da, bias, boundary = mip_scene(cube, 21 + k)
+    full = 5
+    count = min(k, full - 1) + 1
+    chain = R.mip_chain(tex, k)
+    explicit = box_chain(tex, count)
+    assert len(chain) == count and len(R.texture_construct_mip(tex, k)) == count - 1
+    for ours, expect in zip(chain, explicit):
+        assert ours.shape == expect.shape
+        torch.testing.assert_close(ours, expect, rtol=1e-13, atol=1e-13)
+    for mode in ("linear-mipmap-linear", "linear-mipmap-nearest"):
+        limited = R.texture(tex, uv, uv_da, mode, boundary, k, mip_level_bias=bias)
+        listed = R.texture(tex, uv, uv_da, mode, boundary, None, mip_level_bias=bias,
+                           mip=explicit[1:])
+        torch.testing.assert_close(limited, listed, rtol=1e-12, atol=1e-12)
+        cut = R.texture(tex, uv, uv_da, mode, boundary, k, mip_level_bias=bias,
+                        mip=box_chain(tex, full)[1:])
+        torch.testing.assert_close(cut, listed, rtol=1e-12, atol=1e-12)
+        packed = R.texture(tex, uv, uv_da, mode, boundary, k, mip_level_bias=bias,
+                           packed=R.pack(box_chain(tex, full)))
+        torch.testing.assert_close(packed, listed, rtol=1e-12, atol=1e-12)
+    far = torch.full_like(bias, 40.0)
+    top = R.texture(tex, uv, uv_da, "linear-mipmap-linear", boundary, k, mip_level_bias=far)
+    alone = R.texture(explicit[-1], uv, None, "linear", boundary, None)
+    torch.testing.assert_close(top, alone, rtol=1e-13, atol=1e-13)
+
+
 # ---- cube maps -------------------------------------------------------------------------------
 
 
