@@ -7,30 +7,36 @@ triangles, radially perturbed, 8 views at 1024x1024. One step is
     -> texture(1024x1024x4, full mip chain built in the call, trilinear, wrap)
     -> shade = colour + 0.1 * (f[..., 0:4] + f[..., 4:8]) -> antialias -> MSE -> backward
 
-with gradients to positions, features and texture (the feature sum is written as a sum over a
-[..., 2, 4] view of f: one reduction instead of two strided slices). ``--workload`` selects one
-of the other four configurations (``make_step`` shows each step) and ``--all-workloads`` runs
-all five, one JSON line each. Inputs are synthetic and resident on the GPU before timing
-starts. ``--steps`` steps are timed between synchronisations, after ``--warmup`` untimed ones.
+with gradients to positions, features and texture. ``--workload`` selects one of the other
+four configurations (``make_step`` shows each step) and ``--all-workloads`` runs all five, one
+JSON line each. Inputs are synthetic and resident on the GPU before timing starts.
+
+Timing: the first two of the ``--warmup`` untimed steps are timed one by one as the first-call
+costs (``first_call``); ``--steps`` steps are timed back to back between synchronisations
+(``value``); then ``--repeats`` individually synchronised steps give the median, p10 and p90
+(``synced_steps``, the reference benchmarks' rule).
 
 Per-kernel time: HIP events around the C-ABI entry points, on the stream they launch on (in the
-timed steps only around the dominant one; every entry point in five further steps for the
-per-kernel table). Algorithmic bytes are the unique-byte model of ``BytesModel``: every input
-read once and every output written once, from each call's own arguments. ``roofline`` reports
-the longest-running entry point that launches a single kernel (so that its event time is that
-kernel's duration): its unique bytes per launch over its mean duration, against 8 TB/s; its
-vector issue against the issue peak (``valu``, from the committed counter summary); each op's
-forward+backward time against the HBM time of its unique bytes (``ops``); and the whole step
-against the four ops' bytes (``step``). ``traffic`` is the HBM bytes per launch measured for
-that kernel with rocprofv3 counters (FETCH_SIZE, WRITE_SIZE, each scaled by the counter's
-reading for a copy of known size), from ``profiles/kernels.<workload>.pmc.txt`` when present.
-``--graph`` times a step captured in a HIP graph and replayed (the eager time stays in the
-line as ``eager_ms_per_step``).
+timed steps only around the dominant one; every entry point in 15 further steps for the
+per-kernel and per-op tables, with each op's p10 and p90 over those steps). Algorithmic bytes
+are the unique-byte model of ``BytesModel``: every input read once and every output written
+once, from each call's own arguments. ``roofline`` reports the longest-running entry point that
+launches a single kernel (so that its event time is that kernel's duration): its unique bytes
+per launch over its mean duration, against 8 TB/s; its vector issue against the issue peak
+(``valu``, from the committed counter summary); each op's forward+backward time against the HBM
+time of its unique bytes (``ops``); the whole step against the four ops' bytes (``step``); and
+the device atomics of the backward scatters (``atomics``, from the committed counter summary,
+rated over the live launch times). ``traffic`` is the HBM bytes per launch measured for that
+kernel with rocprofv3 counters (FETCH_SIZE, WRITE_SIZE, each scaled by the counter's reading
+for a copy of known size), from ``profiles/kernels.<workload>.pmc.txt`` when present.
+``--graph`` times a step captured in a HIP graph and replayed, the loss reduction outside the
+graph (the eager time stays in the line as ``eager_ms_per_step``).
 
 CPU baseline: the oracle (a pure-PyTorch restatement of the reference backend) on the host
-cores, on a bounded sample of the same workload -- one image, its visibility over a subset of
-the triangles and the rest of the pipeline in full -- extrapolated linearly to all triangles,
-layers and images.
+cores, the whole step where its brute-force visibility is small enough (the sphere and textured
+workloads), else a bounded sample of the same workload -- one image, its visibility over a
+subset of the triangles and the rest of the pipeline in full -- extrapolated linearly to all
+triangles, layers and images.
 """
 
 from __future__ import annotations
@@ -72,12 +78,13 @@ SINGLE_KERNEL = {
 class KernelTimer:
     """HIP events around the backend's C-ABI calls, on the current stream, with the algorithmic
     bytes of each call: its kernel's own (``kernel_bytes``) and its share of its op's
-    (``op_bytes``)."""
+    (``op_bytes``). Each event pair is tagged with ``step_index`` at the time of the call."""
 
     def __init__(self, model):
         self.model = model
         self.active = False
         self.only = None  # entry point names to time (None: every one)
+        self.step_index = 0
         self._call = hip.call
         self.reset()
 
@@ -96,7 +103,7 @@ class KernelTimer:
             start.record()
             self._call(name, *args)
             end.record()
-            self.events[name].append((start, end))
+            self.events[name].append((start, end, self.step_index))
             self.bytes[name] += self.model.kernel_bytes(name, args)
             self.op_bytes[name] += self.model.op_bytes(name, args)
 
@@ -106,11 +113,21 @@ class KernelTimer:
         hip.call = self._call
 
     def summary(self):
+        """name -> (total ms, launches)."""
         torch.cuda.synchronize()
         out = {}
         for name, pairs in self.events.items():
-            times = [s.elapsed_time(e) for s, e in pairs]
+            times = [s.elapsed_time(e) for s, e, _ in pairs]
             out[name] = (sum(times), len(times))
+        return out
+
+    def per_step(self, names) -> dict[int, float]:
+        """step index -> ms of the entry points ``names`` in that step."""
+        torch.cuda.synchronize()
+        out = defaultdict(float)
+        for name in names:
+            for s, e, index in self.events.get(name, ()):
+                out[index] += s.elapsed_time(e)
         return out
 
 
@@ -302,7 +319,24 @@ class _Shade(torch.autograd.Function):
         return g, torch.mul(halves, 0.1).flatten(-2)
 
 
-def make_step(w, device):
+class Step:
+    """One forward+backward step of a workload on the GPU: ``render()`` runs the four ops and
+    returns the final image and its target; ``__call__`` adds the MSE loss and its backward
+    pass. ``leaves`` are the tensors that receive gradients."""
+
+    def __init__(self, render, leaves):
+        self.render, self.leaves = render, leaves
+
+    def __call__(self):
+        for x in self.leaves:
+            x.grad = None
+        image, target = self.render()
+        loss = _mse(image, target)
+        loss.backward()
+        return loss
+
+
+def make_step(w, device) -> Step:
     """One forward+backward step of workload ``w`` on the GPU (inputs copied to ``device``)."""
     # Range tables stay on the host, as nvdiffrast takes them (reading them needs no device
     # synchronisation, so the step can be captured in a HIP graph).
@@ -321,89 +355,94 @@ def make_step(w, device):
         pos, attr = leaf("pos"), leaf("attr")
         tri, target = t["tri"], t["target"]
 
-        def body():
+        def render():
             rast, _ = dr.rasterize(ctx, pos, tri, res, grad_db=False)
             col, _ = dr.interpolate(attr, rast, tri)
-            return _mse(dr.antialias(col, rast, pos, tri), target)
+            return dr.antialias(col, rast, pos, tri), target
     elif w.name == "textured":
         pos, tex = leaf("pos"), leaf("tex")
         tri, uv_attr, target = t["tri"], t["uv"], t["target"]
 
-        def body():
+        def render():
             rast, rast_db = dr.rasterize(ctx, pos, tri, res)
             uv, uv_da = dr.interpolate(uv_attr, rast, tri, rast_db, diff_attrs="all")
             mip = dr.texture_construct_mip(tex)
             col = dr.texture(tex, uv, uv_da, mip=mip, filter_mode="linear-mipmap-linear",
                              boundary_mode="wrap")
-            return _mse(dr.antialias(col, rast, pos, tri), target)
+            return dr.antialias(col, rast, pos, tri), target
     elif w.name == "large":
         pos, feat, tex = leaf("pos"), leaf("feat"), leaf("tex")
         tri, uv_attr, target = t["tri"], t["uv"], t["target"]
 
-        def body():
+        def render():
             rast, rast_db = dr.rasterize(ctx, pos, tri, res)
             f, _ = dr.interpolate(feat, rast, tri)
             st, st_da = dr.interpolate(uv_attr, rast, tri, rast_db, diff_attrs="all")
             col = dr.texture(tex, st, st_da, filter_mode="linear-mipmap-linear",
                              boundary_mode="wrap")
             shaded = _Shade.apply(col, f)  # col + 0.1 * (f[..., :4] + f[..., 4:])
-            return _mse(dr.antialias(shaded, rast, pos, tri), target)
+            return dr.antialias(shaded, rast, pos, tri), target
     elif w.name == "cubemap":
         pos, cube = leaf("pos"), leaf("cube")
         tri, normals, target = t["tri"], t["normals"], t["target"]
         view, view_da = t["view"], t["view_da"]
 
-        def body():
+        def render():
             rast, rast_db = dr.rasterize(ctx, pos, tri, res)
             n, n_da = dr.interpolate(normals, rast, tri, rast_db, diff_attrs="all")
             dirs, dirs_da = workloads.reflect(view, view_da, n, n_da)
             col = dr.texture(cube, dirs, dirs_da, filter_mode="linear-mipmap-linear",
                              boundary_mode="cube")
-            return _mse(dr.antialias(col, rast, pos, tri), target)
+            return dr.antialias(col, rast, pos, tri), target
     elif w.name == "instances":
         pos, color = leaf("pos"), leaf("color")
         tri, ranges = t["tri"], t["ranges"]
         target = torch.zeros_like(color)
 
-        def body():
+        def render():
             with dr.DepthPeeler(ctx, pos, tri, res, ranges=ranges) as peeler:
                 layers = [peeler.rasterize_next_layer()[0] for _ in range(4)]
-            return _mse(dr.antialias(color, layers[0], pos, tri), target)
+            return dr.antialias(color, layers[0], pos, tri), target
     else:
         raise ValueError(w.name)
-
-    def step():
-        for x in leaves:
-            x.grad = None
-        loss = body()
-        loss.backward()
-        return loss
-
-    return step
+    return Step(render, leaves)
 
 
-def first_image_ids(w, device):
-    """Triangle ids [1, H, W] (-1: none) of the first image (range mode: item 0's first layer),
-    from the GPU, for the CPU baseline's rest-of-pipeline leg."""
+def image_ids(w, device, images: int = 1):
+    """Triangle ids [images, H, W] (-1: none) of the first images (range mode: item 0's first
+    layer), from the GPU, for the CPU baseline's rest-of-pipeline leg."""
     t = w.tensors
     ctx = dr.RasterizeContext(device)
     with torch.no_grad():
         if w.name == "instances":
             rast, _ = dr.rasterize(ctx, t["pos"].to(device), t["tri"].to(device),
-                                   w.resolution, ranges=t["ranges"][:1])
+                                   w.resolution, ranges=t["ranges"][:images])
         else:
-            rast, _ = dr.rasterize(ctx, t["pos"][:1].to(device), t["tri"].to(device),
+            rast, _ = dr.rasterize(ctx, t["pos"][:images].to(device), t["tri"].to(device),
                                    w.resolution)
     return (rast[..., 3].long() - 1).cpu()
 
 
-def cpu_baseline(w, sample_tris: int, ids) -> dict:
-    """The oracle on the host: one image's brute-force visibility over a sample of its
-    triangles, and the rest of the pipeline forward and backward on that image in full (with
-    the true visibility), extrapolated linearly to all triangles, layers and images."""
+def host_threads() -> tuple[int, int]:
+    """(threads to use, cores this process may run on): the affinity count, limited by
+    OMP_NUM_THREADS where the environment sets it (a machine's share of cores for this job)."""
+    affinity = len(os.sched_getaffinity(0))
+    limit = os.environ.get("OMP_NUM_THREADS")
+    threads = min(affinity, int(limit)) if limit and limit.isdigit() and int(limit) > 0 \
+        else affinity
+    return threads, affinity
+
+
+def cpu_baseline(w, sample_tris: int, device, full_work: float) -> dict:
+    """The oracle on the host. Where the visibility's brute force (images x triangles x pixels
+    evaluations) is at most ``full_work``, the whole step on every image, median of up to three
+    individually timed runs; beyond it, one image's brute-force visibility over a sample of its
+    triangles and the rest of the pipeline forward and backward on that image in full (with the
+    true visibility), extrapolated linearly to all triangles, layers and images (the
+    reference's own skip rule, benchmarks/bench_pipeline.py:56, :73-75)."""
     from oracle import reference as R
 
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    threads, affinity = host_threads()
     torch.set_num_threads(threads)
     t = w.tensors
     (H, W), B = w.resolution, w.batch
@@ -412,67 +451,86 @@ def cpu_baseline(w, sample_tris: int, ids) -> dict:
     if w.name == "instances":
         start, count = (int(v) for v in t["ranges"][0])
         own = tri[start:start + count]
-        pos1 = t["pos"][None]
         layers = 4
     else:
         own = tri
-        pos1 = t["pos"][:1].clone()
     T = own.shape[0]
-    sample = min(sample_tris, T)
-    sub = own[torch.randperm(T, generator=torch.Generator().manual_seed(0))[:sample]]
-    px, py = R.pixel_centres(H, W, pos1)
-    start_s = time.perf_counter()
-    with torch.no_grad():
-        R.visible_triangles(pos1, sub, px, py)
-    vis_s = time.perf_counter() - start_s
+    full = w.name != "instances" and B * T * H * W <= full_work
+    images = B if full else 1
+    ids = image_ids(w, device, images)
+    pos_n = t["pos"][None] if w.name == "instances" else t["pos"][:images].clone()
+    sample = T if full else min(sample_tris, T)
+    keep = torch.randperm(T, generator=torch.Generator().manual_seed(0))[:sample]
+    sub = own if full else own[keep]
+    px, py = R.pixel_centres(H, W, pos_n)
 
-    p = pos1.clone().requires_grad_(True)
-    start_s = time.perf_counter()
-    if w.name == "sphere":
-        attr = t["attr"].clone().requires_grad_(True)
-        rast, _ = R.rasterize_from_ids(p, tri, ids, False)
-        col, _ = R.interpolate(attr, rast, tri, None, [])
-        _mse(R.antialias(col, rast, p, tri), t["target"][:1]).backward()
-    elif w.name == "textured":
-        tex = t["tex"].clone().requires_grad_(True)
-        rast, rast_db = R.rasterize_from_ids(p, tri, ids, True)
-        uv, uv_da = R.interpolate(t["uv"], rast, tri, rast_db, [0, 1])
-        col = R.texture(tex, uv, uv_da, "linear-mipmap-linear", "wrap", None)
-        _mse(R.antialias(col, rast, p, tri), t["target"][:1]).backward()
-    elif w.name == "large":
-        feat = t["feat"].clone().requires_grad_(True)
-        tex = t["tex"].clone().requires_grad_(True)
-        rast, rast_db = R.rasterize_from_ids(p, tri, ids, True)
-        f, _ = R.interpolate(feat, rast, tri, None, [])
-        st, st_da = R.interpolate(t["uv"], rast, tri, rast_db, [0, 1])
-        col = R.texture(tex, st, st_da, "linear-mipmap-linear", "wrap", None)
-        shaded = col + 0.1 * (f[..., 0:4] + f[..., 4:8])
-        _mse(R.antialias(shaded, rast, p, tri), t["target"][:1]).backward()
-    elif w.name == "cubemap":
-        cube = t["cube"].clone().requires_grad_(True)
-        rast, rast_db = R.rasterize_from_ids(p, tri, ids, True)
-        n, n_da = R.interpolate(t["normals"], rast, tri, rast_db, [0, 1, 2])
-        dirs, dirs_da = workloads.reflect(t["view"][:1], t["view_da"][:1], n, n_da)
-        col = R.texture(cube, dirs, dirs_da, "linear-mipmap-linear", "cube", None)
-        _mse(R.antialias(col, rast, p, tri), t["target"][:1]).backward()
-    elif w.name == "instances":
-        color = t["color"][:1].clone().requires_grad_(True)
-        rast, _ = R.rasterize_from_ids(p, tri, ids, False)
-        _mse(R.antialias(color, rast, p, tri), torch.zeros_like(color)).backward()
-    rest_s = time.perf_counter() - start_s
-    total_ms = B * (layers * vis_s * T / sample + rest_s) * 1e3
+    def rest(p):
+        if w.name == "sphere":
+            attr = t["attr"].clone().requires_grad_(True)
+            rast, _ = R.rasterize_from_ids(p, tri, ids, False)
+            col, _ = R.interpolate(attr, rast, tri, None, [])
+            _mse(R.antialias(col, rast, p, tri), t["target"][:images]).backward()
+        elif w.name == "textured":
+            tex = t["tex"].clone().requires_grad_(True)
+            rast, rast_db = R.rasterize_from_ids(p, tri, ids, True)
+            uv, uv_da = R.interpolate(t["uv"], rast, tri, rast_db, [0, 1])
+            col = R.texture(tex, uv, uv_da, "linear-mipmap-linear", "wrap", None)
+            _mse(R.antialias(col, rast, p, tri), t["target"][:images]).backward()
+        elif w.name == "large":
+            feat = t["feat"].clone().requires_grad_(True)
+            tex = t["tex"].clone().requires_grad_(True)
+            rast, rast_db = R.rasterize_from_ids(p, tri, ids, True)
+            f, _ = R.interpolate(feat, rast, tri, None, [])
+            st, st_da = R.interpolate(t["uv"], rast, tri, rast_db, [0, 1])
+            col = R.texture(tex, st, st_da, "linear-mipmap-linear", "wrap", None)
+            shaded = col + 0.1 * (f[..., 0:4] + f[..., 4:8])
+            _mse(R.antialias(shaded, rast, p, tri), t["target"][:images]).backward()
+        elif w.name == "cubemap":
+            cube = t["cube"].clone().requires_grad_(True)
+            rast, rast_db = R.rasterize_from_ids(p, tri, ids, True)
+            n, n_da = R.interpolate(t["normals"], rast, tri, rast_db, [0, 1, 2])
+            dirs, dirs_da = workloads.reflect(t["view"][:images], t["view_da"][:images], n, n_da)
+            col = R.texture(cube, dirs, dirs_da, "linear-mipmap-linear", "cube", None)
+            _mse(R.antialias(col, rast, p, tri), t["target"][:images]).backward()
+        elif w.name == "instances":
+            color = t["color"][:1].clone().requires_grad_(True)
+            rast, _ = R.rasterize_from_ids(p, tri, ids, False)
+            _mse(R.antialias(color, rast, p, tri), torch.zeros_like(color)).backward()
+
+    runs = []
+    while True:
+        start_s = time.perf_counter()
+        with torch.no_grad():
+            R.visible_triangles(pos_n, sub, px, py)
+        vis_s = time.perf_counter() - start_s
+        start_s = time.perf_counter()
+        rest(pos_n.clone().requires_grad_(True))
+        rest_s = time.perf_counter() - start_s
+        runs.append((vis_s + rest_s, vis_s, rest_s))
+        if not full or len(runs) == 3 or sum(r[0] for r in runs) > 20.0:
+            break
+    total_s, vis_s, rest_s = sorted(runs)[len(runs) // 2]
     what = "item" if w.name == "instances" else "view"
+    if full:
+        total_ms = total_s * 1e3
+        sample_text = (f"the whole step on all {B} {what}s at {H}x{W}: reference brute-force "
+                       f"visibility over all {T} triangles ({vis_s:.1f} s) and the rest of the "
+                       f"pipeline fwd+bwd ({rest_s:.1f} s); median of {len(runs)} run(s)")
+    else:
+        total_ms = B * (layers * vis_s * T / sample + rest_s) * 1e3
+        sample_text = (f"one {what} of {B} at {H}x{W}: reference brute-force visibility over "
+                       f"{sample} of its {T} triangles ({vis_s:.1f} s), x{layers} layer(s), and "
+                       f"the rest of the pipeline fwd+bwd in full ({rest_s:.1f} s), extrapolated "
+                       f"linearly to all triangles, layers and {what}s")
     return {
         "value": round(total_ms, 1),
         "unit": "ms",
         "cores": torch.get_num_threads(),
+        "affinity_cores": affinity,
         "cpu_model": cpu_model(),
         "kind": "port",
-        "sample": (f"one {what} of {B} at {H}x{W}: reference brute-force visibility over "
-                   f"{sample} of its {T} triangles ({vis_s:.1f} s), x{layers} layer(s), and the "
-                   f"rest of the pipeline fwd+bwd in full ({rest_s:.1f} s), extrapolated "
-                   f"linearly to all triangles, layers and {what}s"),
-        "extrapolated": sample < T or B > 1,
+        "sample": sample_text,
+        "extrapolated": not full,
     }
 
 
@@ -571,60 +629,212 @@ def dominant_entry(per_kernel: dict) -> str:
 
 
 def cpu_model() -> str:
+    """The host processor as /proc/cpuinfo names it, with its family, model, clock and the
+    logical CPUs the kernel lists."""
+    fields, logical = {}, 0
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, value = line.partition(":")
+            key = key.strip()
+            if key == "processor":
+                logical += 1
+            elif key in ("model name", "cpu family", "model", "cpu MHz") and key not in fields:
+                fields[key] = value.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    return (f"{fields.get('model name', 'unknown')} (family {fields.get('cpu family', '?')}, "
+            f"model {fields.get('model', '?')}, {fields.get('cpu MHz', '?')} MHz, "
+            f"{logical} logical CPUs listed)")
 
 
-def graph_step_ms(step, steps: int) -> float | None:
-    """ms per step when one step, captured in a HIP graph (torch.cuda.graph), is replayed
-    `steps` times back to back: the same kernels with no host work between them. None when the
-    step cannot be captured (the reason goes to stderr)."""
+def _loss_of(diff):
+    """The MSE from the difference image, as _MSE computes it."""
+    flat = diff.view(-1)
+    return torch.linalg.vector_norm(flat).square().div_(flat.numel())
+
+
+def _graph_nodes(graph, path: Path) -> dict | None:
+    """Kernel and memset nodes of a captured graph, from its DOT dump (None where the runtime
+    does not dump graphs)."""
+    try:
+        graph.debug_dump(str(path))
+        text = path.read_text().lower()
+    except (RuntimeError, OSError) as error:
+        print(f"graph dump unavailable: {error}", file=sys.stderr)
+        return None
+    finally:
+        if path.exists():
+            path.unlink()
+    return {"kernel": text.count("kernel_node") or text.count("kernel"),
+            "memset": text.count("memset")}
+
+
+def graph_step(step: Step, steps: int, repeats: int) -> dict | None:
+    """A step captured once in a HIP graph (torch.cuda.graph) and replayed: the render and its
+    backward pass, seeded with the MSE's gradient 2 (image - target) / n, are captured; the
+    loss itself -- a multi-workgroup reduction, whose semaphores PyTorch clears with a memory
+    fill that must not be replayed from a graph -- runs eagerly after each replay, so a step is
+    one replay plus one reduction. Before timing, one replay's gradients and loss are compared
+    with an eager step's. Returns the timing (``steps`` back to back, and the median, p10 and
+    p90 of ``repeats`` individually synchronised ones), the check and the graph's node counts;
+    None when the step cannot be captured (the reason goes to stderr)."""
+
+    def captured():
+        for x in step.leaves:
+            x.grad = None
+        image, target = step.render()
+        diff = torch.sub(image, target)
+        image.backward(torch.mul(diff, 2.0 / diff.numel()))
+        return diff
+
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     try:
         with torch.cuda.stream(side):  # capture wants its allocations warmed on a side stream
             for _ in range(2):
-                step()
+                captured()
         torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
+        graph.enable_debug_mode()
         with torch.cuda.graph(graph):
-            step()
+            diff = captured()
+        grads = [x.grad for x in step.leaves]
     except RuntimeError as error:
         print(f"graph capture failed, eager timing only: {error}", file=sys.stderr)
         torch.cuda.synchronize()
         return None
+    nodes = _graph_nodes(graph, ROOT / "gpurun_out" / f"graph.{os.getpid()}.dot")
+
+    # One replay against one eager step of the same inputs.
     graph.replay()
+    replay_loss = _loss_of(diff).item()
+    replayed = [g.clone() for g in grads]
+    eager_loss = step().item()
+    torch.cuda.synchronize()
+    worst = 0.0
+    for ours, leaf in zip(replayed, step.leaves):
+        scale = leaf.grad.abs().max().item()
+        worst = max(worst, (ours - leaf.grad).abs().max().item() / max(scale, 1e-30))
+    loss_diff = abs(replay_loss - eager_loss) / max(abs(eager_loss), 1e-30)
+    check = {"gradients_max_rel_diff": worst, "loss_rel_diff": loss_diff,
+             "passed": worst < 1e-5 and loss_diff < 1e-5}
+
+    def one():
+        graph.replay()
+        return _loss_of(diff)
+
+    one()
     torch.cuda.synchronize()
     start = time.perf_counter()
     for _ in range(steps):
-        graph.replay()
+        one()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - start) * 1e3 / steps
+    synced = synced_steps(one, repeats)
     del graph
     torch.cuda.synchronize()
-    return ms
+    return {"ms_per_step": ms, "synced": synced, "check": check, "nodes": nodes}
+
+
+def _percentile(values: list[float], q: float) -> float:
+    """The q-quantile of values, linear between order statistics."""
+    v = sorted(values)
+    k = (len(v) - 1) * q
+    lo = int(k)
+    hi = min(lo + 1, len(v) - 1)
+    return v[lo] + (v[hi] - v[lo]) * (k - lo)
+
+
+def synced_steps(fn, repeats: int) -> dict:
+    """Median, p10 and p90 of ``repeats`` individually synchronised calls of ``fn`` (ms), the
+    rule of the reference's benchmarks (benchmarks/bench_rasterize.py:56-72)."""
+    times = []
+    for _ in range(repeats):
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - start) * 1e3)
+    return {"n": repeats, "median_ms": round(_percentile(times, 0.5), 4),
+            "p10_ms": round(_percentile(times, 0.1), 4),
+            "p90_ms": round(_percentile(times, 0.9), 4)}
+
+
+# Entry points whose results are cached per mesh (tri): they run in the first step only.
+ONCE_PER_MESH = ("dr_raster_order", "dr_edge_neighbours")
+
+# Single-kernel entry points of the backward scatters, by kernel (their live times rate the
+# atomic counts of the committed counter summary).
+SCATTER_ENTRY = {k: n for n, k in SINGLE_KERNEL.items() if n.endswith("_backward")}
+
+
+def profiled_atomics(workload: str, live_ms: dict) -> dict | None:
+    """Device atomic requests per launch of the backward scatters and the visibility's setup
+    pass, from the workload's committed counter summary (lines ``<kernel>.atomic_requests: N``,
+    ``<kernel>.atomic_beyond_l2: N`` and ``<kernel>.mean_us: D``, the kernel-trace mean of the
+    same profiling session), rated per second over the live mean launch of the kernel's entry
+    point where it launches that kernel alone, else over the summary's mean."""
+    path = ROOT / "profiles" / f"atomics.{workload}.pmc.txt"
+    if not path.exists():
+        return None
+    f = _profile_fields(path)
+    out = {}
+    for key in f:
+        if not key.endswith(".atomic_requests"):
+            continue
+        kernel = key[:-len(".atomic_requests")]
+        entry = SCATTER_ENTRY.get(kernel)
+        ms = live_ms.get(entry) if entry else None
+        source = "live"
+        if ms is None:
+            ms = f.get(f"{kernel}.mean_us", 0.0) * 1e-3
+            source = "profile"
+        if not ms:
+            continue
+        requests = f[key]
+        out[kernel] = {"requests_per_launch": int(requests),
+                       "beyond_l2_per_launch": int(f.get(f"{kernel}.atomic_beyond_l2", -1)),
+                       "G_requests_per_s": round(requests / (ms * 1e-3) / 1e9, 2),
+                       "mean_launch_ms": round(ms, 4), "duration_from": source}
+    return {"kernels": out, "source": str(path.relative_to(ROOT))} if out else None
 
 
 def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int,
-        graph: bool = False) -> dict:
-    """Warm-up steps (timed per entry point after the first, to find the dominant kernel), then
-    exactly `steps` timed steps in which only the dominant entry point carries HIP events (the
-    roofline's live launch time; events around every call would add ~0.13 ms per step), then a
-    few more steps with every entry point timed, for the per-kernel and per-op tables. With
-    `graph`, `value` is instead the time per step of a captured step replayed `steps` times
-    (the eager time stays in the line, and the kernel times come from the eager steps)."""
+        graph: bool = False, repeats: int = 20, cpu_full_work: float = 2.2e10) -> dict:
+    """The first two warm-up steps timed one by one (the first call of the process and of the
+    mesh: library code loaded, processing order and edge adjacency computed, the visibility's
+    list sizes learnt with one host wait), the other warm-up steps timed per entry point to
+    find the dominant kernel, then exactly `steps` timed steps back to back in which only the
+    dominant entry point carries HIP events (the roofline's live launch time; events around
+    every call would add ~0.13 ms per step), then `repeats` individually synchronised steps
+    (median, p10, p90), then 15 steps with every entry point timed for the per-kernel and
+    per-op tables. With `graph`, `value` is instead the time per step of a captured step
+    replayed `steps` times (the eager time stays in the line)."""
     w = workloads.build(name)
     step = make_step(w, device)
     model = BytesModel(w)
     timer = KernelTimer(model)
     timer.install()
+    first_call = None
     for i in range(warmup):
         timer.active = i > 0 or warmup == 1
+        if i < 2 and warmup >= 2:
+            timer.active = i == 0
+            torch.cuda.synchronize()
+            start = time.perf_counter()
+            step()
+            torch.cuda.synchronize()
+            wall = (time.perf_counter() - start) * 1e3
+            if i == 0:
+                once = timer.summary()
+                timer.reset()
+                first_call = {"first_step_ms": round(wall, 3), "once_per_mesh_ms": {
+                    n: round(once[n][0], 4) for n in ONCE_PER_MESH if n in once}}
+            else:
+                first_call["second_step_ms"] = round(wall, 3)
+            continue
+        timer.step_index += 1
         step()
     timer.active = False
     torch.cuda.synchronize()
@@ -648,12 +858,15 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int,
     dom_ms = dom_total / dom_count
     dom_bytes = timer.bytes[dominant] / dom_count
 
+    synced = synced_steps(step, repeats)
+
     # The per-kernel and per-op tables, from their own steps after the timed ones.
-    table_steps = min(steps, 5)
+    table_steps = 15
     timer.reset()
     timer.only = None
     timer.active = True
-    for _ in range(table_steps):
+    for i in range(table_steps):
+        timer.step_index = i
         step()
     torch.cuda.synchronize()
     timer.active = False
@@ -661,6 +874,7 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int,
     per_kernel = timer.summary()
     kernels = {}
     op_ms, op_bytes = defaultdict(float), defaultdict(float)
+    op_entries = defaultdict(list)
     for kname, (total_ms, count) in per_kernel.items():
         mean_ms = total_ms / count
         entry = {"ms_per_step": round(total_ms / table_steps, 4), "launches_per_step":
@@ -674,6 +888,7 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int,
         if op is not None:
             op_ms[op] += total_ms / table_steps
             op_bytes[op] += timer.op_bytes[kname] / table_steps
+            op_entries[op].append(kname)
     # The tile pass carries the whole visibility's unique bytes: its rate is quoted over the
     # four visibility entry points together (in range mode the setup pass does most of the work
     # and the tile pass alone would read above the HBM peak).
@@ -690,24 +905,27 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int,
         if op not in op_ms:
             continue
         floor_ms = op_bytes[op] / HBM_PEAK * 1e3
-        ops[op] = {"ms": round(op_ms[op], 4), "bytes": int(op_bytes[op]),
+        per_step = list(timer.per_step(op_entries[op]).values())
+        ops[op] = {"ms": round(op_ms[op], 4), "p10_ms": round(_percentile(per_step, 0.1), 4),
+                   "p90_ms": round(_percentile(per_step, 0.9), 4), "bytes": int(op_bytes[op]),
                    "roofline_ms": round(floor_ms, 4), "frac": round(floor_ms / op_ms[op], 4)}
     step_bytes = sum(op_bytes.values())
     step_floor_ms = step_bytes / HBM_PEAK * 1e3
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     traffic = profiled_traffic(SINGLE_KERNEL[dominant], name)
+    atomics = profiled_atomics(name, {k: v["mean_launch_ms"] for k, v in kernels.items()})
 
     eager_ms = ms_per_step
-    replay_ms = graph_step_ms(step, steps) if graph else None
-    if replay_ms is not None:
-        ms_per_step = replay_ms
+    replay = graph_step(step, steps, repeats) if graph else None
+    if replay is not None:
+        ms_per_step = replay["ms_per_step"]
 
     baseline = None
     if cpu:
-        baseline = cpu_baseline(w, sample_tris, first_image_ids(w, device))
+        baseline = cpu_baseline(w, sample_tris, device, cpu_full_work)
 
     tris = w.tensors["tri"].shape[0]
-    return {
+    result = {
         "metric": METRIC if name == "large" else "ms per fwd+bwd render (4-op pipeline)",
         "value": round(ms_per_step, 3),
         "unit": "ms",
@@ -715,8 +933,11 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int,
         "steps": steps,
         "warmup": warmup,
         "ms_per_step": round(ms_per_step, 3),
-        "timing": "HIP graph replay" if replay_ms is not None else "eager",
+        "timing": "HIP graph replay" if replay is not None else "eager",
         "eager_ms_per_step": round(eager_ms, 3),
+        # The reference's rule: median (and p10, p90) of individually synchronised steps.
+        "synced_steps": synced,
+        "first_call": first_call,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -749,10 +970,16 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int,
             "step": {"bytes": int(step_bytes), "roofline_ms": round(step_floor_ms, 4),
                      "frac": round(step_floor_ms / ms_per_step, 4),
                      "ops_ms": round(sum(op_ms.values()), 4)},
+            # The backward scatters' device atomics (counter summary, live launch times).
+            "atomics": atomics,
         },
         "cpu_baseline": baseline,
         "kernels": kernels,
     }
+    if replay is not None:
+        result["graph"] = {"synced_steps": replay["synced"], "check": replay["check"],
+                           "nodes": replay["nodes"]}
+    return result
 
 
 def main():
@@ -765,8 +992,13 @@ def main():
                         help="one JSON line per workload (the headline first)")
     parser.add_argument("--cpu-sample-tris", type=int, default=4096)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-full-work", type=float, default=2.2e10,
+                        help="CPU baseline measured in full up to this many coverage "
+                             "evaluations (images x triangles x pixels), sampled beyond")
     parser.add_argument("--graph", action="store_true",
                         help="time a captured step replayed as a HIP graph (eager time kept)")
+    parser.add_argument("--repeats", type=int, default=20,
+                        help="individually synchronised steps for the median, p10 and p90")
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="run one copy of this size first (counter calibration)")
     args = parser.parse_args()
@@ -783,7 +1015,7 @@ def main():
         else [args.workload]
     for name in names:
         result = run(name, args.steps, args.warmup, device, not args.no_cpu_baseline,
-                     args.cpu_sample_tris, args.graph)
+                     args.cpu_sample_tris, args.graph, args.repeats, args.cpu_full_work)
         print(json.dumps(result), flush=True)
 
 

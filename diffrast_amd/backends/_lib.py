@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent.parent / "libdiffrast_hip.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 MAX_LEVELS = 32
 
 c_float_p = ctypes.POINTER(ctypes.c_float)

@@ -278,7 +278,7 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
         arrived.synchronize()
         found = [v & 0xFFFFFFFF for v in host.tolist()]
         counts = (ctypes.c_uint32 * 4)(found[0], found[1], _tile_grid(geo, found[2]), found[3])
-        entries = torch.empty(max(found[1], 1), dtype=torch.int32, device=device)
+        entries = torch.empty(max(found[1], 1), dtype=torch.int64, device=device)
         call("dr_raster_visibility_bin", ref(geo.struct), ptr(workspace), size.value,
              ptr(entries), counts, stream)
         call("dr_raster_visibility_tiles", ref(geo.struct), ptr(prev), ptr(keys),
@@ -293,7 +293,7 @@ def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
                 sizes.refresh()
             capacity = _entry_capacity(sizes.entries)
             groups = min(sizes.groups + sizes.groups // 8 + 8, 0xffffffff) if sizes.groups else 0
-    entries = torch.empty(capacity, dtype=torch.int32, device=device)
+    entries = torch.empty(capacity, dtype=torch.int64, device=device)
     # The four passes of dr_raster_visibility, queued one call each (so that each can be timed
     # on its own): start, bin and tiles into the buffer, overflow when it was too small.
     spec = (ctypes.c_uint32 * 4)(0, capacity, _tile_grid(geo, groups), 0)

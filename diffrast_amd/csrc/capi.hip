@@ -10,12 +10,12 @@ extern "C" const char* dr_error_string(int code) {
     case DR_ERR_SCRATCH:
       return "the call needs more memory than the 64 MiB static scratch buffer of the "
              "allocation-free entry point holds (its visibility workspace, "
-             "dr_raster_workspace_size, must be at most 64 MiB - 16 KiB)";
+             "dr_raster_workspace_size, must be at most 64 MiB - 32 KiB)";
     default: return "unknown error";
   }
 }
 
-extern "C" int dr_abi_version(void) { return 14; }
+extern "C" int dr_abi_version(void) { return 15; }
 
 extern "C" int dr_struct_size(int which) {
   switch (which) {

@@ -66,6 +66,8 @@ struct Workspace {
   float4* records;           // binned triangles, kRecord float4 each: the three clip-space
                              // vertices, then the bits of (image, row, tx0 | tx1 << 16,
                              // ty0 | ty1 << 16)
+  float* record_bound;       // per record slot: depth_lower_bound of its triangle, which the bin
+                             // pass copies into the tile entries
   // Tile lists: list tile * slabs + slab holds the binned triangles of that tile whose
   // nearest depth falls in depth slab `slab` of their image, so a tile's entries are one range
   // that runs near to far.
@@ -160,6 +162,7 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
     w.bound_parts = (uint32_t*)take(sizeof(uint32_t) * 6 * (size_t)blocks_for(g.num_tri, 256));
   }
   w.records = (float4*)take(sizeof(float4) * kRecord * 256 * (size_t)w.record_blocks);
+  w.record_bound = (float*)take(sizeof(float) * 256 * (size_t)w.record_blocks);
   w.bytes = off;
   if (w.ordered && g.order != nullptr) w.order = (int4*)g.order;
   return w;
@@ -270,6 +273,19 @@ __device__ __forceinline__ void vertex_depths(const Tri& T, float (&d)[3]) {
     d[k] = T.z[k] * r;
     if (r == 0.0f || !isfinite(d[k])) d[k] = T.z[k] / T.w[k];
   }
+}
+
+// A lower bound of the triangle's depth at any pixel it covers (-inf when it crosses the camera
+// plane). The depth computed at a covered pixel is a convex combination of the vertex depths
+// z_k / w_k up to a few float32 roundings (~6 * 2^-24 of the largest |z_k / w_k|); the margin
+// is 1e-5 of it. approx_rcp's error (2^-22 relative) is far inside the margin.
+__device__ __forceinline__ float depth_lower_bound(const Tri& T) {
+  if (!(T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f)) return -__int_as_float(0x7f800000);
+  float d[3];
+  vertex_depths(T, d);
+  const float nearest = fminf(fminf(d[0], d[1]), d[2]);
+  const float scale = fmaxf(fmaxf(fabsf(d[0]), fabsf(d[1])), fabsf(d[2]));
+  return nearest - 1e-5f * scale;
 }
 
 // Box [x_lo, x_hi] x [y_lo, y_hi] of the pixel centres a triangle may cover; empty (lo > hi)
@@ -665,17 +681,33 @@ __global__ __launch_bounds__(kRangeParts) void raster_depth_range_merge(Workspac
 
 // Depth slab of a binned triangle: its nearest vertex depth's place in the image's depth span
 // (order-preserving bits of its nearest and farthest depth, from ws.depth_range). Triangles that
-// cross the camera plane go first (slab 0).
+// cross the camera plane, or have a vertex depth beyond [-1, 1], go first (slab 0): in slab
+// s >= 1 every triangle's depth_lower_bound is at least slab_floor(span, s, slabs).
 __device__ __forceinline__ int depth_slab(uint2 span, const Tri& T, int slabs) {
   if (slabs == 1 || !(T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f)) return 0;
   float d[3];
   vertex_depths(T, d);
+  if (!(fmaxf(fmaxf(fabsf(d[0]), fabsf(d[1])), fabsf(d[2])) <= 1.0f)) return 0;
   const float nearest = fminf(fminf(d[0], d[1]), d[2]);
   const float lo = from_ordered_bits(span.x);
   const float hi = from_ordered_bits(span.y);
   const float f = (nearest - lo) / (hi - lo) * (float)slabs;
   if (!(hi > lo) || !isfinite(f)) return 0;
   return min(max((int)f, 0), slabs - 1);
+}
+
+// A lower bound of depth_lower_bound over the triangles of slab s >= 1 (depth_slab). Such a
+// triangle has all w > 0, every vertex depth within [-1, 1] and f = fl(fl(fl(nearest - lo) /
+// fl(hi - lo)) * slabs) >= s, so nearest >= lo + s (hi - lo) / slabs * (1 - 3 * 2^-24) (three
+// roundings of relative error at most 2^-24; the product by slabs, a power of two, is exact);
+// its bound fl(nearest - fl(1e-5 * scale)) with scale <= 1 is then above nearest - 1.0001e-5 -
+// 2^-23. Evaluated in double (exact for these float operands up to 2^-50 relative) with that
+// slack widened to 2e-5 + 2^-20.
+__device__ __forceinline__ double slab_floor(uint2 span, int s, int slabs) {
+  const double lo = (double)from_ordered_bits(span.x);
+  const double hi = (double)from_ordered_bits(span.y);
+  return lo + (double)s * (hi - lo) / (double)slabs * (1.0 - 4.0 / 16777216.0) - 2e-5 -
+         1.0 / 1048576.0;
 }
 
 // ---- kernels: setup, scan, bin, tiles -----------------------------------------------------
@@ -811,6 +843,7 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
       float4* out = ws.records + (size_t)rec * kRecord;
 #pragma unroll
       for (int k = 0; k < 3; ++k) out[k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
+      ws.record_bound[rec] = depth_lower_bound(T);
       out[3] = make_float4(__int_as_float(b), __int_as_float(t | (slab << 24)),
                            __uint_as_float((uint32_t)tx0 | ((uint32_t)tx1 << 16)),
                            __uint_as_float((uint32_t)ty0 | ((uint32_t)ty1 << 16)));
@@ -928,7 +961,7 @@ __global__ __launch_bounds__(256) void raster_scan_apply(const uint32_t* counts,
 
 // Fills the per-tile lists: the workgroup counts its records per tile in LDS, reserves its
 // share of each tile's list with one global atomic, then writes the entries.
-__global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint32_t* entries,
+__global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint2* entries,
                                                          uint32_t capacity) {
   // Entries beyond the buffer's capacity: the pass is left to a later launch with a larger
   // buffer (the cursors stay untouched, so that launch places every entry).
@@ -939,8 +972,11 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint32_t*
   // The records of setup workgroup blockIdx.x.
   const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
   int tx0 = 0, tx1 = -1, ty0 = 0, ty1 = -1;
-  uint32_t image_tiles = 0, slab = 0;
+  uint32_t image_tiles = 0, slab = 0, bound_bits = 0u;
   if (threadIdx.x < ws.block_records[blockIdx.x]) {
+    // Each entry carries the triangle's depth bound, so that the tile pass can skip a
+    // triangle behind every key of its tile without reading its record.
+    bound_bits = __float_as_uint(ws.record_bound[r]);
     const float4 rec = ws.records[(size_t)r * kRecord + 3];
     const uint32_t rx = __float_as_uint(rec.z), ry = __float_as_uint(rec.w);
     tx0 = (int)(rx & 0xffffu);
@@ -979,7 +1015,7 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint32_t*
       const int slot = table.find(list);
       const uint32_t at = slot >= 0 ? table.base[slot] + atomicAdd(table.count + slot, 1u)
                                     : atomicAdd(ws.list_cursor + list, 1u);
-      entries[at] = r;
+      entries[at] = make_uint2(r, bound_bits);
     }
 }
 
@@ -1114,7 +1150,7 @@ template <bool kLoop>
 __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
                                                           const uint64_t* prev, uint64_t* keys,
                                                           Workspace ws,
-                                                          const uint32_t* entries,
+                                                          const uint2* entries,
                                                           uint32_t capacity) {
   // Per staged triangle: the three vertices, (reach_x, reach_y) and its row of tri.
   __shared__ float4 s_tri[kChunk][3];
@@ -1157,8 +1193,8 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     continue;
   }
 
-  // This thread's entry of the next chunk, read ahead.
-  uint32_t next = begin + threadIdx.x < end ? entries[begin + threadIdx.x] : 0u;
+  // This thread's entry of the next chunk, read ahead: (record, depth bound).
+  uint2 next = begin + threadIdx.x < end ? entries[begin + threadIdx.x] : make_uint2(0u, 0u);
 
   const int per_image = ws.tiles_x * ws.tiles_y;
   const int b = (int)(tile / per_image);
@@ -1180,13 +1216,30 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   const int lane = lane_id();
   const int wave = threadIdx.x / DR_WAVE;
 
-  for (uint32_t at = begin; at < end; at += kChunk) {
+  // The depth of the tile's farthest key when the previous chunk began (+inf while a pixel is
+  // empty). Keys only get nearer, so an entry whose bound lies beyond it lies beyond the
+  // farthest key of its own chunk too: it is dropped before its record is read.
+  float stale_far = __int_as_float(0x7f800000);
+  // Lane s (1 <= s < slabs) of each wave holds the floor of slab s's depth bounds: once the
+  // tile's farthest key lies before it, slab s and every farther one are behind every key of
+  // the tile, and the walk ends at the slab's first entry.
+  const bool by_slab = ws.slabs > 1 && ws.slabs <= DR_WAVE;
+  double floor_s = 0.0;
+  if (by_slab && lane >= 1 && lane < ws.slabs) {
+    const uint2 span = reinterpret_cast<const uint2*>(ws.depth_range)[ws.depth_ranges > 1 ? b : 0];
+    floor_s = slab_floor(span, lane, ws.slabs);
+  }
+  uint32_t stop = end;
+  for (uint32_t at = begin; at < stop; at += kChunk) {
+    const uint32_t end = stop;
     const int n = (int)min(end - at, (uint32_t)kChunk);
-    const bool staged = (int)threadIdx.x < n;
+    // A lower bound of the entry's triangle's depth at any pixel it covers.
+    const float bound = __uint_as_float(next.y);
+    const bool staged = (int)threadIdx.x < n && !(bound > stale_far);
     Tri T = {};
     uint32_t tri_row = 0u;
     if (staged) {
-      const float4* rec = ws.records + (size_t)next * kRecord;
+      const float4* rec = ws.records + (size_t)next.x * kRecord;
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
         const float4 v = rec[k];
@@ -1200,11 +1253,9 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     if (at + kChunk + threadIdx.x < end) next = entries[at + kChunk + threadIdx.x];
 
     // The farthest key of the tile so far (pixels outside the image count as nearest). A
-    // triangle whose nearest vertex lies beyond it, by more than the rounding of the depth,
-    // cannot win any pixel of the tile and is skipped; the same bound skips single pixels that
-    // already hold a nearer key. The depth computed at a covered pixel is a convex combination
-    // of the vertex depths z_k / w_k up to a few float32 roundings (~6 * 2^-24 of the largest
-    // |z_k / w_k|; the margin is 1e-5 of it), and equal depths are never skipped.
+    // triangle whose depth bound lies beyond it (depth_lower_bound: the nearest vertex depth
+    // less the rounding of the depth) cannot win any pixel of the tile and is skipped; the same
+    // bound skips single pixels that already hold a nearer key. Equal depths are never skipped.
     __syncthreads();  // the previous chunk's merges (and the set-up above) are done
     const uint64_t own_key = inside ? s_key[threadIdx.x] : 0ull;
     const uint64_t row_far = row_max_u64(own_key);  // a wave holds four rows of the tile
@@ -1216,6 +1267,15 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     for (int w = 0; w < 256 / DR_WAVE; ++w) far_key = s_far[w] > far_key ? s_far[w] : far_key;
     const bool cull = far_key != kEmptyKey;
     const float far_depth = key_depth(far_key);
+    stale_far = cull ? far_depth : __int_as_float(0x7f800000);
+    if (cull && by_slab) {
+      const uint64_t behind_slabs =
+          __ballot(lane >= 1 && lane < ws.slabs && floor_s > (double)far_depth);  // uniform
+      if (behind_slabs != 0) {
+        const int first = __ffsll((unsigned long long)behind_slabs) - 1;
+        stop = min(stop, ws.list_offsets[(size_t)tile * ws.slabs + first]);
+      }
+    }
 
     int items = 0;
     if (staged) {
@@ -1227,17 +1287,6 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
       candidate_box(g, T, x_lo, x_hi, y_lo, y_hi);
       const int bx0 = max(x_lo - tile_x0, 0), bx1 = min(x_hi - tile_x0, kTile - 1);
       const int by0 = max(y_lo - tile_y0, 0), by1 = min(y_hi - tile_y0, kTile - 1);
-      // A lower bound of the triangle's depth at any pixel it covers (-inf when it crosses the
-      // camera plane).
-      float bound = -__int_as_float(0x7f800000);
-      if (T.w[0] > 0.0f && T.w[1] > 0.0f && T.w[2] > 0.0f) {
-        // approx_rcp's error (2^-22 relative) is far inside the margin.
-        float d[3];
-        vertex_depths(T, d);
-        const float nearest = fminf(fminf(d[0], d[1]), d[2]);
-        const float scale = fmaxf(fmaxf(fabsf(d[0]), fabsf(d[1])), fabsf(d[2]));
-        bound = nearest - 1e-5f * scale;
-      }
       s_bound[threadIdx.x] = bound;
       s_reach[threadIdx.x] = make_float2(T.reach_x, T.reach_y);
       asm volatile("" : "+v"(tri_row));  // keeps the mask (and the wait for the load) here
@@ -1736,7 +1785,7 @@ constexpr int64_t kPlainTileGrid = 1 << 16;
 // of 8 and kept below 2^24, each taking every (grid / 8)-th busy tile of its XCD share. So a
 // grid sized before the busy tiles were known, or sized wrongly by a caller, loses no tile.
 static void launch_tile_pass(const DrRasterGeometry& g, const uint64_t* prev, uint64_t* keys,
-                             const Workspace& ws, const uint32_t* entries, uint32_t capacity,
+                             const Workspace& ws, const uint2* entries, uint32_t capacity,
                              uint32_t requested, hipStream_t s) {
   const int64_t bound = tile_grid_bound(ws);
   const int64_t limit = ((int64_t)1 << 24) - kXcdShares;
@@ -1760,7 +1809,7 @@ static int overflow_grid(const Workspace& ws) { return std::min(ws.record_blocks
 // for the host).
 static int queue_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys,
                             uint64_t* keys, void* workspace, size_t workspace_bytes,
-                            uint32_t* entries, uint32_t capacity, uint32_t tile_groups,
+                            uint2* entries, uint32_t capacity, uint32_t tile_groups,
                             uint32_t* host_counts, hipStream_t s) {
   const int status = queue_visibility_start(g, prev_keys, keys, workspace, workspace_bytes,
                                             host_counts, s);
@@ -1824,14 +1873,14 @@ extern "C" int dr_raster_visibility_static(const DrRasterGeometry* g,
                                            void* stream) {
   if (!valid_geometry(g)) return DR_ERR_ARGUMENT;
   const size_t workspace_bytes = layout(*g, nullptr).bytes;  // a multiple of 256
-  if (workspace_bytes + kScratchMinEntries * sizeof(uint32_t) > kScratchBytes)
+  if (workspace_bytes + kScratchMinEntries * sizeof(uint2) > kScratchBytes)
     return DR_ERR_SCRATCH;
   void* base = nullptr;
   const int status = scratch_of_current_device(&base);
   if (status != DR_OK) return status;
-  uint32_t* entries = (uint32_t*)((char*)base + workspace_bytes);
+  uint2* entries = (uint2*)((char*)base + workspace_bytes);
   const size_t capacity =
-      std::min<size_t>((kScratchBytes - workspace_bytes) / sizeof(uint32_t), 0xffffffffu);
+      std::min<size_t>((kScratchBytes - workspace_bytes) / sizeof(uint2), 0xffffffffu);
   // Everything the passes read is set up by raster_prepare at the start of the call (keys,
   // list counts, counters), so what the previous call left in the buffer does not matter.
   return queue_visibility(g, prev_keys, keys, base, workspace_bytes, entries,
@@ -1840,11 +1889,11 @@ extern "C" int dr_raster_visibility_static(const DrRasterGeometry* g,
 
 extern "C" int dr_raster_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                     uint64_t* keys, void* workspace, size_t workspace_bytes,
-                                    uint32_t* entries, uint32_t entry_capacity,
+                                    void* entries, uint32_t entry_capacity,
                                     uint32_t tile_groups, uint32_t* host_counts, void* stream) {
   if (!valid_geometry(g) || (entry_capacity > 0 && !entries)) return DR_ERR_ARGUMENT;
   if (host_counts) host_counts[0] = host_counts[1] = host_counts[2] = host_counts[3] = 0;
-  return queue_visibility(g, prev_keys, keys, workspace, workspace_bytes, entries,
+  return queue_visibility(g, prev_keys, keys, workspace, workspace_bytes, (uint2*)entries,
                           entry_capacity, tile_groups, host_counts, (hipStream_t)stream);
 }
 
@@ -1882,7 +1931,7 @@ extern "C" int dr_raster_visibility_begin(const DrRasterGeometry* g, const uint6
 }
 
 extern "C" int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspace,
-                                        size_t workspace_bytes, uint32_t* entries,
+                                        size_t workspace_bytes, void* entries,
                                         const uint32_t counts[4], void* stream) {
   if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
   // Nothing was binned without pixels or triangles (and the workspace was not prepared).
@@ -1891,20 +1940,21 @@ extern "C" int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspa
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
-  raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, entries, counts[1]);
+  raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, (uint2*)entries, counts[1]);
   return launch_status();
 }
 
 extern "C" int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                           uint64_t* keys, void* workspace,
-                                          size_t workspace_bytes, const uint32_t* entries,
+                                          size_t workspace_bytes, const void* entries,
                                           const uint32_t counts[4], void* stream) {
   if (!valid_geometry(g) || !counts) return DR_ERR_ARGUMENT;
   if (counts[1] == 0 || g->batch == 0 || g->num_instances == 0) return DR_OK;
   if (!entries || !keys) return DR_ERR_ARGUMENT;
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
-  launch_tile_pass(*g, prev_keys, keys, ws, entries, counts[1], counts[2], (hipStream_t)stream);
+  launch_tile_pass(*g, prev_keys, keys, ws, (const uint2*)entries, counts[1], counts[2],
+                   (hipStream_t)stream);
   return launch_status();
 }
 

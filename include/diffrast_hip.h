@@ -115,15 +115,17 @@ int dr_raster_visibility_start(const DrRasterGeometry* g, const uint64_t* prev_k
                                uint64_t* keys, void* workspace, size_t workspace_bytes,
                                uint32_t* host_counts, void* stream);
 
-/* Visibility, second part: fills the per-tile lists. entries holds counts[1] uint32: the
- * lists of all tiles, tile by tile, near to far. Nothing to do when counts[1] == 0. counts[1]
+/* Visibility, second part: fills the per-tile lists. entries holds counts[1] entries of 8
+ * bytes (8-byte aligned): the lists of all tiles, tile by tile, near to far; an entry is a
+ * binned triangle's record number (uint32) and a lower bound of its depth (float32), by which
+ * the tile pass skips triangles behind every key of a tile without reading their records. Nothing to do when counts[1] == 0. counts[1]
  * may also be a capacity larger than the lists: the kernel returns at once if they exceed it.
  * (The reference's pure-PyTorch visibility tests every triangle at every pixel,
  * reference.py:368-397; its Triton path bins triangles into tile chunks,
  * _triton_rasterize.py:371-424, and keeps the nearest per pixel in _tile_kernel,
  * _triton_rasterize.py:219-269.) */
 int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspace, size_t workspace_bytes,
-                             uint32_t* entries, const uint32_t counts[4], void* stream);
+                             void* entries, const uint32_t counts[4], void* stream);
 
 /* Visibility, third part: rasterizes the binned triangles tile by tile into keys, after
  * dr_raster_visibility_bin with the same entries and counts. Nothing to do when
@@ -135,7 +137,7 @@ int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspace, size_t 
  * smallest grid that gives each busy tile its own workgroup. counts[3] is not read. */
 int dr_raster_visibility_tiles(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                uint64_t* keys, void* workspace, size_t workspace_bytes,
-                               const uint32_t* entries, const uint32_t counts[4], void* stream);
+                               const void* entries, const uint32_t counts[4], void* stream);
 
 /* The overflow pass on its own, after dr_raster_visibility_bin and _tiles were queued with a
  * buffer of entry_capacity entries: when the lists turned out longer (the device knows; the
@@ -148,7 +150,7 @@ int dr_raster_visibility_overflow(const DrRasterGeometry* g, const uint64_t* pre
 
 /* The whole visibility in one call that never waits for the host: the work of
  * dr_raster_visibility_start, then the bin and tile passes with an entry buffer of
- * entry_capacity uint32 (entries may be NULL when it is 0) and a tile pass of tile_groups
+ * entry_capacity 8-byte entries (entries may be NULL when it is 0) and a tile pass of tile_groups
  * workgroups (as counts[2] above; 0: one per tile), then an overflow pass. If the tile lists
  * turn out longer than the buffer, the bin and tile passes return without work and the overflow
  * pass rasterizes the binned triangles straight into keys (64-bit atomic min per covered pixel:
@@ -160,7 +162,7 @@ int dr_raster_visibility_overflow(const DrRasterGeometry* g, const uint64_t* pre
  * src/diffrast/backends/triton.py:21-40, whose binning sizes its buffers on the host,
  * _triton_rasterize.py:387-424.) */
 int dr_raster_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys, uint64_t* keys,
-                         void* workspace, size_t workspace_bytes, uint32_t* entries,
+                         void* workspace, size_t workspace_bytes, void* entries,
                          uint32_t entry_capacity, uint32_t tile_groups, uint32_t* host_counts,
                          void* stream);
 
@@ -170,12 +172,13 @@ int dr_raster_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys, u
  * for callers that cannot allocate -- code under HIP graph capture, tight serving loops,
  * harnesses that forbid allocation. Limit: the visibility workspace of the geometry
  * (dr_raster_workspace_size) must leave room for 4096 tile entries, i.e. be at most
- * 64 MiB - 16 KiB (DR_ERR_SCRATCH otherwise: about 690K triangle instances at 512x512, 870K
+ * 64 MiB - 32 KiB (DR_ERR_SCRATCH otherwise: about 660K triangle instances at 512x512, 820K
  * at 4 x 1024^2); tile lists beyond the rest of the buffer go through the overflow pass.
  * The buffer is part of the library's device code: each GPU on which the library's code is
  * loaded (the first launch of any of its kernels there, whichever entry point) holds its own
- * 64 MiB copy until the process ends, also in processes that never call this entry point. Every call on a GPU shares that GPU's buffer: calls that
- * overlap on one GPU (other streams, other threads) race and must be serialised by the caller.
+ * 64 MiB copy until the process ends, also in processes that never call this entry point.
+ * Every call on a GPU shares that GPU's buffer: calls that overlap on one GPU (other streams,
+ * other threads) race and must be serialised by the caller.
  * Each call prepares what it reads, so what an earlier call left there does not matter. */
 int dr_raster_visibility_static(const DrRasterGeometry* g, const uint64_t* prev_keys,
                                 uint64_t* keys, void* stream);

@@ -42,10 +42,14 @@ def load():
 
 
 def _threads() -> int:
+    """The cores this process may run on, limited by OMP_NUM_THREADS where the environment sets
+    it (a machine's share of cores for this job)."""
     try:
-        return len(os.sched_getaffinity(0))
+        cores = len(os.sched_getaffinity(0))
     except AttributeError:
-        return os.cpu_count() or 1
+        cores = os.cpu_count() or 1
+    limit = os.environ.get("OMP_NUM_THREADS", "")
+    return min(cores, int(limit)) if limit.isdigit() and int(limit) > 0 else cores
 
 
 def visible_at(pos, tri, height, width, b, row, col, previous=None, threads=None):

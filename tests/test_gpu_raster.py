@@ -513,7 +513,7 @@ def _keys_through_abi(pos, tri, res, capacity, prev=None):
               _lib.ptr(keys), _lib.ptr(workspace), size.value, host.data_ptr(), stream)
     arrived = torch.cuda.Event()
     arrived.record()
-    entries = torch.empty(max(capacity, 1), dtype=torch.int32, device=pos.device)
+    entries = torch.empty(max(capacity, 1), dtype=torch.int64, device=pos.device)
     if capacity:
         spec = (ctypes.c_uint32 * 4)(0, capacity, 0, 0)
         _lib.call("dr_raster_visibility_bin", _lib.ref(geo.struct), _lib.ptr(workspace),
@@ -524,7 +524,7 @@ def _keys_through_abi(pos, tri, res, capacity, prev=None):
     arrived.synchronize()
     counts = (ctypes.c_uint32 * 4)(*[v & 0xFFFFFFFF for v in host.tolist()])
     if counts[1] > capacity:
-        entries = torch.empty(counts[1], dtype=torch.int32, device=pos.device)
+        entries = torch.empty(counts[1], dtype=torch.int64, device=pos.device)
         _lib.call("dr_raster_visibility_bin", _lib.ref(geo.struct), _lib.ptr(workspace),
                   size.value, _lib.ptr(entries), counts, stream)
         _lib.call("dr_raster_visibility_tiles", _lib.ref(geo.struct), _lib.ptr(prev),
@@ -547,7 +547,7 @@ def _keys_one_call(pos, tri, res, capacity, groups, prev=None):
     _lib.call("dr_raster_workspace_size", _lib.ref(geo.struct), ctypes.byref(size))
     workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=pos.device)
     host = torch.full((4,), -1, dtype=torch.int32, pin_memory=True)
-    entries = torch.empty(max(capacity, 1), dtype=torch.int32, device=pos.device)
+    entries = torch.empty(max(capacity, 1), dtype=torch.int64, device=pos.device)
     _lib.call("dr_raster_visibility", _lib.ref(geo.struct), _lib.ptr(prev), _lib.ptr(keys),
               _lib.ptr(workspace), size.value, _lib.ptr(entries) if capacity else None,
               capacity, groups, host.data_ptr(), _lib.stream(pos.device))
@@ -572,7 +572,7 @@ def _keys_waiting(pos, tri, res, prev=None, groups=None):
     _lib.call("dr_raster_visibility_begin", _lib.ref(geo.struct), _lib.ptr(prev),
               _lib.ptr(keys), _lib.ptr(workspace), size.value, counts, stream)
     if counts[1]:
-        entries = torch.empty(counts[1], dtype=torch.int32, device=pos.device)
+        entries = torch.empty(counts[1], dtype=torch.int64, device=pos.device)
         _lib.call("dr_raster_visibility_bin", _lib.ref(geo.struct), _lib.ptr(workspace),
                   size.value, _lib.ptr(entries), counts, stream)
         grid = counts if groups is None else (ctypes.c_uint32 * 4)(

@@ -30,7 +30,7 @@ def _keys_allocated(pos, tri, res, prev=None):
     _lib.call("dr_raster_visibility_begin", _lib.ref(geo.struct), _lib.ptr(prev), _lib.ptr(keys),
               _lib.ptr(workspace), size.value, counts, _lib.stream(pos.device))
     capacity = max(counts[1], 1)
-    entries = torch.empty(capacity, dtype=torch.int32, device=pos.device)
+    entries = torch.empty(capacity, dtype=torch.int64, device=pos.device)
     _lib.call("dr_raster_visibility", _lib.ref(geo.struct), _lib.ptr(prev), _lib.ptr(keys),
               _lib.ptr(workspace), size.value, _lib.ptr(entries), capacity, 0, None,
               _lib.stream(pos.device))
