@@ -321,8 +321,12 @@ class _Shade(torch.autograd.Function):
 
 class Step:
     """One forward+backward step of a workload on the GPU: ``render()`` runs the four ops and
-    returns the final image and its target; ``__call__`` adds the MSE loss and its backward
-    pass. ``leaves`` are the tensors that receive gradients."""
+    returns the final image and its target; ``__call__`` computes the MSE loss
+    mean((image - target)^2) and runs the backward pass from it: the render's backward seeded
+    with the loss's gradient 2 (image - target) / n, as ``loss.backward()`` would (the same
+    values; seeding through autograd would scale by a one-element device tensor, which
+    PyTorch does in a non-vectorized kernel over the whole image). ``leaves`` are the tensors
+    that receive gradients."""
 
     def __init__(self, render, leaves):
         self.render, self.leaves = render, leaves
@@ -331,8 +335,9 @@ class Step:
         for x in self.leaves:
             x.grad = None
         image, target = self.render()
-        loss = _mse(image, target)
-        loss.backward()
+        diff = torch.sub(image, target)
+        loss = _loss_of(diff)
+        image.backward(torch.mul(diff, 2.0 / diff.numel()))
         return loss
 
 
@@ -653,20 +658,36 @@ def _loss_of(diff):
     return torch.linalg.vector_norm(flat).square().div_(flat.numel())
 
 
-def _graph_nodes(graph, path: Path) -> dict | None:
-    """Kernel and memset nodes of a captured graph, from its DOT dump (None where the runtime
-    does not dump graphs)."""
+# hipGraphNodeType values (hip_runtime_api.h) named in the node counts.
+_NODE_TYPES = {0: "kernel", 1: "memcpy", 2: "memset", 3: "host", 4: "graph", 5: "empty",
+               6: "wait_event", 7: "event_record", 10: "mem_alloc", 11: "mem_free"}
+
+
+def _graph_nodes(graph) -> dict | None:
+    """Nodes of a captured graph by type, read through the HIP runtime (hipGraphGetNodes,
+    hipGraphNodeGetType); None where the graph or the runtime does not give them."""
+    import ctypes
+
     try:
-        graph.debug_dump(str(path))
-        text = path.read_text().lower()
+        handle = graph.raw_cuda_graph()
+        hip_rt = ctypes.CDLL("libamdhip64.so")
     except (RuntimeError, OSError) as error:
-        print(f"graph dump unavailable: {error}", file=sys.stderr)
+        print(f"graph nodes unavailable: {error}", file=sys.stderr)
         return None
-    finally:
-        if path.exists():
-            path.unlink()
-    return {"kernel": text.count("kernel_node") or text.count("kernel"),
-            "memset": text.count("memset")}
+    count = ctypes.c_size_t(0)
+    if hip_rt.hipGraphGetNodes(ctypes.c_void_p(handle), None, ctypes.byref(count)) != 0:
+        return None
+    nodes = (ctypes.c_void_p * count.value)()
+    if hip_rt.hipGraphGetNodes(ctypes.c_void_p(handle), nodes, ctypes.byref(count)) != 0:
+        return None
+    out = defaultdict(int)
+    kind = ctypes.c_int(0)
+    for node in nodes[:count.value]:
+        if hip_rt.hipGraphNodeGetType(ctypes.c_void_p(node), ctypes.byref(kind)) != 0:
+            return None
+        out[_NODE_TYPES.get(kind.value, f"type{kind.value}")] += 1
+    out.setdefault("memset", 0)
+    return dict(out)
 
 
 def graph_step(step: Step, steps: int, repeats: int) -> dict | None:
@@ -687,6 +708,11 @@ def graph_step(step: Step, steps: int, repeats: int) -> dict | None:
         image.backward(torch.mul(diff, 2.0 / diff.numel()))
         return diff
 
+    # The leaves' gradient accumulators were made on the default stream by the eager steps;
+    # the warm-up on the side stream reuses them, which PyTorch reports (harmlessly) each time.
+    quiet = getattr(torch.autograd.graph, "set_warn_on_accumulate_grad_stream_mismatch", None)
+    if quiet is not None:
+        quiet(False)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     try:
@@ -695,8 +721,7 @@ def graph_step(step: Step, steps: int, repeats: int) -> dict | None:
                 captured()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        graph.enable_debug_mode()
+        graph = torch.cuda.CUDAGraph(keep_graph=True)
         with torch.cuda.graph(graph):
             diff = captured()
         grads = [x.grad for x in step.leaves]
@@ -704,7 +729,8 @@ def graph_step(step: Step, steps: int, repeats: int) -> dict | None:
         print(f"graph capture failed, eager timing only: {error}", file=sys.stderr)
         torch.cuda.synchronize()
         return None
-    nodes = _graph_nodes(graph, ROOT / "gpurun_out" / f"graph.{os.getpid()}.dot")
+    graph.instantiate()
+    nodes = _graph_nodes(graph)
 
     # One replay against one eager step of the same inputs.
     graph.replay()
@@ -844,12 +870,18 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int,
 
     timer.active = True
     torch.cuda.synchronize()
+    before = torch.cuda.memory_stats(device)
     start = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
+    after = torch.cuda.memory_stats(device)
     timer.active = False
+    # Device memory the caching allocator took from or gave back to the runtime during the
+    # timed steps (0 in a steady state: every buffer reused).
+    allocator = {k: int(after.get(k, 0) - before.get(k, 0))
+                 for k in ("segment.all.allocated", "segment.all.freed", "num_alloc_retries")}
     ms_per_step = elapsed * 1e3 / steps
     live = timer.summary()
     if dominant is None:  # no warm-up: every entry point was timed in the timed steps
@@ -938,6 +970,7 @@ def run(name: str, steps: int, warmup: int, device, cpu: bool, sample_tris: int,
         # The reference's rule: median (and p10, p90) of individually synchronised steps.
         "synced_steps": synced,
         "first_call": first_call,
+        "allocator_during_timed_steps": allocator,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,

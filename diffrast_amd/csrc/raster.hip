@@ -1171,6 +1171,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   __shared__ uint64_t s_far[256 / DR_WAVE];
   __shared__ float s_row_far[kTile];  // the depth of the farthest key of each tile row (NaN: empty)
   __shared__ float s_bound[kChunk];  // lower bound of each staged triangle's depth
+  __shared__ float s_floor[DR_WAVE];  // per depth slab: a lower bound of its triangles' bounds
 
   // Workgroups are dispatched round-robin over the 8 XCDs: XCD k runs the busy tiles of share
   // k (for a batch of 8 images, one image), so the records that neighbouring tiles share stay in
@@ -1220,14 +1221,14 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   // empty). Keys only get nearer, so an entry whose bound lies beyond it lies beyond the
   // farthest key of its own chunk too: it is dropped before its record is read.
   float stale_far = __int_as_float(0x7f800000);
-  // Lane s (1 <= s < slabs) of each wave holds the floor of slab s's depth bounds: once the
-  // tile's farthest key lies before it, slab s and every farther one are behind every key of
-  // the tile, and the walk ends at the slab's first entry.
+  // s_floor[s] (1 <= s < slabs) is the floor of slab s's depth bounds, rounded down to float:
+  // once the tile's farthest key lies before it, slab s and every farther one are behind every
+  // key of the tile, and the walk ends at the slab's first entry. (The previous tile's last
+  // chunk ended with a barrier, so the table is free.)
   const bool by_slab = ws.slabs > 1 && ws.slabs <= DR_WAVE;
-  double floor_s = 0.0;
-  if (by_slab && lane >= 1 && lane < ws.slabs) {
+  if (by_slab && threadIdx.x >= 1 && (int)threadIdx.x < ws.slabs) {
     const uint2 span = reinterpret_cast<const uint2*>(ws.depth_range)[ws.depth_ranges > 1 ? b : 0];
-    floor_s = slab_floor(span, lane, ws.slabs);
+    s_floor[threadIdx.x] = __double2float_rd(slab_floor(span, threadIdx.x, ws.slabs));
   }
   uint32_t stop = end;
   for (uint32_t at = begin; at < stop; at += kChunk) {
@@ -1267,13 +1268,16 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     for (int w = 0; w < 256 / DR_WAVE; ++w) far_key = s_far[w] > far_key ? s_far[w] : far_key;
     const bool cull = far_key != kEmptyKey;
     const float far_depth = key_depth(far_key);
-    stale_far = cull ? far_depth : __int_as_float(0x7f800000);
+    // (Uniform over the workgroup: kept in scalar registers.)
+    stale_far = __uint_as_float(__builtin_amdgcn_readfirstlane(
+        __float_as_uint(cull ? far_depth : __int_as_float(0x7f800000))));
     if (cull && by_slab) {
       const uint64_t behind_slabs =
-          __ballot(lane >= 1 && lane < ws.slabs && floor_s > (double)far_depth);  // uniform
+          __ballot(lane >= 1 && lane < ws.slabs && s_floor[lane] > far_depth);  // uniform
       if (behind_slabs != 0) {
         const int first = __ffsll((unsigned long long)behind_slabs) - 1;
-        stop = min(stop, ws.list_offsets[(size_t)tile * ws.slabs + first]);
+        stop = __builtin_amdgcn_readfirstlane(
+            min(stop, ws.list_offsets[(size_t)tile * ws.slabs + first]));
       }
     }
 
