@@ -575,22 +575,24 @@ def _profile_fields(path: Path) -> dict:
 
 
 def profiled_valu(kernel: str, workload: str, mean_ms: float) -> dict | None:
-    """Vector issue of ``kernel`` from its committed rocprofv3 counter summary: wave64 VALU
+    """Vector issue of ``kernel`` from the workload's committed rocprofv3 counter summary
+    (lines ``<kernel>.valu_instructions: N`` and ``<kernel>.valu_busy: F``): wave64 VALU
     instructions per launch (SQ_INSTS_VALU) over the live mean duration, against the issue
     peak, and the VALU-busy fraction that the summary derives from SQ_ACTIVE_INST_VALU (its
     header states how)."""
-    path = ROOT / "profiles" / f"{kernel}.{workload}.valu.txt"
+    path = ROOT / "profiles" / f"valu.{workload}.txt"
     if not path.exists():
         return None
     f = _profile_fields(path)
-    if "valu_instructions" not in f:
+    if f"{kernel}.valu_instructions" not in f:
         return None
-    rate = f["valu_instructions"] / (mean_ms * 1e-3)
-    out = {"instructions": int(f["valu_instructions"]),
+    instructions = f[f"{kernel}.valu_instructions"]
+    rate = instructions / (mean_ms * 1e-3)
+    out = {"instructions": int(instructions),
            "issue_rate": round(rate / 1e9, 1), "issue_peak": round(VALU_ISSUE_PEAK / 1e9, 1),
            "unit": "G wave64 instructions/s", "issue_frac": round(rate / VALU_ISSUE_PEAK, 4)}
-    if "valu_busy" in f:
-        out["busy_frac"] = round(f["valu_busy"], 4)
+    if f"{kernel}.valu_busy" in f:
+        out["busy_frac"] = round(f[f"{kernel}.valu_busy"], 4)
     out["source"] = str(path.relative_to(ROOT))
     return out
 
