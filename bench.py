@@ -798,11 +798,12 @@ SCATTER_ENTRY = {k: n for n, k in SINGLE_KERNEL.items() if n.endswith("_backward
 
 
 def profiled_atomics(workload: str, live_ms: dict) -> dict | None:
-    """Device atomic requests per launch of the backward scatters and the visibility's setup
-    pass, from the workload's committed counter summary (lines ``<kernel>.atomic_requests: N``,
-    ``<kernel>.atomic_beyond_l2: N`` and ``<kernel>.mean_us: D``, the kernel-trace mean of the
-    same profiling session), rated per second over the live mean launch of the kernel's entry
-    point where it launches that kernel alone, else over the summary's mean."""
+    """Device atomic requests per launch of the kernels of a step that issue them (the backward
+    scatters, the visibility's setup and bin passes), from the workload's committed counter
+    summary (lines ``<kernel>.launches``, ``<kernel>.atomic_requests``,
+    ``<kernel>.atomic_beyond_l2`` and ``<kernel>.mean_us``, the kernel-trace mean), rated per
+    second over the live mean launch of the kernel's entry point where it launches that kernel
+    alone, else over the summary's mean. Kernels launched once per mesh are left out."""
     path = ROOT / "profiles" / f"atomics.{workload}.pmc.txt"
     if not path.exists():
         return None
@@ -812,6 +813,8 @@ def profiled_atomics(workload: str, live_ms: dict) -> dict | None:
         if not key.endswith(".atomic_requests"):
             continue
         kernel = key[:-len(".atomic_requests")]
+        if f.get(f"{kernel}.launches", 2) < 2:
+            continue  # once per mesh (edge hash, processing order), not per step
         entry = SCATTER_ENTRY.get(kernel)
         ms = live_ms.get(entry) if entry else None
         source = "live"
