@@ -554,7 +554,7 @@ def profiled_traffic(kernel: str, workload: str) -> dict | None:
 
 
 # Vector issue of the MI355X: 256 CUs x 4 SIMDs, each issuing one wave64 VALU instruction
-# (64 lanes over a 16-lane SIMD) every 4 clocks without packed fp32, which this build does not
+# (64 lanes over a 16-lane SIMD) every 4 clocks without packed fp32, which the kernels do not
 # use; at 2.4 GHz that is 614 G wave instructions/s (39.3 T lane operations/s; with fused
 # multiply-adds counted twice and packed fp32, the published 157.3 TFLOP/s).
 SIMDS = 256 * 4

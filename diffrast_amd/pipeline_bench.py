@@ -166,7 +166,7 @@ def _label(x, y, body, size=12, color=_SOFT, anchor="start", bold=False) -> str:
 
 def chart(report: dict, views: int = PUBLISHED_VIEWS) -> str:
     """Two log-scale panels (forward; forward + backward) of ms against resolution, one solid
-    line per triangle count for this build and a dashed one for the published figures."""
+    line per triangle count for these kernels and a dashed one for the published figures."""
     rows = [r for r in report["results"] if r["views"] == views]
     if not rows:
         raise ValueError(f"no results for {views} views")

@@ -1,7 +1,7 @@
 """CPU oracle for the render pipeline: TEST INFRASTRUCTURE, never part of the product.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-import this package, and only as the checker that the HIP backend is compared against (and,
+import this package, and only as the reference that the HIP backend is compared against (and,
 in ``bench.py``, as the reported CPU baseline). ``diffrast_amd`` never imports it and has no
 CPU fallback.
 
