@@ -66,8 +66,10 @@ struct Workspace {
   float4* records;           // binned triangles, kRecord float4 each: the three clip-space
                              // vertices, then the bits of (image, row, tx0 | tx1 << 16,
                              // ty0 | ty1 << 16)
-  float* record_bound;       // per record slot: depth_lower_bound of its triangle, which the bin
-                             // pass copies into the tile entries
+  uint4* record_bins;        // per record slot, what the bin pass reads (16 bytes, not the
+                             // record's 64): tx0 | tx1 << 16, ty0 | ty1 << 16, the list of tile
+                             // (0, 0) of its image and slab, and the bits of its triangle's
+                             // depth_lower_bound, which the bin pass copies into the entries
   // Tile lists: list tile * slabs + slab holds the binned triangles of that tile whose
   // nearest depth falls in depth slab `slab` of their image, so a tile's entries are one range
   // that runs near to far.
@@ -162,7 +164,7 @@ Workspace layout(const DrRasterGeometry& g, char* base) {
     w.bound_parts = (uint32_t*)take(sizeof(uint32_t) * 6 * (size_t)blocks_for(g.num_tri, 256));
   }
   w.records = (float4*)take(sizeof(float4) * kRecord * 256 * (size_t)w.record_blocks);
-  w.record_bound = (float*)take(sizeof(float) * 256 * (size_t)w.record_blocks);
+  w.record_bins = (uint4*)take(sizeof(uint4) * 256 * (size_t)w.record_blocks);
   w.bytes = off;
   if (w.ordered && g.order != nullptr) w.order = (int4*)g.order;
   return w;
@@ -843,15 +845,16 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
       float4* out = ws.records + (size_t)rec * kRecord;
 #pragma unroll
       for (int k = 0; k < 3; ++k) out[k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
-      ws.record_bound[rec] = depth_lower_bound(T);
+      const uint32_t tx_range = (uint32_t)tx0 | ((uint32_t)tx1 << 16);
+      const uint32_t ty_range = (uint32_t)ty0 | ((uint32_t)ty1 << 16);
       out[3] = make_float4(__int_as_float(b), __int_as_float(t | (slab << 24)),
-                           __uint_as_float((uint32_t)tx0 | ((uint32_t)tx1 << 16)),
-                           __uint_as_float((uint32_t)ty0 | ((uint32_t)ty1 << 16)));
-      const uint32_t image_tiles = (uint32_t)b * ws.tiles_x * ws.tiles_y;
+                           __uint_as_float(tx_range), __uint_as_float(ty_range));
+      const uint32_t list0 = (uint32_t)b * ws.tiles_x * ws.tiles_y * ws.slabs + (uint32_t)slab;
+      ws.record_bins[rec] =
+          make_uint4(tx_range, ty_range, list0, __float_as_uint(depth_lower_bound(T)));
       for (int ty = ty0; ty <= ty1; ++ty)
         for (int tx = tx0; tx <= tx1; ++tx) {
-          const uint32_t list =
-              (image_tiles + ty * ws.tiles_x + tx) * ws.slabs + (uint32_t)slab;
+          const uint32_t list = list0 + (uint32_t)(ty * ws.tiles_x + tx) * ws.slabs;
           const int slot = table.insert(list);
           if (slot >= 0)
             atomicAdd(table.count + slot, 1u);
@@ -972,23 +975,21 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint2* en
   // The records of setup workgroup blockIdx.x.
   const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
   int tx0 = 0, tx1 = -1, ty0 = 0, ty1 = -1;
-  uint32_t image_tiles = 0, slab = 0, bound_bits = 0u;
+  uint32_t list0 = 0u, bound_bits = 0u;
   if (threadIdx.x < ws.block_records[blockIdx.x]) {
     // Each entry carries the triangle's depth bound, so that the tile pass can skip a
     // triangle behind every key of its tile without reading its record.
-    bound_bits = __float_as_uint(ws.record_bound[r]);
-    const float4 rec = ws.records[(size_t)r * kRecord + 3];
-    const uint32_t rx = __float_as_uint(rec.z), ry = __float_as_uint(rec.w);
-    tx0 = (int)(rx & 0xffffu);
-    tx1 = (int)(rx >> 16);
-    ty0 = (int)(ry & 0xffffu);
-    ty1 = (int)(ry >> 16);
-    slab = __float_as_uint(rec.y) >> 24;
-    image_tiles = (uint32_t)__float_as_int(rec.x) * ws.tiles_x * ws.tiles_y;
+    const uint4 info = ws.record_bins[r];
+    tx0 = (int)(info.x & 0xffffu);
+    tx1 = (int)(info.x >> 16);
+    ty0 = (int)(info.y & 0xffffu);
+    ty1 = (int)(info.y >> 16);
+    list0 = info.z;
+    bound_bits = info.w;
   }
   for (int ty = ty0; ty <= ty1; ++ty)
     for (int tx = tx0; tx <= tx1; ++tx) {
-      const int slot = table.insert((image_tiles + ty * ws.tiles_x + tx) * ws.slabs + slab);
+      const int slot = table.insert(list0 + (uint32_t)(ty * ws.tiles_x + tx) * ws.slabs);
       if (slot >= 0) atomicAdd(table.count + slot, 1u);
     }
   __syncthreads();
@@ -1011,7 +1012,7 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint2* en
   __syncthreads();
   for (int ty = ty0; ty <= ty1; ++ty)
     for (int tx = tx0; tx <= tx1; ++tx) {
-      const uint32_t list = (image_tiles + ty * ws.tiles_x + tx) * ws.slabs + slab;
+      const uint32_t list = list0 + (uint32_t)(ty * ws.tiles_x + tx) * ws.slabs;
       const int slot = table.find(list);
       const uint32_t at = slot >= 0 ? table.base[slot] + atomicAdd(table.count + slot, 1u)
                                     : atomicAdd(ws.list_cursor + list, 1u);

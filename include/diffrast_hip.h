@@ -172,7 +172,7 @@ int dr_raster_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys, u
  * for callers that cannot allocate -- code under HIP graph capture, tight serving loops,
  * harnesses that forbid allocation. Limit: the visibility workspace of the geometry
  * (dr_raster_workspace_size) must leave room for 4096 tile entries, i.e. be at most
- * 64 MiB - 32 KiB (DR_ERR_SCRATCH otherwise: about 660K triangle instances at 512x512, 820K
+ * 64 MiB - 32 KiB (DR_ERR_SCRATCH otherwise: about 590K triangle instances at 512x512, 710K
  * at 4 x 1024^2); tile lists beyond the rest of the buffer go through the overflow pass.
  * The buffer is part of the library's device code: each GPU on which the library's code is
  * loaded (the first launch of any of its kernels there, whichever entry point) holds its own
