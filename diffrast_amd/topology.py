@@ -12,7 +12,7 @@ import weakref
 
 from torch import Tensor
 
-from diffrast_amd._cache import TensorCache, stamp
+from diffrast_amd._cache import TensorCache, fingerprint
 from diffrast_amd.backends import get_backend
 
 
@@ -33,7 +33,7 @@ class TopologyHash:
         self._shape = tuple(tri.shape)
         self._device = tri.device
         # What the source tensor looked like, to notice in-place edits of that same object.
-        self._origin: tuple[weakref.ref, tuple | None] | None = (weakref.ref(tri), stamp(tri))
+        self._origin: tuple[weakref.ref, tuple | None] | None = (weakref.ref(tri), fingerprint(tri))
 
     def __repr__(self) -> str:
         return f"TopologyHash(triangles={self._shape[0]}, device={str(self._device)!r})"
@@ -47,8 +47,8 @@ class TopologyHash:
     def _edited(self, tri: Tensor) -> bool:
         if self._origin is None:
             return False
-        source, fingerprint = self._origin
-        return source() is tri and stamp(tri) != fingerprint
+        source, recorded = self._origin
+        return source() is tri and fingerprint(tri) != recorded
 
     def neighbours(self, tri: Tensor) -> Tensor:
         """The adjacency, int32 ``[triangles, 3]``, after checking that it fits ``tri``."""
