@@ -249,6 +249,38 @@ def _order(geo: _Geometry, workspace: Tensor, workspace_bytes: int, capturing: b
     geo.struct.order = entry.tensor.data_ptr()
 
 
+def share_order(source: Tensor, copy: Tensor) -> bool:
+    """Lets ``copy``, a tensor holding what ``source`` holds now (a depth peeler's copy of its
+    tri), use the processing orders remembered for ``source``: an order depends only on the
+    contents of tri (and the vertex count, part of its key), so the two can share it instead of
+    the copy computing its own (some 27 ms at 1.3M triangles) in its first call. Nothing happens
+    where ``source`` has no order yet or either tensor keeps no version counter. Returns
+    whether an order was shared."""
+    if source.is_inference() or copy.is_inference() or source.shape != copy.shape:
+        return False
+    shared = False
+    with _orders_lock:
+        found = [(key, entry) for key, entry in _ORDERS.items()
+                 if entry.ref() is source and key[1] == source.data_ptr()
+                 and key[2] == source._version]
+        for (device, _, _, num_tri, num_vertices), entry in found:
+            key = (device, copy.data_ptr(), copy._version, num_tri, num_vertices)
+            held = _ORDERS.get(key)
+            if held is not None and held.ref() is copy:
+                shared = True
+                continue
+            _ORDERS.pop(key, None)
+            if len(_ORDERS) >= _ORDERS_KEPT:
+                for old in list(_ORDERS):
+                    if not _ORDERS[old].pinned:
+                        _ORDERS.pop(old)
+                        break
+            _ORDERS[key] = _Order(entry.tensor, weakref.ref(
+                copy, lambda dead, key=key: _forget_order(key, dead)))
+            shared = True
+    return shared
+
+
 def _visibility(geo: _Geometry, previous: Tensor | None) -> Tensor:
     """Visibility keys [batch, height, width] (int64 holding the uint64 key bits).
 

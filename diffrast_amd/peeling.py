@@ -7,6 +7,7 @@ the same call.
 
 from __future__ import annotations
 
+import weakref
 from types import TracebackType
 
 from torch import Tensor
@@ -47,6 +48,14 @@ class DepthPeeler:
         self._backend = get_backend(pos.device, "rasterize")
         self._state = None
         self._open = True
+        # A backend that keeps per-tri state (the HIP backend's processing order of a large
+        # mesh) may let the copy of tri use what it keeps for tri, and, once the first layer
+        # has made it for the copy, give it back to tri while tri still holds the same values.
+        self._share = getattr(self._backend, "share_order", None)
+        self._source = None
+        if self._share is not None and not tri.is_inference():
+            if not self._share(tri, self._geometry[1]):
+                self._source = (weakref.ref(tri), tri._version, tri.data_ptr())
 
     def __enter__(self) -> DepthPeeler:
         return self
@@ -68,6 +77,13 @@ class DepthPeeler:
             rast, rast_db, state = self._backend.rasterize_ranges(
                 pos, tri, self._resolution, self._grad_db, ranges, self._state)
         self._state = state
+        if self._source is not None:
+            source, version, address = self._source
+            self._source = None
+            original = source()
+            if original is not None and original._version == version and \
+                    original.data_ptr() == address:
+                self._share(tri, original)
         if not self._output_db:
             rast_db = rast.new_zeros(*rast.shape[:3], 0)
         return rast, rast_db

@@ -221,6 +221,39 @@ def test_processing_order_is_reused_per_tri_and_recomputed_when_tri_changes():
                for e in hip._ORDERS.values())
 
 
+def test_depth_peelers_share_the_processing_order_of_their_tri():
+    # A peeler rasterizes a copy of tri. A peeler made before tri has a processing order
+    # computes one for its copy and hands it back to tri; a later peeler's copy takes tri's
+    # instead of computing its own. The layers are the oracle's either way.
+    from diffrast_amd import workloads as W
+    verts, tri = W.icosphere(5)
+    pos_cpu = W.clip_positions(verts, W.random_eyes(2, 3.0, torch.Generator().manual_seed(25)),
+                               1.0)
+    pos, tri_dev, res = pos_cpu.cuda(), tri.cuda(), (64, 80)
+    ctx = dr.RasterizeContext("cuda")
+    hip._ORDERS.clear()
+    with dr.DepthPeeler(ctx, pos, tri_dev, res) as peeler:
+        first = [peeler.rasterize_next_layer()[0] for _ in range(2)]
+    assert any(e.ref() is tri_dev for e in hip._ORDERS.values())
+    computed = {id(e.tensor) for e in hip._ORDERS.values()}
+    assert len(computed) == 1
+    with dr.DepthPeeler(ctx, pos, tri_dev, res) as peeler:
+        assert sum(e.ref() is peeler._geometry[1] for e in hip._ORDERS.values()) == 1
+        second = [peeler.rasterize_next_layer()[0] for _ in range(2)]
+    assert {id(e.tensor) for e in hip._ORDERS.values()} == computed
+    for layer, (a, b, (er, _)) in enumerate(zip(first, second, oracle_layers(pos_cpu, tri, res, 2))):
+        assert torch.equal(a, b), layer
+        assert torch.equal(a[..., 3].cpu(), er[..., 3]), layer
+    # A tri changed in place after its peeler was made keeps its own state: the peeler's copy
+    # holds the old triangles, so its order is not handed back.
+    hip._ORDERS.clear()
+    flipped = tri_dev.clone()
+    with dr.DepthPeeler(ctx, pos, flipped, res) as peeler:
+        flipped[:, [1, 2]] = flipped[:, [2, 1]]
+        peeler.rasterize_next_layer()
+    assert not any(e.ref() is flipped for e in hip._ORDERS.values())
+
+
 @pytest.mark.parametrize("w_range", [(1.0, 2.0), (-1.0, 2.0)])
 def test_every_pixel_of_every_layer(w_range):
     gen = torch.Generator().manual_seed(9)
