@@ -313,9 +313,9 @@ __global__ __launch_bounds__(256) void tex_fwd(DrTextureArgs a, double* out) {
     return;
   }
   const tex::LevelDims D = tex::lookup_levels(a, K);
-  const Bilinear<double> L0 = tex::level_setup(a, K, D, 0);
+  const Bilinear<double> L0 = tex::level_setup<CUBE>(a, K, D, 0);
   const bool two = K.levels == 2;
-  const Bilinear<double> L1 = two ? tex::level_setup(a, K, D, 1) : L0;
+  const Bilinear<double> L1 = two ? tex::level_setup<CUBE>(a, K, D, 1) : L0;
   const bool bad = K.bad || L0.bad || (two && L1.bad);
   const double frac = K.level_weight[1];
   for (int c = 0; c < C; ++c) {
@@ -355,9 +355,9 @@ __global__ __launch_bounds__(256) void tex_bwd(DrTextureArgs a, const double* gr
     live = false;  // nearest passes no coordinate gradient
   } else if (live) {
     const tex::LevelDims D = tex::lookup_levels(a, K);
-    const Bilinear<double> L[2] = {tex::level_setup(a, K, D, 0),
-                                   K.levels == 2 ? tex::level_setup(a, K, D, 1)
-                                                 : tex::level_setup(a, K, D, 0)};
+    const Bilinear<double> L[2] = {tex::level_setup<CUBE>(a, K, D, 0),
+                                   K.levels == 2 ? tex::level_setup<CUBE>(a, K, D, 1)
+                                                 : tex::level_setup<CUBE>(a, K, D, 0)};
     const int levels = K.levels;
     if (K.bad || L[0].bad || (levels == 2 && L[1].bad)) {
       live = false;

@@ -86,9 +86,9 @@ __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* __
     return;
   }
   const LevelDims D = lookup_levels(a, K);
-  const Bilinear<float> L0 = level_setup(a, K, D, 0);
+  const Bilinear<float> L0 = level_setup<CUBE>(a, K, D, 0);
   const bool two = K.levels == 2;
-  const Bilinear<float> L1 = two ? level_setup(a, K, D, 1) : L0;
+  const Bilinear<float> L1 = two ? level_setup<CUBE>(a, K, D, 1) : L0;
   const bool bad = K.bad || L0.bad || (two && L1.bad);
   const float frac = K.level_weight[1];
   for (int c0 = 0; c0 < C; c0 += NC) {
@@ -215,10 +215,10 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     live = false;  // no coordinate gradient
   } else if (live) {
     const LevelDims D = lookup_levels(a, K);
-    const Bilinear<float> L0 = level_setup(a, K, D, 0);
+    const Bilinear<float> L0 = level_setup<CUBE>(a, K, D, 0);
     Bilinear<float> L1 = L0;
     const bool two = K.levels == 2;
-    if (two) L1 = level_setup(a, K, D, 1);
+    if (two) L1 = level_setup<CUBE>(a, K, D, 1);
     if (K.bad || L0.bad || (two && L1.bad)) {
       live = false;
     } else {

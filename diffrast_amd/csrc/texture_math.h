@@ -273,6 +273,30 @@ __device__ __forceinline__ bool tap(int row, int col, int face, int h, int w, in
   return valid;
 }
 
+// Rows (or columns) i and i + 1 of a level n texels long under a 2D boundary: wrapped or
+// clamped into [0, n), and whether each reads a texel (as tap() decides for each tap; the
+// four taps of a bilinear lookup combine two of each).
+struct AxisPair {
+  int at[2];
+  bool valid[2];
+};
+
+__device__ __forceinline__ AxisPair axis_pair(int i, int n, int boundary) {
+  AxisPair p;
+  if (boundary == DR_BOUNDARY_WRAP) {
+    p.at[0] = wrap_index(i, n);
+    p.at[1] = p.at[0] + 1 == n ? 0 : p.at[0] + 1;  // (i + 1) mod n
+    p.valid[0] = p.valid[1] = true;
+  } else {
+    const bool zero = boundary == DR_BOUNDARY_ZERO;
+    p.valid[0] = !zero || (i >= 0 && i < n);
+    p.valid[1] = !zero || (i + 1 >= 0 && i + 1 < n);
+    p.at[0] = min(max(i, 0), n - 1);
+    p.at[1] = min(max(i + 1, 0), n - 1);
+  }
+  return p;
+}
+
 template <class S>
 struct Bilinear {
   int64_t index[4];
@@ -286,7 +310,9 @@ struct Bilinear {
   S corner[4];  // 1 where (left|right) & (above|below) for taps 00, 01, 10, 11
 };
 
-template <class S>
+// CUBE: boundary is DR_BOUNDARY_CUBE, else one of the 2D boundaries (known when compiling, so
+// that 2D lookups carry no cube-corner arithmetic).
+template <class S, bool CUBE>
 __device__ __forceinline__ Bilinear<S> bilinear_setup(S s, S t, int face, int h, int w,
                                                       int64_t offset, int boundary) {
   Bilinear<S> L;
@@ -301,11 +327,25 @@ __device__ __forceinline__ Bilinear<S> bilinear_setup(S s, S t, int face, int h,
   L.size_x = (S)w;
   L.size_y = (S)h;
   const int col = (int)x0, row = (int)y0;
-  L.valid[0] = tap(row, col, face, h, w, offset, boundary, L.index[0]);
-  L.valid[1] = tap(row, col + 1, face, h, w, offset, boundary, L.index[1]);
-  L.valid[2] = tap(row + 1, col, face, h, w, offset, boundary, L.index[2]);
-  L.valid[3] = tap(row + 1, col + 1, face, h, w, offset, boundary, L.index[3]);
-  L.cube = boundary == DR_BOUNDARY_CUBE;
+  L.cube = CUBE;
+  if constexpr (CUBE) {
+    L.valid[0] = tap(row, col, face, h, w, offset, boundary, L.index[0]);
+    L.valid[1] = tap(row, col + 1, face, h, w, offset, boundary, L.index[1]);
+    L.valid[2] = tap(row + 1, col, face, h, w, offset, boundary, L.index[2]);
+    L.valid[3] = tap(row + 1, col + 1, face, h, w, offset, boundary, L.index[3]);
+  } else {
+    // The two rows and two columns once each, then the four taps from them.
+    const AxisPair R = axis_pair(row, h, boundary), K = axis_pair(col, w, boundary);
+    const int64_t above = offset + (int64_t)R.at[0] * w, below = offset + (int64_t)R.at[1] * w;
+    L.index[0] = above + K.at[0];
+    L.index[1] = above + K.at[1];
+    L.index[2] = below + K.at[0];
+    L.index[3] = below + K.at[1];
+    L.valid[0] = R.valid[0] && K.valid[0];
+    L.valid[1] = R.valid[0] && K.valid[1];
+    L.valid[2] = R.valid[1] && K.valid[0];
+    L.valid[3] = R.valid[1] && K.valid[1];
+  }
   if (L.cube) {
     const bool left = col < 0, right = col + 1 >= w, above = row < 0, below = row + 1 >= h;
     L.corner[0] = (left && above) ? S(1) : S(0);
@@ -536,10 +576,11 @@ __device__ __forceinline__ LevelDims lookup_levels(const DrTextureArgs& a, const
   return D;
 }
 
-template <class S>
+template <bool CUBE, class S>
 __device__ __forceinline__ Bilinear<S> level_setup(const DrTextureArgs& a, const Lookup<S>& K,
                                                    const LevelDims& D, int l) {
-  return bilinear_setup<S>(K.s, K.t, K.face, D.h[l], D.w[l], D.off[l], a.boundary);
+  return bilinear_setup<S, CUBE>(K.s, K.t, K.face, D.h[l], D.w[l], D.off[l],
+                                 CUBE ? (int)DR_BOUNDARY_CUBE : a.boundary);
 }
 
 // Nearest: the texel containing the coordinate (reference.py:555-573).
