@@ -60,15 +60,16 @@ __device__ __forceinline__ void tap_column(const float (&t)[4][N], int c, float 
 }
 
 // NC channels per pass (the channel count when it is 1-4; 4 with a loop for more). Every tap
-// of a pass is loaded before its stores.
-template <int NC, bool CUBE>
+// of a pass is loaded before its stores. FILTER and BOUNDARY: a.filter and a.boundary, fixed
+// when compiling (DR_BOUNDARY_CUBE for cube maps; FILTER may be kAnyMode: read at run time).
+template <int NC, bool CUBE, int FILTER, int BOUNDARY>
 __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* __restrict__ out) {
   const int64_t pixel = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (pixel >= (int64_t)a.batch * a.height * a.width) return;
   const int C = a.channels;
   float* o = out + pixel * C;
   Lookup<float> K;
-  lookup_setup<float, CUBE>(a, pixel, K);
+  lookup_setup<float, CUBE, FILTER>(a, pixel, K);
   if (K.dir_invalid) {
     for (int c = 0; c < C; ++c) o[c] = 0.0f;
     return;
@@ -81,14 +82,14 @@ __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* __
   if (K.levels == 0) {
     int64_t index;
     bool valid;
-    const bool bad = nearest_setup(a, K, index, valid);
+    const bool bad = nearest_setup<BOUNDARY>(a, K, index, valid);
     for (int c = 0; c < C; ++c) o[c] = bad ? nan : (valid ? texels[index * C + c] : 0.0f);
     return;
   }
   const LevelDims D = lookup_levels(a, K);
-  const Bilinear<float> L0 = level_setup<CUBE>(a, K, D, 0);
+  const Bilinear<float> L0 = level_setup<CUBE, BOUNDARY>(a, K, D, 0);
   const bool two = K.levels == 2;
-  const Bilinear<float> L1 = two ? level_setup<CUBE>(a, K, D, 1) : L0;
+  const Bilinear<float> L1 = two ? level_setup<CUBE, BOUNDARY>(a, K, D, 1) : L0;
   const bool bad = K.bad || L0.bad || (two && L1.bad);
   const float frac = K.level_weight[1];
   for (int c0 = 0; c0 < C; c0 += NC) {
@@ -174,7 +175,7 @@ __device__ __forceinline__ void level_taps(const Bilinear<float>& L, float level
   }
 }
 
-template <int NC, bool CUBE>
+template <int NC, bool CUBE, int FILTER, int BOUNDARY>
 __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const float* grad_out,
                                                       float* grad_texels, float* grad_uv,
                                                       float* grad_uv_da, float* grad_bias) {
@@ -201,13 +202,13 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
   float g_s = 0.0f, g_t = 0.0f, g_lod = 0.0f;
   bool live = false;
   if (tp.inside) {
-    lookup_setup<float, CUBE>(a, pixel, K);
+    lookup_setup<float, CUBE, FILTER>(a, pixel, K);
     live = !K.dir_invalid;
   }
   if (live && K.levels == 0) {
     int64_t index;
     bool valid;
-    const bool bad = nearest_setup(a, K, index, valid);
+    const bool bad = nearest_setup<BOUNDARY>(a, K, index, valid);
     if (!bad && valid) {
       tap_key[0] = (uint32_t)(tex_off + index);
       tap_weight[0] = 1.0f;
@@ -215,10 +216,10 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     live = false;  // no coordinate gradient
   } else if (live) {
     const LevelDims D = lookup_levels(a, K);
-    const Bilinear<float> L0 = level_setup<CUBE>(a, K, D, 0);
+    const Bilinear<float> L0 = level_setup<CUBE, BOUNDARY>(a, K, D, 0);
     Bilinear<float> L1 = L0;
     const bool two = K.levels == 2;
-    if (two) L1 = level_setup<CUBE>(a, K, D, 1);
+    if (two) L1 = level_setup<CUBE, BOUNDARY>(a, K, D, 1);
     if (K.bad || L0.bad || (two && L1.bad)) {
       live = false;
     } else {
@@ -616,6 +617,39 @@ MipLevels copy_levels(int n, const int32_t* h, const int32_t* w, const int64_t* 
   return L;
 }
 
+// Calls f(channel group, cube, filter, boundary) with each as a compile-time constant
+// (std::integral_constant), from a's channel count and modes (checked by valid_args): the
+// kernels are compiled for every combination, each without the other modes' code.
+template <typename F>
+int texture_modes(const DrTextureArgs& a, F f) {
+  auto with_boundary = [&](auto nc, auto filter) {
+    using std::integral_constant;
+    switch (a.boundary) {
+      case DR_BOUNDARY_CUBE:
+        return f(nc, std::true_type(), filter, integral_constant<int, DR_BOUNDARY_CUBE>());
+      case DR_BOUNDARY_WRAP:
+        return f(nc, std::false_type(), filter, integral_constant<int, DR_BOUNDARY_WRAP>());
+      case DR_BOUNDARY_CLAMP:
+        return f(nc, std::false_type(), filter, integral_constant<int, DR_BOUNDARY_CLAMP>());
+      default:
+        return f(nc, std::false_type(), filter, integral_constant<int, DR_BOUNDARY_ZERO>());
+    }
+  };
+  return channel_groups(a.channels, [&](auto nc) {
+    using std::integral_constant;
+    switch (a.filter) {
+      case DR_FILTER_NEAREST:
+        return with_boundary(nc, integral_constant<int, DR_FILTER_NEAREST>());
+      case DR_FILTER_LINEAR:
+        return with_boundary(nc, integral_constant<int, DR_FILTER_LINEAR>());
+      case DR_FILTER_MIP_NEAREST:
+        return with_boundary(nc, integral_constant<int, DR_FILTER_MIP_NEAREST>());
+      default:
+        return with_boundary(nc, integral_constant<int, DR_FILTER_MIP_LINEAR>());
+    }
+  });
+}
+
 bool valid_args(const DrTextureArgs* a) {
   if (!a || !a->texels || !a->uv || a->batch < 0 || a->height <= 0 || a->width <= 0) return false;
   if (a->channels <= 0 || a->tex_batch < 1 || a->num_levels < 1 || a->num_levels > DR_MAX_LEVELS)
@@ -638,13 +672,10 @@ extern "C" int dr_texture_forward(const DrTextureArgs* a, float* out, void* stre
   const int64_t pixels = (int64_t)a->batch * a->height * a->width;
   if (pixels == 0) return DR_OK;
   const DrTextureArgs args = *a;
-  const bool cube = args.boundary == DR_BOUNDARY_CUBE;
-  return channel_groups(args.channels, [&](auto nc) {
-    constexpr int NC = decltype(nc)::value;
-    if (cube)
-      tex_fwd_kernel<NC, true><<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(args, out);
-    else
-      tex_fwd_kernel<NC, false><<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(args, out);
+  return texture_modes(args, [&](auto nc, auto cube, auto filter, auto boundary) {
+    tex_fwd_kernel<decltype(nc)::value, decltype(cube)::value, decltype(filter)::value,
+                   decltype(boundary)::value>
+        <<<blocks_for(pixels, 256), 256, 0, (hipStream_t)stream>>>(args, out);
     return launch_status();
   });
 }
@@ -657,18 +688,17 @@ extern "C" int dr_texture_backward(const DrTextureArgs* a, const float* grad_out
   if (pixels == 0) return DR_OK;
   if ((int64_t)a->tex_batch * a->num_texels >= 0xffffffffLL) return DR_ERR_ARGUMENT;
   const DrTextureArgs args = *a;
-  const bool cube = args.boundary == DR_BOUNDARY_CUBE;
   const int64_t blocks = tile_blocks(args.batch, args.height, args.width);
   float* g_da = args.uv_da ? grad_uv_da : nullptr;
   float* g_bias = args.bias ? grad_bias : nullptr;
-  return channel_groups(args.channels, [&](auto nc) {
-    constexpr int NC = decltype(nc)::value;
-    if (cube)
-      tex_bwd_kernel<NC, true><<<blocks, 256, 0, (hipStream_t)stream>>>(
-          args, grad_out, grad_texels, grad_uv, g_da, g_bias);
-    else
-      tex_bwd_kernel<NC, false><<<blocks, 256, 0, (hipStream_t)stream>>>(
-          args, grad_out, grad_texels, grad_uv, g_da, g_bias);
+  return texture_modes(args, [&](auto nc, auto cube, auto filter, auto boundary) {
+    // Cube maps read the filter at run time: fixed, the trilinear cube-map kernel holds more
+    // registers (123 against 94 VGPRs) and runs slower.
+    constexpr bool kCube = decltype(cube)::value;
+    constexpr int kFilter = kCube ? kAnyMode : decltype(filter)::value;
+    tex_bwd_kernel<decltype(nc)::value, kCube, kFilter, decltype(boundary)::value>
+        <<<blocks, 256, 0, (hipStream_t)stream>>>(args, grad_out, grad_texels, grad_uv, g_da,
+                                                  g_bias);
     return launch_status();
   });
 }

@@ -490,12 +490,18 @@ __device__ __forceinline__ Deriv4<S> load_deriv4(const S* p) {
   }
 }
 
+// A filter or boundary mode given as a template argument: a DR_FILTER_* or DR_BOUNDARY_* value
+// fixed when compiling (which drops the other modes' code and registers from the kernel), or
+// kAnyMode to read it from the arguments at run time.
+constexpr int kAnyMode = -1;
+
 // CUBE: a.boundary is DR_BOUNDARY_CUBE (the kernels are compiled for both cases, so that the
-// 2D one carries no cube-map state).
-template <class S, bool CUBE>
+// 2D one carries no cube-map state). FILTER: a.filter, or kAnyMode.
+template <class S, bool CUBE, int FILTER = kAnyMode>
 __device__ __forceinline__ void lookup_setup(const DrTextureArgs& a, int64_t pixel, Lookup<S>& K) {
   constexpr bool cube = CUBE;
-  const bool mip = a.filter == DR_FILTER_MIP_NEAREST || a.filter == DR_FILTER_MIP_LINEAR;
+  const int filter = FILTER == kAnyMode ? a.filter : FILTER;
+  const bool mip = filter == DR_FILTER_MIP_NEAREST || filter == DR_FILTER_MIP_LINEAR;
   const S* uv = as<S>(a.uv);
   const S* uv_da = as<S>(a.uv_da);
   K.mip = mip;
@@ -529,7 +535,7 @@ __device__ __forceinline__ void lookup_setup(const DrTextureArgs& a, int64_t pix
   K.level_weight[0] = S(1);
   K.level_weight[1] = S(0);
   if (!mip) {
-    K.levels = a.filter == DR_FILTER_NEAREST ? 0 : 1;
+    K.levels = filter == DR_FILTER_NEAREST ? 0 : 1;
     return;
   }
   S lod = S(0);
@@ -541,7 +547,7 @@ __device__ __forceinline__ void lookup_setup(const DrTextureArgs& a, int64_t pix
   if (K.bad) lod = S(0);
   const bool inside = lod >= S(0) && lod <= (S)top;
   lod = s_min(s_max(lod, S(0)), (S)top);
-  const bool blend = a.filter == DR_FILTER_MIP_LINEAR;
+  const bool blend = filter == DR_FILTER_MIP_LINEAR;
   const int lower = (int)s_floor(lod + (blend ? S(0) : S(0.5)));
   K.level[0] = lower;
   if (blend) {
@@ -576,21 +582,25 @@ __device__ __forceinline__ LevelDims lookup_levels(const DrTextureArgs& a, const
   return D;
 }
 
-template <bool CUBE, class S>
+// BOUNDARY: a.boundary (ignored for cube maps), or kAnyMode.
+template <bool CUBE, int BOUNDARY = kAnyMode, class S>
 __device__ __forceinline__ Bilinear<S> level_setup(const DrTextureArgs& a, const Lookup<S>& K,
                                                    const LevelDims& D, int l) {
-  return bilinear_setup<S, CUBE>(K.s, K.t, K.face, D.h[l], D.w[l], D.off[l],
-                                 CUBE ? (int)DR_BOUNDARY_CUBE : a.boundary);
+  const int boundary =
+      CUBE ? (int)DR_BOUNDARY_CUBE : (BOUNDARY == kAnyMode ? a.boundary : BOUNDARY);
+  return bilinear_setup<S, CUBE>(K.s, K.t, K.face, D.h[l], D.w[l], D.off[l], boundary);
 }
 
-// Nearest: the texel containing the coordinate (reference.py:555-573).
-template <class S>
+// Nearest: the texel containing the coordinate (reference.py:555-573). BOUNDARY: a.boundary,
+// or kAnyMode.
+template <int BOUNDARY = kAnyMode, class S>
 __device__ __forceinline__ bool nearest_setup(const DrTextureArgs& a, const Lookup<S>& K,
                                               int64_t& index, bool& valid) {
   const int h = a.level_height[0], w = a.level_width[0];
-  const Axis<S> X = texel_axis(K.s, w, S(0), a.boundary);
-  const Axis<S> Y = texel_axis(K.t, h, S(0), a.boundary);
-  const int boundary = a.boundary == DR_BOUNDARY_CUBE ? DR_BOUNDARY_CLAMP : a.boundary;
+  const int mode = BOUNDARY == kAnyMode ? a.boundary : BOUNDARY;
+  const Axis<S> X = texel_axis(K.s, w, S(0), mode);
+  const Axis<S> Y = texel_axis(K.t, h, S(0), mode);
+  const int boundary = mode == DR_BOUNDARY_CUBE ? DR_BOUNDARY_CLAMP : mode;
   valid = tap((int)s_floor(Y.x), (int)s_floor(X.x), K.face, h, w, a.level_offset[0], boundary,
               index);
   return X.bad || Y.bad;
