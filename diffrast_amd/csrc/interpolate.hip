@@ -105,7 +105,8 @@ constexpr int kGenericChannels = 4;
 // PPT pixels per thread, in rows or tiles (pixel_slots). The pixels' loads go out level by
 // level -- rast, then the triangles' index rows, then the attribute rows -- so that a thread
 // waits once per level for all its pixels, not once per pixel: the gathers are latency-bound.
-template <int NC, int PPT, bool TILES>
+// DIFF: out_da is written (num_diff > 0); without it the kernel holds no derivative state.
+template <int NC, int PPT, bool TILES, bool DIFF>
 __global__ __launch_bounds__(256) void interp_fwd_kernel(DrInterpolateArgs a,
                                                          float* __restrict__ out,
                                                          float* __restrict__ out_da,
@@ -124,7 +125,7 @@ __global__ __launch_bounds__(256) void interp_fwd_kernel(DrInterpolateArgs a,
   for (int j = 0; j < PPT; ++j) {
     p[j] = pixel_of(a, r[j], s.b[j], rows_per_image);
     db[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (out_da != nullptr && p[j].valid) db[j] = load4(a.rast_db + 4 * pixel[j]);  // du/dx, du/dy, dv/dx, dv/dy
+    if (DIFF && p[j].valid) db[j] = load4(a.rast_db + 4 * pixel[j]);  // du/dx, du/dy, dv/dx, dv/dy
   }
   for (int c0 = 0; c0 < C; c0 += N) {
     float A[PPT][3][N];
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(256) void interp_fwd_kernel(DrInterpolateArgs a,
 #pragma unroll
       for (int c = 0; c < N; ++c)
         res[c] = p[j].valid ? u * A[j][0][c] + v * A[j][1][c] + w * A[j][2][c] : 0.0f;
-      if (out_da != nullptr) {
+      if constexpr (DIFF) {
         float* od = out_da + pixel[j] * 2 * a.num_diff;
         for (int k = 0; k < a.num_diff; ++k) {
           const int c = a.diff[k] - c0;
@@ -164,7 +165,9 @@ __global__ __launch_bounds__(256) void interp_fwd_kernel(DrInterpolateArgs a,
   }
 }
 
-template <int NC>
+// DIFF: num_diff > 0 (grad_db is written, grad_da read if given); without it the kernel holds
+// no derivative state.
+template <int NC, bool DIFF>
 __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
                                                          const float* __restrict__ grad_out,
                                                          const float* __restrict__ grad_da,
@@ -179,7 +182,7 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
   const TilePixel tp = tile_pixel(a.batch, a.height, a.width);
   const int64_t pixel = tp.pixel;
   const int C = NC > 0 ? NC : a.channels;
-  const int D = grad_da != nullptr ? a.num_diff : 0;
+  const int D = DIFF && grad_da != nullptr ? a.num_diff : 0;
   Pixel p;
   p.valid = false;
   p.t = 0;
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
   float4 db = make_float4(0.f, 0.f, 0.f, 0.f);
   if (tp.inside) {
     p = load_pixel(a, pixel, tp.b, rows_per_image);
-    if (p.valid && a.num_diff > 0) db = load4(a.rast_db + 4 * pixel);
+    if (DIFF && p.valid) db = load4(a.rast_db + 4 * pixel);
   }
   const float w = 1.0f - p.u - p.v;
   const float* g = grad_out + (tp.inside ? pixel * C : 0);
@@ -217,7 +220,7 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
       v[N + c] = G[c] * p.v;
       v[2 * N + c] = G[c] * w;
     }
-    if (gd != nullptr && live) {
+    if (DIFF && gd != nullptr && live) {
       for (int k = 0; k < D; ++k) {
         const int c = a.diff[k] - c0;
         if (c < 0 || c >= N) continue;
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
   }
   if (tp.inside) {
     if (grad_rast) store4(grad_rast + 4 * pixel, make_float4(gu, gv, 0.f, 0.f));
-    if (grad_db) store4(grad_db + 4 * pixel, make_float4(g_dudx, g_dudy, g_dvdx, g_dvdy));
+    if (DIFF && grad_db) store4(grad_db + 4 * pixel, make_float4(g_dudx, g_dudy, g_dvdx, g_dvdy));
   }
 }
 
@@ -274,6 +277,12 @@ int dispatch_channels(int channels, F f) {
     case 8: return f(std::integral_constant<int, 8>());
     default: return f(std::integral_constant<int, 0>());
   }
+}
+
+// f(std::true_type) when the call has derivatives, else f(std::false_type).
+template <typename F>
+int with_derivatives(bool diff, F f) {
+  return diff ? f(std::true_type()) : f(std::false_type());
 }
 
 // Attribute rows per image: 0 when shared, else attr_batch_stride / channels.
@@ -314,18 +323,21 @@ extern "C" int dr_interpolate_forward(const DrInterpolateArgs* a, float* out, fl
   const int64_t rows = rows_per_image != 0 ? rows_per_image : args.num_vertices;
   const bool tiles = gather_tiles(12 * (int64_t)args.num_tri + 4 * rows * args.channels);
   return dispatch_channels(args.channels, [&](auto nc) {
-    constexpr int NC = decltype(nc)::value;
-    constexpr int PPT = NC > 0 ? 2 : 1;  // pixels per thread
-    const hipStream_t st = (hipStream_t)stream;
-    if (tiles)
-      interp_fwd_kernel<NC, PPT, true>
-          <<<pixel_slot_blocks<PPT, true>(args.batch, args.height, args.width), 256, 0, st>>>(
-              args, out, da, rows_per_image);
-    else
-      interp_fwd_kernel<NC, PPT, false>
-          <<<pixel_slot_blocks<PPT, false>(args.batch, args.height, args.width), 256, 0, st>>>(
-              args, out, da, rows_per_image);
-    return launch_status();
+    return with_derivatives(args.num_diff > 0, [&](auto diff) {
+      constexpr int NC = decltype(nc)::value;
+      constexpr bool DIFF = decltype(diff)::value;
+      constexpr int PPT = NC > 0 ? 2 : 1;  // pixels per thread
+      const hipStream_t st = (hipStream_t)stream;
+      if (tiles)
+        interp_fwd_kernel<NC, PPT, true, DIFF>
+            <<<pixel_slot_blocks<PPT, true>(args.batch, args.height, args.width), 256, 0, st>>>(
+                args, out, da, rows_per_image);
+      else
+        interp_fwd_kernel<NC, PPT, false, DIFF>
+            <<<pixel_slot_blocks<PPT, false>(args.batch, args.height, args.width), 256, 0,
+               st>>>(args, out, da, rows_per_image);
+      return launch_status();
+    });
   });
 }
 
@@ -338,10 +350,12 @@ extern "C" int dr_interpolate_backward(const DrInterpolateArgs* a, const float* 
   const uint32_t rows_per_image = image_rows(*a);
   const float* gda = a->num_diff > 0 ? grad_out_da : nullptr;
   return dispatch_channels(a->channels, [&](auto nc) {
-    interp_bwd_kernel<decltype(nc)::value>
-        <<<tile_blocks(a->batch, a->height, a->width), 256, 0, (hipStream_t)stream>>>(
-            *a, grad_out, gda, grad_attr, grad_rast, a->num_diff > 0 ? grad_rast_db : nullptr,
-            rows_per_image);
-    return launch_status();
+    return with_derivatives(a->num_diff > 0, [&](auto diff) {
+      interp_bwd_kernel<decltype(nc)::value, decltype(diff)::value>
+          <<<tile_blocks(a->batch, a->height, a->width), 256, 0, (hipStream_t)stream>>>(
+              *a, grad_out, gda, grad_attr, grad_rast, a->num_diff > 0 ? grad_rast_db : nullptr,
+              rows_per_image);
+      return launch_status();
+    });
   });
 }
