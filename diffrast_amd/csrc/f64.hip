@@ -306,10 +306,10 @@ __global__ __launch_bounds__(256) void tex_fwd(DrTextureArgs a, double* out) {
   const double* texels = as<double>(a.texels) + (a.tex_batch > 1 ? image * a.num_texels * C : 0);
   const double nan = tex::s_nan<double>();
   if (K.levels == 0) {
-    int64_t index;
+    uint32_t index;
     bool valid;
     const bool bad = tex::nearest_setup(a, K, index, valid);
-    for (int c = 0; c < C; ++c) o[c] = bad ? nan : (valid ? texels[index * C + c] : 0.0);
+    for (int c = 0; c < C; ++c) o[c] = bad ? nan : (valid ? texels[(int64_t)index * C + c] : 0.0);
     return;
   }
   const tex::LevelDims D = tex::lookup_levels(a, K);
@@ -321,8 +321,8 @@ __global__ __launch_bounds__(256) void tex_fwd(DrTextureArgs a, double* out) {
   for (int c = 0; c < C; ++c) {
     double t0[4], t1[4];
     for (int k = 0; k < 4; ++k) {
-      t0[k] = L0.valid[k] ? texels[L0.index[k] * C + c] : 0.0;
-      t1[k] = two && L1.valid[k] ? texels[L1.index[k] * C + c] : 0.0;
+      t0[k] = L0.valid[k] ? texels[(int64_t)L0.index[k] * C + c] : 0.0;
+      t1[k] = two && L1.valid[k] ? texels[(int64_t)L1.index[k] * C + c] : 0.0;
     }
     double v = tex::bilinear_value(L0, t0);
     if (two) v = v * (1.0 - frac) + tex::bilinear_value(L1, t1) * frac;
@@ -347,11 +347,11 @@ __global__ __launch_bounds__(256) void tex_bwd(DrTextureArgs a, const double* gr
   bool live = !K.dir_invalid;
   double g_s = 0.0, g_t = 0.0, g_lod = 0.0;
   if (live && K.levels == 0) {
-    int64_t index;
+    uint32_t index;
     bool valid;
     const bool bad = tex::nearest_setup(a, K, index, valid);
     if (!bad && valid && gt)
-      for (int c = 0; c < C; ++c) add64(gt + index * C + c, g[c]);
+      for (int c = 0; c < C; ++c) add64(gt + (int64_t)index * C + c, g[c]);
     live = false;  // nearest passes no coordinate gradient
   } else if (live) {
     const tex::LevelDims D = tex::lookup_levels(a, K);
@@ -367,7 +367,7 @@ __global__ __launch_bounds__(256) void tex_bwd(DrTextureArgs a, const double* gr
         double g_fx = 0.0, g_fy = 0.0;
         for (int c = 0; c < C; ++c) {
           double t[4], wgt[4], dfx, dfy;
-          for (int k = 0; k < 4; ++k) t[k] = L[l].valid[k] ? texels[L[l].index[k] * C + c] : 0.0;
+          for (int k = 0; k < 4; ++k) t[k] = L[l].valid[k] ? texels[(int64_t)L[l].index[k] * C + c] : 0.0;
           tex::bilinear_grad(L[l], t, wgt, dfx, dfy);
           const double gl = g[c] * K.level_weight[l];
           g_fx += gl * dfx;
@@ -376,7 +376,7 @@ __global__ __launch_bounds__(256) void tex_bwd(DrTextureArgs a, const double* gr
           if (gt)
             for (int k = 0; k < 4; ++k)
               if (L[l].valid[k] && wgt[k] * K.level_weight[l] != 0.0)
-                add64(gt + L[l].index[k] * C + c, gl * wgt[k]);
+                add64(gt + (int64_t)L[l].index[k] * C + c, gl * wgt[k]);
         }
         if (L[l].pass_x) g_s += g_fx * L[l].size_x;
         if (L[l].pass_y) g_t += g_fy * L[l].size_y;
@@ -888,6 +888,8 @@ extern "C" int dr_interpolate_backward_f64(const DrInterpolateArgs* a, const dou
 
 static bool texture_ok(const DrTextureArgs* a) {
   if (!a || !a->texels || !a->uv || a->batch < 0 || a->height <= 0 || a->width <= 0) return false;
+  // Texel indices within an image's packed buffer are 32-bit.
+  if (a->num_texels < 1 || a->num_texels >= 0xffffffffLL) return false;
   if (a->channels <= 0 || a->tex_batch < 1 || a->num_levels < 1 || a->num_levels > DR_MAX_LEVELS)
     return false;
   if (a->filter < 0 || a->filter > 3 || a->boundary < 0 || a->boundary > 3) return false;

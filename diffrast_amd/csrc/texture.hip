@@ -35,7 +35,7 @@ __device__ __forceinline__ void fetch_taps(const float* __restrict__ texels, con
     if (C == 4 && (reinterpret_cast<uintptr_t>(texels) & 15u) == 0) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const float4 v = L.valid[k] ? *reinterpret_cast<const float4*>(texels + L.index[k] * 4)
+        const float4 v = L.valid[k] ? *reinterpret_cast<const float4*>(texels + (size_t)L.index[k] * 4)
                                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         t[k][0] = v.x;
         t[k][1] = v.y;
@@ -47,7 +47,7 @@ __device__ __forceinline__ void fetch_taps(const float* __restrict__ texels, con
   }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const float* row = texels + L.index[k] * C + c0;
+    const float* row = texels + (size_t)L.index[k] * C + c0;
 #pragma unroll
     for (int c = 0; c < N; ++c) t[k][c] = (L.valid[k] && c0 + c < C) ? row[c] : 0.0f;
   }
@@ -80,10 +80,10 @@ __global__ __launch_bounds__(256) void tex_fwd_kernel(DrTextureArgs a, float* __
   const float* __restrict__ texels = a.texels + image * a.num_texels * C;
   const float nan = __int_as_float(0x7fc00000);
   if (K.levels == 0) {
-    int64_t index;
+    uint32_t index;
     bool valid;
     const bool bad = nearest_setup<BOUNDARY>(a, K, index, valid);
-    for (int c = 0; c < C; ++c) o[c] = bad ? nan : (valid ? texels[index * C + c] : 0.0f);
+    for (int c = 0; c < C; ++c) o[c] = bad ? nan : (valid ? texels[(size_t)index * C + c] : 0.0f);
     return;
   }
   const LevelDims D = lookup_levels(a, K);
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const flo
     live = !K.dir_invalid;
   }
   if (live && K.levels == 0) {
-    int64_t index;
+    uint32_t index;
     bool valid;
     const bool bad = nearest_setup<BOUNDARY>(a, K, index, valid);
     if (!bad && valid) {
@@ -652,6 +652,8 @@ int texture_modes(const DrTextureArgs& a, F f) {
 
 bool valid_args(const DrTextureArgs* a) {
   if (!a || !a->texels || !a->uv || a->batch < 0 || a->height <= 0 || a->width <= 0) return false;
+  // Texel indices within an image's packed buffer are 32-bit.
+  if (a->num_texels < 1 || a->num_texels >= 0xffffffffLL) return false;
   if (a->channels <= 0 || a->tex_batch < 1 || a->num_levels < 1 || a->num_levels > DR_MAX_LEVELS)
     return false;
   if (a->filter < 0 || a->filter > 3 || a->boundary < 0 || a->boundary > 3) return false;

@@ -253,10 +253,11 @@ __device__ __forceinline__ int wrap_index(int i, int n) {
   return r;
 }
 
-// Texel index (in texels from the start of the image's packed buffer) of integer tap
-// (row, col) of a level; false when the tap reads zero (reference.py:636-672).
+// Texel index (in texels from the start of the image's packed buffer, which holds fewer than
+// 2^32 texels) of integer tap (row, col) of a level; false when the tap reads zero
+// (reference.py:636-672).
 __device__ __forceinline__ bool tap(int row, int col, int face, int h, int w, int64_t offset,
-                                    int boundary, int64_t& index) {
+                                    int boundary, uint32_t& index) {
   bool valid = true;
   if (boundary == DR_BOUNDARY_CUBE) {
     valid = cube_fold(face, row, col, w);
@@ -269,7 +270,7 @@ __device__ __forceinline__ bool tap(int row, int col, int face, int h, int w, in
     col = min(max(col, 0), w - 1);
   }
   if (face >= 0) row += face * h;
-  index = offset + (int64_t)row * w + col;
+  index = (uint32_t)offset + (uint32_t)row * (uint32_t)w + (uint32_t)col;
   return valid;
 }
 
@@ -299,7 +300,7 @@ __device__ __forceinline__ AxisPair axis_pair(int i, int n, int boundary) {
 
 template <class S>
 struct Bilinear {
-  int64_t index[4];
+  uint32_t index[4];  // texels from the start of the image's packed buffer (tap())
   bool valid[4];
   S fx, fy;
   bool bad;
@@ -336,7 +337,8 @@ __device__ __forceinline__ Bilinear<S> bilinear_setup(S s, S t, int face, int h,
   } else {
     // The two rows and two columns once each, then the four taps from them.
     const AxisPair R = axis_pair(row, h, boundary), K = axis_pair(col, w, boundary);
-    const int64_t above = offset + (int64_t)R.at[0] * w, below = offset + (int64_t)R.at[1] * w;
+    const uint32_t above = (uint32_t)offset + (uint32_t)R.at[0] * (uint32_t)w;
+    const uint32_t below = (uint32_t)offset + (uint32_t)R.at[1] * (uint32_t)w;
     L.index[0] = above + K.at[0];
     L.index[1] = above + K.at[1];
     L.index[2] = below + K.at[0];
@@ -595,7 +597,7 @@ __device__ __forceinline__ Bilinear<S> level_setup(const DrTextureArgs& a, const
 // or kAnyMode.
 template <int BOUNDARY = kAnyMode, class S>
 __device__ __forceinline__ bool nearest_setup(const DrTextureArgs& a, const Lookup<S>& K,
-                                              int64_t& index, bool& valid) {
+                                              uint32_t& index, bool& valid) {
   const int h = a.level_height[0], w = a.level_width[0];
   const int mode = BOUNDARY == kAnyMode ? a.boundary : BOUNDARY;
   const Axis<S> X = texel_axis(K.s, w, S(0), mode);

@@ -243,7 +243,7 @@ typedef struct DrTextureArgs {
   const float* texels;         /* packed levels */
   int32_t tex_batch;           /* 1 (shared) or batch */
   int32_t channels;
-  int64_t num_texels;          /* texels per batch entry of the packed buffer */
+  int64_t num_texels;          /* texels per batch entry of the packed buffer (< 2^32 - 1) */
   int32_t num_levels;          /* levels a lookup may use (<= DR_MAX_LEVELS) */
   int32_t faces;               /* 1, or 6 for a cube map */
   int32_t level_height[DR_MAX_LEVELS];
