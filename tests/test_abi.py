@@ -64,6 +64,14 @@ def test_argument_checks_before_launch():
     t = _lib.TextureArgs(texels=1, uv=1, tex_batch=1, channels=3, num_levels=40, faces=1,
                          batch=1, height=4, width=4)
     assert lib.dr_texture_forward(ctypes.byref(t), 1, None) == 1001
+    # Texel indices within an image's packed buffer are 32-bit: 2^32 - 1 texels is too many.
+    t.num_levels, t.num_texels = 1, (1 << 32) - 1
+    t.level_height[0] = t.level_width[0] = 4
+    assert lib.dr_texture_forward(ctypes.byref(t), 1, None) == 1001
+    assert lib.dr_texture_backward(ctypes.byref(t), 1, None, None, None, None, None) == 1001
+    t.batch = 0  # in range, and nothing to do
+    t.num_texels = 16
+    assert lib.dr_texture_forward(ctypes.byref(t), 1, None) == 0
     heights = (ctypes.c_int32 * 2)(4, 3)  # 4 halves to 2, not 3
     widths = (ctypes.c_int32 * 2)(4, 2)
     offsets = (ctypes.c_int64 * 2)(0, 16)
