@@ -733,6 +733,7 @@ struct SmallStage {
   float4 tri[256][4];  // the three vertices, then (reach_x, reach_y, row bits, image bits)
   uint2 box[256];      // (x0 | (w - 1) << 20, y0 | (h - 1) << 20), w * h <= small_pixels()
   int start[256];      // first work item of each lane's triangle within its wave
+  uint8_t mark[256 / DR_WAVE][DR_WAVE];  // per wave: lane + 1 at the first item of its triangle
 };
 
 // One thread per triangle instance. A small triangle's pixels become work items of its wave
@@ -787,24 +788,35 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
       }
     }
   }
-  // Small triangles: exclusive prefix of the areas over the wave, then the wave's items.
+  // Small triangles: exclusive prefix of the areas over the wave, then the wave's items, 64
+  // per round. An item's triangle (lane) is found by marks: the lane whose first item falls in
+  // the round marks that place with lane + 1, and a max-scan over the round (marks grow with
+  // the lane) gives each item the last mark at or before it, or the last triangle of the
+  // rounds before.
   const int lane = lane_id();
   const int wave_base = threadIdx.x - lane;
-  int incl = area;
-#pragma unroll
-  for (int d = 1; d < DR_WAVE; d <<= 1) {
-    const int up = __shfl_up(incl, d);
-    if (lane >= d) incl += up;
-  }
-  const int total = __shfl(incl, DR_WAVE - 1);
-  lds.small.start[threadIdx.x] = incl - area;
+  const int incl = (int)wave_inclusive_sum((uint32_t)area);
+  const int total = __builtin_amdgcn_readlane(incl, DR_WAVE - 1);
+  const int first_item = incl - area;
+  lds.small.start[threadIdx.x] = first_item;
+  uint8_t* mark = lds.small.mark[threadIdx.x / DR_WAVE];
   __syncthreads();
-  for (int item = lane; item < total; item += DR_WAVE) {
+  uint32_t carry = 0u;
+  for (int round = 0; round < total; round += DR_WAVE) {  // uniform over the wave
+    mark[lane] = 0;
+    if (area > 0 && first_item >= round && first_item < round + DR_WAVE)
+      mark[first_item - round] = (uint8_t)(lane + 1);
+    // Lanes read marks other lanes of the wave wrote: the fences keep the compiler from
+    // answering the read from this lane's own store.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t owner_mark = max(wave_inclusive_max((uint32_t)mark[lane]), carry);
+    carry = (uint32_t)__builtin_amdgcn_readlane((int)owner_mark, DR_WAVE - 1);
+    const int item = round + lane;
+    if (item >= total) continue;
+    const int j = (int)owner_mark - 1;
     const int* start = lds.small.start + wave_base;
-    int j = 0;  // the last lane whose first item is at or before this one (start[0] = 0)
-#pragma unroll
-    for (int step = DR_WAVE / 2; step >= 1; step >>= 1)
-      if (start[j + step] <= item) j += step;
     const int owner = wave_base + j;
     const float4 v0 = lds.small.tri[owner][0], v1 = lds.small.tri[owner][1];
     const float4 v2 = lds.small.tri[owner][2], extra = lds.small.tri[owner][3];
