@@ -246,6 +246,37 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
     // Pixels of a tile row that show one triangle are summed first, so each run of them makes
     // one table update per vertex.
     const int n = min(N, C - c0);
+    if constexpr (!DIFF) {
+      // One vertex at a time (fewer registers than all three at once), the table's scale set
+      // beforehand from a bound of every value added: a run sum of at most 16 products
+      // G[c] * b_k, each at most max |G| * max |b| (rounding is monotone).
+      float g_max = 0.0f;
+      bool bad = !(isfinite(p.u) && isfinite(p.v) && isfinite(w));
+#pragma unroll
+      for (int c = 0; c < N; ++c) {
+        bad = bad || !isfinite(G[c]);
+        g_max = fmaxf(g_max, fabsf(G[c]));
+      }
+      const float b_max = fmaxf(fmaxf(fabsf(p.u), fabsf(p.v)), fabsf(w));
+      const float bound = bad ? __int_as_float(0x7f800000) : 16.0f * (g_max * b_max);
+      const FixedPass f = table.begin(live ? bound : 0.0f);
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const float b = k == 0 ? p.u : (k == 1 ? p.v : w);
+        float vk[N];
+#pragma unroll
+        for (int c = 0; c < N; ++c) vk[c] = G[c] * b;
+        const bool last = row_run_sums(run_key, vk);
+        if (last && live) table.add_or_global(p.row[k], vk, n, grad_attr + c0, C, f);
+      }
+      __syncthreads();
+      table.flush(grad_attr + c0, C, n, f);
+      if (c0 + N < C) {
+        __syncthreads();
+        table.reset();
+      }
+      continue;
+    }
     const bool last = row_run_sums(run_key, v);
     const bool adds = last && live;
     const FixedPass f = table.begin(adds ? max_magnitude(v, 3 * N) : 0.0f);
