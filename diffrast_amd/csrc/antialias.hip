@@ -168,17 +168,14 @@ __global__ __launch_bounds__(256) void aa_mark_shown(const float* rast, int64_t 
   mask[row * num_tri + (int64_t)id - 1] = kShown;
 }
 
-// Silhouette bits of (pos batch, triangle) i: bit k when edge k has no partner or both
-// triangles lie on one side of it.
-__device__ __forceinline__ void silhouette_bits(const float* pos, int64_t stride,
-                                                const int32_t* tri, int num_tri,
-                                                const int32_t* nbr, int64_t i, uint8_t* mask) {
-  const int b = (int)(i / num_tri);
-  const int t = (int)(i - (int64_t)b * num_tri);
-  const float* P = pos + (int64_t)b * stride;
-  const int v[3] = {tri[3 * t], tri[3 * t + 1], tri[3 * t + 2]};
-  const int partner[3] = {nbr[3 * t], nbr[3 * t + 1], nbr[3 * t + 2]};
+// Silhouette bits of a triangle with vertex rows v in positions P, given the partner edge of
+// each of its edges (-1: none) and the vertex opposite each partner edge (tri[partner]): bit k
+// when edge k has no partner or both triangles lie on one side of it.
+__device__ __forceinline__ uint8_t fold_bits(const float* P, const int (&v)[3],
+                                             const int (&partner)[3], const int (&opposite)[3]) {
   const XYW p[3] = {load_xyw(P, v[0]), load_xyw(P, v[1]), load_xyw(P, v[2])};
+  const XYW q[3] = {load_xyw(P, opposite[0]), load_xyw(P, opposite[1]),
+                    load_xyw(P, opposite[2])};
   uint8_t bits = 0;
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
@@ -196,24 +193,78 @@ __device__ __forceinline__ void silhouette_bits(const float* pos, int64_t stride
     const float line[3] = {__builtin_fmaf(s.y, e.w, -(s.w * e.y)),
                            __builtin_fmaf(s.w, e.x, -(s.x * e.w)),
                            __builtin_fmaf(s.x, e.y, -(s.y * e.x))};
-    const XYW theirs = load_xyw(P, tri[partner[k]]);  // vertex opposite the partner edge
-    if (side(line, p[k]) * side(line, theirs) > 0.0f) bits |= (uint8_t)(1u << k);
+    if (side(line, p[k]) * side(line, q[k]) > 0.0f) bits |= (uint8_t)(1u << k);
   }
-  mask[i] = bits;
+  return bits;
 }
 
-// Silhouette bits of each (pos batch, triangle); with shown_only, of the marked ones only (the
-// others stay 0).
+// The partner edges of triangle t and the vertices opposite them (row 0 where there is none).
+__device__ __forceinline__ void partners(const int32_t* tri, const int32_t* nbr, int t,
+                                         int (&v)[3], int (&partner)[3], int (&opposite)[3]) {
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    v[k] = tri[3 * t + k];
+    partner[k] = nbr[3 * t + k];
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) opposite[k] = partner[k] >= 0 ? tri[partner[k]] : 0;
+}
+
+// Silhouette bits of (pos batch, triangle) i.
+__device__ __forceinline__ void silhouette_bits(const float* pos, int64_t stride,
+                                                const int32_t* tri, int num_tri,
+                                                const int32_t* nbr, int64_t i, uint8_t* mask) {
+  const int b = (int)(i / num_tri);
+  const int t = (int)(i - (int64_t)b * num_tri);
+  int v[3], partner[3], opposite[3];
+  partners(tri, nbr, t, v, partner, opposite);
+  mask[i] = fold_bits(pos + (int64_t)b * stride, v, partner, opposite);
+}
+
+// Silhouette bits of every (pos batch, triangle).
 __global__ __launch_bounds__(256) void aa_silhouette_kernel(const float* pos, int64_t stride,
                                                             int pos_batch, const int32_t* tri,
                                                             int num_tri, const int32_t* nbr,
-                                                            bool shown_only, uint8_t* mask) {
-  // A grid-stride loop: with shown_only most entries end at their mask byte, and one thread
-  // per entry would spend the pass launching workgroups.
+                                                            uint8_t* mask) {
   const int64_t n = (int64_t)pos_batch * num_tri;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    if (!shown_only || mask[i] == kShown) silhouette_bits(pos, stride, tri, num_tri, nbr, i, mask);
+       i += (int64_t)gridDim.x * blockDim.x)
+    silhouette_bits(pos, stride, tri, num_tri, nbr, i, mask);
+}
+
+// Silhouette bits of the marked (pos batch, triangle) entries only (the others stay 0): one
+// thread per triangle, over the batch entries it is marked in. Its index row, partners and
+// opposite vertices are read once for every entry, together with the marks of eight entries at
+// a time, so that a thread waits for two rounds of loads and then one per entry it is marked
+// in, not three per (entry, triangle) in turn: the pass is bound by the latency of its gathers.
+__global__ __launch_bounds__(256) void aa_silhouette_shown_kernel(const float* pos,
+                                                                  int64_t stride, int pos_batch,
+                                                                  const int32_t* tri,
+                                                                  int num_tri, const int32_t* nbr,
+                                                                  uint8_t* mask) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= num_tri) return;
+  int v[3], partner[3], opposite[3];
+  bool rows = false;
+  constexpr int kGroup = 8;
+  for (int b0 = 0; b0 < pos_batch; b0 += kGroup) {
+    uint8_t marks[kGroup];
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j)
+      marks[j] = b0 + j < pos_batch ? mask[(int64_t)(b0 + j) * num_tri + t] : 0;
+    if (!rows) {
+      partners(tri, nbr, t, v, partner, opposite);  // issued before the marks are waited for
+      rows = true;
+    }
+    uint32_t shown = 0u;
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) shown |= (marks[j] == kShown ? 1u : 0u) << j;
+    while (shown != 0u) {
+      const int j = __ffs(shown) - 1;
+      shown &= shown - 1u;
+      const int64_t b = b0 + j;
+      mask[b * num_tri + t] = fold_bits(pos + b * stride, v, partner, opposite);
+    }
   }
 }
 
@@ -829,8 +880,12 @@ extern "C" int dr_silhouette_mask(const float* pos, int64_t pos_batch_stride, in
       aa_mark_shown<<<blocks_for(pixels, 256), 256, 0, s>>>(rast, image_pixels, pixels, num_tri,
                                                            pos_batch, mask);
   }
-  aa_silhouette_kernel<<<(int)std::min<int64_t>(blocks_for(n, 256), 4096), 256, 0, s>>>(
-      pos, pos_batch_stride, pos_batch, tri, num_tri, neighbours, rast != nullptr, mask);
+  if (rast != nullptr)
+    aa_silhouette_shown_kernel<<<blocks_for(num_tri, 256), 256, 0, s>>>(
+        pos, pos_batch_stride, pos_batch, tri, num_tri, neighbours, mask);
+  else
+    aa_silhouette_kernel<<<(int)std::min<int64_t>(blocks_for(n, 256), 4096), 256, 0, s>>>(
+        pos, pos_batch_stride, pos_batch, tri, num_tri, neighbours, mask);
   return launch_status();
 }
 
