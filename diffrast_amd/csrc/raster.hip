@@ -1295,7 +1295,9 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
     }
 
     int items = 0;
-    if (staged) {
+    // A staged triangle behind the farthest key as it is now makes no items: nothing of it is
+    // kept.
+    if (staged && !(cull && bound > far_depth)) {
 #pragma unroll
       for (int k = 0; k < 3; ++k) s_tri[threadIdx.x][k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
       T.reach_x = reach(T.x, T.w);
@@ -1308,8 +1310,7 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
       s_reach[threadIdx.x] = make_float2(T.reach_x, T.reach_y);
       asm volatile("" : "+v"(tri_row));  // keeps the mask (and the wait for the load) here
       s_row[threadIdx.x] = tri_row & 0xffffffu;
-      const bool behind = cull && bound > far_depth;
-      if (bx0 <= bx1 && by0 <= by1 && !behind) {
+      if (bx0 <= bx1 && by0 <= by1) {
         RowSpans se = {};
         const bool spans =
             span_setup(T.x, T.y, T.w, T.reach_x, T.reach_y, g.width, tile_x0, se);
