@@ -113,13 +113,27 @@ DR_HD bool covers(const float* x, const float* y, const float* z, const float* w
 // the margin is twice that plus 2^-16. An edge whose index-space coefficients exceed 2^30
 // (nearly parallel to the rows) is left out: fewer constraints, a wider span.
 
+// Which side an edge bounds is the sign of S_k = sg Wy_k, and with every w > 0 that is the sign
+// of Y_j - Y_i (Y = y / w, the projected row coordinate; the float64 Wy_k is a rounded difference
+// of exact products, so it keeps the exact sign). The three differences Y_j - Y_i around the
+// triangle sum to 0, so at most two edges bound a row from above and at most two from below.
+
 struct RowSpans {
   // Column bounds relative to the column origin x0 given to span_setup(), for the row centre py:
-  // col <= hi_u[k] + hi_v[k] * py and col >= lo_u[k] + lo_v[k] * py for every k (+-inf and 0 for
-  // an edge that is not such a bound), and the row is empty when row_u + row_v * py < 0.
-  float hi_u[3], hi_v[3], lo_u[3], lo_v[3];
+  // col <= hi_u[k] + hi_v[k] * py and col >= lo_u[k] + lo_v[k] * py for k = 0, 1 (+-inf and 0
+  // where fewer edges bound that side), and the row is empty when row_u + row_v * py < 0.
+  float hi_u[2], hi_v[2], lo_u[2], lo_v[2];
   float row_u, row_v;
 };
+
+// Bounds that constrain nothing: every column of every row.
+DR_HD void no_spans(RowSpans& s) {
+  s.hi_u[0] = s.hi_u[1] = HUGE_VALF;
+  s.lo_u[0] = s.lo_u[1] = -HUGE_VALF;
+  s.hi_v[0] = s.hi_v[1] = s.lo_v[0] = s.lo_v[1] = 0.0f;
+  s.row_u = 1.0f;
+  s.row_v = 0.0f;
+}
 
 // 1 / S (S finite and non-zero) for the span bounds. On the GPU: the hardware's approximate
 // reciprocal and two Newton steps (a relative error far below 2^-50 from any start better than
@@ -136,12 +150,13 @@ DR_HD double span_recip(double S) {
 }
 
 // Bounds of the row spans of triangle (x, y, w) in an image `width` pixels across, as column
-// offsets from x0; false when the triangle gets no spans. Formed in double, then rounded to
-// float with a margin of 2^-21 (|u| + |v|) that covers the rounding of the float evaluation in
-// row_span() (at most about 2 eps (|u| + |v|) for |py| <= 1); an edge whose coefficients
-// reach 2^30 is left out.
+// offsets from x0; false when the triangle gets no spans (s then constrains nothing: the whole
+// box is tested). Formed in double, then rounded to float with a margin of 2^-21 (|u| + |v|)
+// that covers the rounding of the float evaluation in row_span() (at most about 2 eps
+// (|u| + |v|) for |py| <= 1); an edge whose coefficients reach 2^30 is left out.
 DR_HD bool span_setup(const float* x, const float* y, const float* w, float reach_x,
                       float reach_y, int width, int x0, RowSpans& s) {
+  no_spans(s);
   if (!(w[0] > 0.0f && w[1] > 0.0f && w[2] > 0.0f)) return false;
   double K[3], Xw[3], Wy[3];
   for (int k = 0; k < 3; ++k) {
@@ -156,48 +171,71 @@ DR_HD bool span_setup(const float* x, const float* y, const float* w, float reac
   const double sg = det > 0.0 ? 1.0 : -1.0;
   const double half = 0.5 * (double)width;
   const double m = ldexp((double)width, -22) + 0x1p-16;
-  const float inf = HUGE_VALF;
-  s.row_u = 1.0f;
-  s.row_v = 0.0f;
+  RowSpans t;
+  no_spans(t);
+  int highs = 0, lows = 0;
   for (int k = 0; k < 3; ++k) {
-    s.hi_u[k] = inf;
-    s.lo_u[k] = -inf;
-    s.hi_v[k] = s.lo_v[k] = 0.0f;
     const double S = sg * Wy[k], U = sg * K[k] + B, V = -sg * Xw[k];
     if (S == 0.0) {  // at most one edge: two would make the triangle degenerate
-      s.row_u = (float)(U + ldexp(fabs(U) + fabs(V), -21));
-      s.row_v = (float)V;
+      t.row_u = (float)(U + ldexp(fabs(U) + fabs(V), -21));
+      t.row_v = (float)V;
       continue;
     }
     const double inv = span_recip(S);
     const double u = (U * inv + 1.0) * half - 0.5 - (double)x0, v = V * inv * half;
     if (!(fabs(u) < 0x1p30 && fabs(v) < 0x1p30)) continue;
     const double slack = m + ldexp(fabs(u) + fabs(v), -21);
+    // A third bound on one side would contradict the sign argument above; were it ever to
+    // happen, the triangle would get no spans (its whole box tested), never a wrong one.
+    // (Slots by constant index: a run-time index would put t in scratch memory on the GPU.)
     if (S > 0.0) {
-      s.hi_u[k] = (float)(u + slack);
-      s.hi_v[k] = (float)v;
+      if (highs == 2) return false;
+      const float bu = (float)(u + slack), bv = (float)v;
+      if (highs++ == 0) {
+        t.hi_u[0] = bu;
+        t.hi_v[0] = bv;
+      } else {
+        t.hi_u[1] = bu;
+        t.hi_v[1] = bv;
+      }
     } else {
-      s.lo_u[k] = (float)(u - slack);
-      s.lo_v[k] = (float)v;
+      if (lows == 2) return false;
+      const float bu = (float)(u - slack), bv = (float)v;
+      if (lows++ == 0) {
+        t.lo_u[0] = bu;
+        t.lo_v[0] = bv;
+      } else {
+        t.lo_u[1] = bu;
+        t.lo_v[1] = bv;
+      }
     }
   }
+  s = t;
   return true;
 }
 
-// Column offsets [lo, hi] of row centre py (float, as covers() gets it) that may be covered,
-// clipped to [lo, hi] as given; lo > hi for none.
+// Column offsets of row centre py (float, as covers() gets it) that may be covered, clipped to
+// [lo, hi] as given (floats holding integers): on return lo = the first, hi = the last, both
+// integers within the given range when lo <= hi; lo > hi (or NaN) for none.
+DR_HD void row_bounds(const RowSpans& s, float py, float& lo, float& hi) {
+  const float h = fminf(fminf(fmaf(s.hi_v[0], py, s.hi_u[0]), fmaf(s.hi_v[1], py, s.hi_u[1])), hi);
+  const float l = fmaxf(fmaxf(fmaf(s.lo_v[0], py, s.lo_u[0]), fmaf(s.lo_v[1], py, s.lo_u[1])), lo);
+  const bool row = !(fmaf(s.row_v, py, s.row_u) < 0.0f);
+  lo = ceilf(l);
+  hi = row ? floorf(h) : -HUGE_VALF;
+}
+
+// The same in integers: [lo, hi] clipped to the given range (|lo|, |hi| < 2^24); lo > hi for none.
 DR_HD void row_span(const RowSpans& s, float py, int& lo, int& hi) {
-  const float h = fminf(fminf(fmaf(s.hi_v[0], py, s.hi_u[0]), fmaf(s.hi_v[1], py, s.hi_u[1])),
-                        fmaf(s.hi_v[2], py, s.hi_u[2]));
-  const float l = fmaxf(fmaxf(fmaf(s.lo_v[0], py, s.lo_u[0]), fmaf(s.lo_v[1], py, s.lo_u[1])),
-                        fmaf(s.lo_v[2], py, s.lo_u[2]));
-  if (fmaf(s.row_v, py, s.row_u) < 0.0f) {
+  float l = (float)lo, h = (float)hi;
+  row_bounds(s, py, l, h);
+  if (l <= h) {
+    lo = (int)l;
+    hi = (int)h;
+  } else {
     lo = 1;
     hi = 0;
-    return;
   }
-  lo = (int)ceilf(fmaxf(l, (float)lo));
-  hi = (int)floorf(fminf(h, (float)hi));
 }
 
 }  // namespace dr

@@ -1150,7 +1150,7 @@ __global__ __launch_bounds__(256) void raster_tile_place(Workspace ws) {
 // One workgroup per tile: the tile's keys stay in LDS while it walks the tile's binned
 // triangles near to far (its depth-slab lists are one range of the entry array), kChunk at a
 // time. Each chunk is staged in LDS together with, per row of the tile, the columns its pixel
-// centres may cover (row_span(); the whole row of the box for a triangle without spans). The
+// centres may cover (row_bounds(); the whole row of the box for a triangle without spans). The
 // pixels of all those row spans form one list of work items, which the 256 threads walk in
 // steps of 256, so every lane has a pixel to test whatever the span lengths. The list is mapped
 // kWindow items at a time: each triangle writes (its first item, itself) at its first item of
@@ -1160,11 +1160,9 @@ __global__ __launch_bounds__(256) void raster_tile_place(Workspace ws) {
 // bounds what can still win: triangles entirely behind it are skipped, and so are single pixels
 // that already hold a nearer key. The improved keys are stored once at the end.
 template <bool kLoop>
-__global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
-                                                          const uint64_t* prev, uint64_t* keys,
-                                                          Workspace ws,
-                                                          const uint2* entries,
-                                                          uint32_t capacity) {
+__device__ __forceinline__ void tile_pass(const DrRasterGeometry& g, const uint64_t* prev,
+                                          uint64_t* keys, const Workspace& ws,
+                                          const uint2* entries, uint32_t capacity) {
   // Per staged triangle: the three vertices, (reach_x, reach_y) and its row of tri.
   __shared__ float4 s_tri[kChunk][3];
   __shared__ float2 s_reach[kChunk];
@@ -1190,8 +1188,8 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   // k (for a batch of 8 images, one image), so the records that neighbouring tiles share stay in
   // one L2, heaviest first. The grid is a multiple of 8 and workgroup b takes slot b / 8 of its
   // share; with kLoop also slots b / 8 + grid / 8, b / 8 + 2 grid / 8, ..., so that a grid
-  // sized before the shares were known still covers every tile. (The loop costs registers:
-  // 90 VGPRs and five waves per SIMD instead of 80 and six, so it is compiled only for that.)
+  // sized before the shares were known still covers every tile. (The loop costs registers, so
+  // it is compiled only for that.)
   const int share = (int)(blockIdx.x % kXcdShares);
   // Lists that did not fit the entry buffer were not binned: nothing to read (the overflow
   // pass rasterizes the binned triangles instead).
@@ -1311,22 +1309,29 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
       asm volatile("" : "+v"(tri_row));  // keeps the mask (and the wait for the load) here
       s_row[threadIdx.x] = tri_row & 0xffffffu;
       if (bx0 <= bx1 && by0 <= by1) {
-        RowSpans se = {};
-        const bool spans =
-            span_setup(T.x, T.y, T.w, T.reach_x, T.reach_y, g.width, tile_x0, se);
-        int held = 0;
-        for (int r = by0; r <= by1; ++r) {
-          int lo = bx0, hi = bx1;
-          if (spans) row_span(se, s_py[r], lo, hi);
+        // (A triangle without spans gets bounds that constrain nothing: its box's whole rows.)
+        RowSpans se;
+        // (The tile's column origin as an opaque scalar: hoisted out of the chunk loop as a
+        // double, it would be spilled at the 96-VGPR budget.)
+        int x0 = tile_x0;
+        asm volatile("" : "+s"(x0));
+        span_setup(T.x, T.y, T.w, T.reach_x, T.reach_y, g.width, x0, se);
+        const float fx0 = (float)bx0, fx1 = (float)bx1;
+        uint16_t* out = s_span[threadIdx.x];
+        uint32_t code = (uint32_t)by0;  // items so far << 8 | row
+        for (int r = by0; r <= by1; ++r, ++code) {
+          float lo = fx0, hi = fx1;
+          row_bounds(se, s_py[r], lo, hi);
           // Every pixel of the row already holds a key nearer than the triangle can reach (an
           // empty key reads as NaN and never compares greater).
-          if (bound > s_row_far[r]) hi = lo - 1;
-          if (lo <= hi) {
-            s_span[threadIdx.x][held++] = (uint16_t)(items << 8 | lo << 4 | r);
-            items += hi - lo + 1;
+          if (bound > s_row_far[r]) hi = -__int_as_float(0x7f800000);
+          if (lo <= hi) {  // then 0 <= lo <= hi <= 15, integers
+            *out++ = (uint16_t)(code | (uint32_t)lo << 4);
+            code += ((uint32_t)(hi - lo) + 1u) << 8;
           }
         }
-        s_spans[threadIdx.x] = (uint8_t)held;
+        s_spans[threadIdx.x] = (uint8_t)(out - s_span[threadIdx.x]);
+        items = (int)(code >> 8);
       }
     }
     // Exclusive prefix of the item counts over the workgroup.
@@ -1419,6 +1424,29 @@ __global__ __launch_bounds__(256) void raster_tile_kernel(DrRasterGeometry g,
   if (!kLoop) break;
   __syncthreads();  // the next tile's set-up reuses the LDS
   }
+}
+
+// The tile pass's two kernels. Without the loop over tiles it fits five waves per SIMD, as many
+// as its LDS allows, when the compiler keeps it to 96 VGPRs (it needs a few more otherwise, and
+// four waves are ~12 % slower); the looping kernel would spill at that budget and keeps its own.
+template <bool kLoop>
+__global__ void raster_tile_kernel(DrRasterGeometry g, const uint64_t* prev, uint64_t* keys,
+                                   Workspace ws, const uint2* entries, uint32_t capacity);
+
+template <>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void
+raster_tile_kernel<false>(DrRasterGeometry g, const uint64_t* prev, uint64_t* keys, Workspace ws,
+                          const uint2* entries, uint32_t capacity) {
+  tile_pass<false>(g, prev, keys, ws, entries, capacity);
+}
+
+template <>
+__global__ __launch_bounds__(256) void raster_tile_kernel<true>(DrRasterGeometry g,
+                                                                const uint64_t* prev,
+                                                                uint64_t* keys, Workspace ws,
+                                                                const uint2* entries,
+                                                                uint32_t capacity) {
+  tile_pass<true>(g, prev, keys, ws, entries, capacity);
 }
 
 // Visibility of the binned triangles when their tile lists did not fit the entry buffer (the
