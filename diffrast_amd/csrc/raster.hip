@@ -619,10 +619,11 @@ __global__ __launch_bounds__(256) void order_place(DrRasterGeometry g, Workspace
 
 // Nearest and farthest depth z / w, clipped to [-1, 1], of the vertices in front of the camera,
 // per image (or once when pos is shared): the span the depth slabs divide. Each of
-// kRangeParts workgroups per image reduces a share of its vertices to a partial span; a second
-// pass merges the partial spans (no atomics on a handful of addresses).
-__global__ __launch_bounds__(256) void raster_depth_range(DrRasterGeometry g, Workspace ws) {
-  __shared__ uint32_t s_lo[256 / DR_WAVE], s_hi[256 / DR_WAVE];
+// kRangeParts workgroups of 1024 threads per image reduces a share of its vertices to a partial
+// span (1024 threads: enough waves to keep the loads in flight with 64 workgroups per image); a
+// second pass merges the partial spans (no atomics on a handful of addresses).
+__global__ __launch_bounds__(1024) void raster_depth_range(DrRasterGeometry g, Workspace ws) {
+  __shared__ uint32_t s_lo[1024 / DR_WAVE], s_hi[1024 / DR_WAVE];
   const int image = blockIdx.x / kRangeParts, part = blockIdx.x % kRangeParts;
   const float* P = g.pos + (int64_t)image * g.pos_batch_stride;
   // Four vertices per thread and step, loaded before any is used; the span only places
@@ -657,7 +658,7 @@ __global__ __launch_bounds__(256) void raster_depth_range(DrRasterGeometry g, Wo
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 256 / DR_WAVE; ++w) {
+    for (int w = 1; w < 1024 / DR_WAVE; ++w) {
       lo = min(lo, s_lo[w]);
       hi = max(hi, s_hi[w]);
     }
@@ -802,6 +803,11 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
   uint8_t* mark = lds.small.mark[threadIdx.x / DR_WAVE];
   __syncthreads();
   uint32_t carry = 0u;
+  // Pixel centres (2 i + 1) / size - 1: for a power-of-two size the quotient is the exact
+  // product with 1 / size (2 i + 1 < 2^24), so three instructions give pixel_centre()'s bits
+  // without the table's dependent load; other sizes read the table.
+  const bool pow2 = (g.width & (g.width - 1)) == 0 && (g.height & (g.height - 1)) == 0;
+  const float inv_w = 1.0f / (float)g.width, inv_h = 1.0f / (float)g.height;
   for (int round = 0; round < total; round += DR_WAVE) {  // uniform over the wave
     mark[lane] = 0;
     if (area > 0 && first_item >= round && first_item < round + DR_WAVE)
@@ -826,8 +832,16 @@ __global__ __launch_bounds__(256) void raster_setup_kernel(DrRasterGeometry g,
     const int x = (int)(box.x & 0xfffffu) + dx, y = (int)(box.y & 0xfffffu) + dy;
     const float X[3] = {v0.x, v1.x, v2.x}, Y[3] = {v0.y, v1.y, v2.y};
     const float Z[3] = {v0.z, v1.z, v2.z}, Wv[3] = {v0.w, v1.w, v2.w};
+    float cx, cy;
+    if (pow2) {  // uniform
+      cx = (float)(2 * x + 1) * inv_w - 1.0f;
+      cy = (float)(2 * y + 1) * inv_h - 1.0f;
+    } else {
+      cx = ws.px[x];
+      cy = ws.py[y];
+    }
     float depth;
-    if (covers(X, Y, Z, Wv, extra.x, extra.y, ws.px[x], ws.py[y], depth)) {
+    if (covers(X, Y, Z, Wv, extra.x, extra.y, cx, cy, depth)) {
       const int64_t pixel = ((int64_t)__float_as_int(extra.w) * g.height + y) * g.width + x;
       merge_key(keys, prev, pixel, depth_key(depth, (uint32_t)__float_as_int(extra.z)));
     }
@@ -1796,7 +1810,7 @@ static int queue_visibility_start(const DrRasterGeometry* g, const uint64_t* pre
   if (g->num_instances > 0) {
     if (ws.ordered && g->order == nullptr) queue_order(*g, ws, s);
     if (ws.slabs > 1) {  // the depth span places binned triangles in slabs
-      raster_depth_range<<<ws.depth_ranges * kRangeParts, 256, 0, s>>>(*g, ws);
+      raster_depth_range<<<ws.depth_ranges * kRangeParts, 1024, 0, s>>>(*g, ws);
       raster_depth_range_merge<<<ws.depth_ranges, kRangeParts, 0, s>>>(ws);
     }
     raster_setup_kernel<<<blocks_for(g->num_instances, 256), 256, 0, s>>>(*g, prev_keys, keys,
