@@ -175,10 +175,13 @@ __device__ __forceinline__ void level_taps(const Bilinear<float>& L, float level
   }
 }
 
+// The 2D kernels are held to 72 VGPRs: seven waves per SIMD, as many as the table's LDS allows
+// (measured: 393 -> 388 us at 8 x 1024^2 with a 1024^2 texture, against six waves at 74 VGPRs;
+// the cube-map kernels spill at such budgets and keep their own).
 template <int NC, bool CUBE, int FILTER, int BOUNDARY>
-__global__ __launch_bounds__(256) void tex_bwd_kernel(DrTextureArgs a, const float* grad_out,
-                                                      float* grad_texels, float* grad_uv,
-                                                      float* grad_uv_da, float* grad_bias) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CUBE ? 1 : 7))) void
+tex_bwd_kernel(DrTextureArgs a, const float* grad_out, float* grad_texels, float* grad_uv,
+               float* grad_uv_da, float* grad_bias) {
   using Table = RowTable<512, 4>;
   __shared__ Table table;
   table.init();
