@@ -431,10 +431,13 @@ template <int SLOTS, int CH>
 struct RowTable {
   static constexpr uint32_t kEmpty = 0xffffffffu;
   static constexpr int kProbe = 16;
-  static_assert((SLOTS & (SLOTS - 1)) == 0 && CH % 2 == 0, "power-of-two slots, even CH");
+  static_assert((SLOTS & (SLOTS - 1)) == 0 && CH % 2 == 0 && SLOTS <= 65536,
+                "power-of-two slots (at most 2^16), even CH");
   uint32_t keys[SLOTS];
   long long vals[CH * SLOTS];  // channel-major: lanes adding to different rows hit different banks
-  uint32_t used[SLOTS];
+  // The slots in use, in 16 bits: a 512 x 4 table then needs 19.5 KB of LDS, under the 20 KB
+  // that lets eight workgroups share a CU.
+  uint16_t used[SLOTS];
   uint32_t count;
   float wave_max[256 / DR_WAVE];
   int wave_bad[256 / DR_WAVE];
@@ -493,7 +496,7 @@ struct RowTable {
       if (seen == kEmpty) {
         seen = atomicCAS(keys + slot, kEmpty, key);
         if (seen == kEmpty) {
-          used[atomicAdd(&count, 1u)] = slot;
+          used[atomicAdd(&count, 1u)] = (uint16_t)slot;
           return (int)slot;
         }
         if (seen == key) return (int)slot;
