@@ -424,7 +424,11 @@ __global__ __launch_bounds__(256) void mip_up(float* grad, int C, int64_t num_te
 // a texel is ((a / 4 + b / 4) + c / 4) + d / 4 of its children in row-major order, and in the
 // adjoint a child adds a quarter of its parent's total.
 
-constexpr int kMipStageLevels = 6;  // at most 64 x 64 bottom texels per tile: 32 x 32 above
+// At most 32 x 32 bottom texels per tile (16 x 16 above it in LDS): a 1024^2 level gives 1024
+// workgroups, and the chain above 32^2 is one more single-workgroup stage. (Tiles of 64 x 64
+// gave a quarter as many workgroups and 32 KB of LDS each: mip chain 1024^2 x 4, built and
+// folded back, 63 -> 53 us; tiles of 16 x 16 need a third stage, 66 us.)
+constexpr int kMipStageLevels = 5;
 
 // Up to four channels of texel p (n valid; vec: four channels on a 16-byte aligned buffer).
 __device__ __forceinline__ float4 load_texel(const float* p, int n, bool vec) {
