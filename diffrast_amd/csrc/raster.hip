@@ -989,7 +989,12 @@ __global__ __launch_bounds__(256) void raster_scan_apply(const uint32_t* counts,
 }
 
 // Fills the per-tile lists: the workgroup counts its records per tile in LDS, reserves its
-// share of each tile's list with one global atomic, then writes the entries.
+// share of each tile's list with one global atomic, then writes the entries. A workgroup takes
+// the records of kBinBlocks consecutive setup workgroups (neighbours in the processing order,
+// so they share tiles): fewer reservations, and fewer workgroups waiting on their round trip
+// (bin pass 186 -> 163 us at 8 x 1024^2 with two; 172 us with four).
+constexpr int kBinBlocks = 2;
+
 __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint2* entries,
                                                          uint32_t capacity) {
   // Entries beyond the buffer's capacity: the pass is left to a later launch with a larger
@@ -998,26 +1003,35 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint2* en
   __shared__ TileTable table;
   table.clear();
   __syncthreads();
-  // The records of setup workgroup blockIdx.x.
-  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
-  int tx0 = 0, tx1 = -1, ty0 = 0, ty1 = -1;
-  uint32_t list0 = 0u, bound_bits = 0u;
-  if (threadIdx.x < ws.block_records[blockIdx.x]) {
-    // Each entry carries the triangle's depth bound, so that the tile pass can skip a
-    // triangle behind every key of its tile without reading its record.
-    const uint4 info = ws.record_bins[r];
-    tx0 = (int)(info.x & 0xffffu);
-    tx1 = (int)(info.x >> 16);
-    ty0 = (int)(info.y & 0xffffu);
-    ty1 = (int)(info.y >> 16);
-    list0 = info.z;
-    bound_bits = info.w;
-  }
-  for (int ty = ty0; ty <= ty1; ++ty)
-    for (int tx = tx0; tx <= tx1; ++tx) {
-      const int slot = table.insert(list0 + (uint32_t)(ty * ws.tiles_x + tx) * ws.slabs);
-      if (slot >= 0) atomicAdd(table.count + slot, 1u);
+  // This thread's record of each of the workgroup's setup workgroups: tile range, first list,
+  // and the triangle's depth bound, which each entry carries so that the tile pass can skip a
+  // triangle behind every key of its tile without reading its record.
+  int tx0[kBinBlocks], tx1[kBinBlocks], ty0[kBinBlocks], ty1[kBinBlocks];
+  uint32_t list0[kBinBlocks], bound_bits[kBinBlocks], rec[kBinBlocks];
+#pragma unroll
+  for (int q = 0; q < kBinBlocks; ++q) {
+    const int block = (int)blockIdx.x * kBinBlocks + q;
+    tx0[q] = ty0[q] = 0;
+    tx1[q] = ty1[q] = -1;
+    list0[q] = bound_bits[q] = 0u;
+    rec[q] = (uint32_t)block * 256u + threadIdx.x;
+    if (block < ws.record_blocks && threadIdx.x < ws.block_records[block]) {
+      const uint4 info = ws.record_bins[rec[q]];
+      tx0[q] = (int)(info.x & 0xffffu);
+      tx1[q] = (int)(info.x >> 16);
+      ty0[q] = (int)(info.y & 0xffffu);
+      ty1[q] = (int)(info.y >> 16);
+      list0[q] = info.z;
+      bound_bits[q] = info.w;
     }
+  }
+#pragma unroll
+  for (int q = 0; q < kBinBlocks; ++q)
+    for (int ty = ty0[q]; ty <= ty1[q]; ++ty)
+      for (int tx = tx0[q]; tx <= tx1[q]; ++tx) {
+        const int slot = table.insert(list0[q] + (uint32_t)(ty * ws.tiles_x + tx) * ws.slabs);
+        if (slot >= 0) atomicAdd(table.count + slot, 1u);
+      }
   __syncthreads();
   // The reservations: each thread's slots' atomics are all issued before it waits for any.
   constexpr int kSlotsPerThread = kTileSlots / 256;
@@ -1036,15 +1050,19 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint2* en
     table.count[s] = 0u;
   }
   __syncthreads();
-  for (int ty = ty0; ty <= ty1; ++ty)
-    for (int tx = tx0; tx <= tx1; ++tx) {
-      const uint32_t list = list0 + (uint32_t)(ty * ws.tiles_x + tx) * ws.slabs;
-      const int slot = table.find(list);
-      const uint32_t at = slot >= 0 ? table.base[slot] + atomicAdd(table.count + slot, 1u)
-                                    : atomicAdd(ws.list_cursor + list, 1u);
-      entries[at] = make_uint2(r, bound_bits);
-    }
+#pragma unroll
+  for (int q = 0; q < kBinBlocks; ++q)
+    for (int ty = ty0[q]; ty <= ty1[q]; ++ty)
+      for (int tx = tx0[q]; tx <= tx1[q]; ++tx) {
+        const uint32_t list = list0[q] + (uint32_t)(ty * ws.tiles_x + tx) * ws.slabs;
+        const int slot = table.find(list);
+        const uint32_t at = slot >= 0 ? table.base[slot] + atomicAdd(table.count + slot, 1u)
+                                      : atomicAdd(ws.list_cursor + list, 1u);
+        entries[at] = make_uint2(rec[q], bound_bits[q]);
+      }
 }
+
+static int bin_grid(const Workspace& ws) { return (ws.record_blocks + kBinBlocks - 1) / kBinBlocks; }
 
 // ---- tile order: heavy tiles first within each XCD's share -----------------------------------
 //
@@ -1877,7 +1895,7 @@ static int queue_visibility(const DrRasterGeometry* g, const uint64_t* prev_keys
   if ((int64_t)g->batch * g->height * g->width == 0 || g->num_instances == 0) return DR_OK;
   Workspace ws = layout(*g, (char*)workspace);
   if (capacity > 0) {
-    raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, entries, capacity);
+    raster_bin_kernel<<<bin_grid(ws), 256, 0, s>>>(ws, entries, capacity);
     launch_tile_pass(*g, prev_keys, keys, ws, entries, capacity, tile_groups, s);
   }
   raster_overflow_kernel<<<overflow_grid(ws), 256, 0, s>>>(*g, prev_keys, keys, ws, capacity);
@@ -2000,7 +2018,7 @@ extern "C" int dr_raster_visibility_bin(const DrRasterGeometry* g, void* workspa
   Workspace ws = layout(*g, (char*)workspace);
   if (!workspace || workspace_bytes < ws.bytes) return DR_ERR_CAPACITY;
   hipStream_t s = (hipStream_t)stream;
-  raster_bin_kernel<<<ws.record_blocks, 256, 0, s>>>(ws, (uint2*)entries, counts[1]);
+  raster_bin_kernel<<<bin_grid(ws), 256, 0, s>>>(ws, (uint2*)entries, counts[1]);
   return launch_status();
 }
 
