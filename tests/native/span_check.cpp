@@ -23,7 +23,41 @@ static int pick(int n) { return (int)(next_u64() % (uint64_t)n); }
 
 static float centre(int i, int size) { return (float)(2 * i + 1) / (float)size - 1.0f; }
 
+// A triangle that gets no spans (a vertex at or behind the camera plane, or too thin for the
+// orientation bound) must leave every column of every row to the box: row_span() returns the
+// range it was given.
+static int check_without_spans() {
+  const float cases[3][3][3] = {
+      {{-0.2f, 0.1f, 1.0f}, {0.3f, -0.4f, 0.0f}, {0.5f, 0.5f, 2.0f}},     // w = 0 at a vertex
+      {{0.1f, 0.2f, 1.0f}, {0.4f, 0.1f, -1.0f}, {-0.3f, -0.2f, 1.5f}},    // w < 0 at a vertex
+      {{0.1f, 0.1f, 1.0f}, {0.2f, 0.2f, 1.0f}, {0.3f, 0.3f, 1.0f}},       // collinear: no area
+  };
+  for (int c = 0; c < 3; ++c) {
+    float x[3], y[3], w[3];
+    for (int k = 0; k < 3; ++k) {
+      x[k] = cases[c][k][0] * cases[c][k][2];
+      y[k] = cases[c][k][1] * cases[c][k][2];
+      w[k] = cases[c][k][2];
+    }
+    RowSpans s;
+    if (span_setup(x, y, w, reach(x, w), reach(y, w), 64, 16, s)) {
+      printf("case %d without spans got spans\n", c);
+      return 1;
+    }
+    for (int r = 0; r < 64; ++r) {
+      int lo = 3, hi = 11;
+      row_span(s, centre(r, 64), lo, hi);
+      if (lo != 3 || hi != 11) {
+        printf("case %d row %d without spans: [%d, %d] instead of [3, 11]\n", c, r, lo, hi);
+        return 1;
+      }
+    }
+  }
+  return 0;
+}
+
 int main(int argc, char** argv) {
+  if (check_without_spans() != 0) return 1;
   const long triangles = argc > 1 ? atol(argv[1]) : 200000;
   const int sizes[] = {16, 37, 64, 256, 1024, 4096};
   long checks = 0, accepted = 0, span_pixels = 0, with_spans = 0;
