@@ -1116,32 +1116,47 @@ __global__ __launch_bounds__(256) void raster_tile_classes(Workspace ws) {
 
 // Pass 2, one workgroup: first position of each class. The busy tiles come first, share by
 // share, heaviest class first within a share; the tiles without entries follow, so that the
-// tile pass launches one workgroup per busy tile.
+// tile pass launches one workgroup per busy tile. The classes' offsets are a scan over 32
+// threads per share (a serial walk over the 128 classes, writing each cursor twice, took 10 us).
 __global__ __launch_bounds__(256) void raster_tile_cursors(Workspace ws) {
-  __shared__ uint32_t counts[kXcdShares * kWorkClasses];
+  static_assert(kXcdShares * 32 == 256 && kWorkClasses == 4 * 32,
+                "32 threads per share, 4 classes each");
   __shared__ uint32_t busy[kXcdShares], idle[kXcdShares];
-  for (int i = threadIdx.x; i < kXcdShares * kWorkClasses; i += blockDim.x)
-    counts[i] = ws.class_counts[i];
-  __syncthreads();
-  const int k = threadIdx.x;
-  uint32_t run = 0u;
-  if (k < kXcdShares) {  // the share's classes, relative to its first busy tile
-    for (int c = kWorkClasses - 1; c >= 1; --c) {
-      ws.class_cursor[k * kWorkClasses + c] = run;
-      run += counts[k * kWorkClasses + c];
-    }
-    busy[k] = run;
-    idle[k] = counts[k * kWorkClasses];
+  // Thread t takes share k = t / 32 and its classes 127 - 4s .. 124 - 4s (s = t % 32), heaviest
+  // first; class 0 (no entries) is counted apart.
+  const int k = threadIdx.x / 32, s = threadIdx.x % 32;
+  uint32_t v[4], local = 0u;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = kWorkClasses - 1 - 4 * s - q;
+    v[q] = c >= 1 ? ws.class_counts[k * kWorkClasses + c] : 0u;
+    local += v[q];
+  }
+  // Exclusive prefix of the share's classes in that order: a wave holds two shares (lanes 0-31
+  // and 32-63), so the upper half drops the lower half's total.
+  const uint32_t incl = wave_inclusive_sum(local);
+  const uint32_t lower = (uint32_t)__builtin_amdgcn_readlane((int)incl, 31);
+  const uint32_t share_incl = lane_id() >= 32 ? incl - lower : incl;
+  if (s == 31) {
+    busy[k] = share_incl;
+    idle[k] = ws.class_counts[k * kWorkClasses];
   }
   __syncthreads();
-  if (k < kXcdShares) {
-    uint32_t first = 0u, idle_first = 0u, widest = 0u;
-    for (int j = 0; j < kXcdShares; ++j) {
-      first += j < k ? busy[j] : 0u;
-      idle_first += busy[j] + (j < k ? idle[j] : 0u);
-      widest = max(widest, busy[j]);
-    }
-    for (int c = kWorkClasses - 1; c >= 1; --c) ws.class_cursor[k * kWorkClasses + c] += first;
+  uint32_t first = 0u, idle_first = 0u, widest = 0u;
+#pragma unroll
+  for (int j = 0; j < kXcdShares; ++j) {
+    first += j < k ? busy[j] : 0u;
+    idle_first += busy[j] + (j < k ? idle[j] : 0u);
+    widest = max(widest, busy[j]);
+  }
+  uint32_t at = first + share_incl - local;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = kWorkClasses - 1 - 4 * s - q;
+    if (c >= 1) ws.class_cursor[k * kWorkClasses + c] = at;
+    at += v[q];
+  }
+  if (s == 0) {
     ws.class_cursor[k * kWorkClasses] = idle_first;
     ws.share_info[k] = busy[k];
     ws.share_info[kXcdShares + k] = first;
