@@ -216,10 +216,12 @@ DR_HD bool span_setup(const float* x, const float* y, const float* w, float reac
 
 // Column offsets of row centre py (float, as covers() gets it) that may be covered, clipped to
 // [lo, hi] as given (floats holding integers): on return lo = the first, hi = the last, both
-// integers within the given range when lo <= hi; lo > hi (or NaN) for none.
+// integers within the given range when lo <= hi; lo > hi for none.
 DR_HD void row_bounds(const RowSpans& s, float py, float& lo, float& hi) {
-  const float h = fminf(fminf(fmaf(s.hi_v[0], py, s.hi_u[0]), fmaf(s.hi_v[1], py, s.hi_u[1])), hi);
-  const float l = fmaxf(fmaxf(fmaf(s.lo_v[0], py, s.lo_u[0]), fmaf(s.lo_v[1], py, s.lo_u[1])), lo);
+  const float h =
+      fminf(fminf(fmaf(s.hi_v[0], py, s.hi_u[0]), fmaf(s.hi_v[1], py, s.hi_u[1])), hi);
+  const float l =
+      fmaxf(fmaxf(fmaf(s.lo_v[0], py, s.lo_u[0]), fmaf(s.lo_v[1], py, s.lo_u[1])), lo);
   const bool row = !(fmaf(s.row_v, py, s.row_u) < 0.0f);
   lo = ceilf(l);
   hi = row ? floorf(h) : -HUGE_VALF;

@@ -1062,7 +1062,9 @@ __global__ __launch_bounds__(256) void raster_bin_kernel(Workspace ws, uint2* en
       }
 }
 
-static int bin_grid(const Workspace& ws) { return (ws.record_blocks + kBinBlocks - 1) / kBinBlocks; }
+static int bin_grid(const Workspace& ws) {
+  return (ws.record_blocks + kBinBlocks - 1) / kBinBlocks;
+}
 
 // ---- tile order: heavy tiles first within each XCD's share -----------------------------------
 //
@@ -1344,7 +1346,8 @@ __device__ __forceinline__ void tile_pass(const DrRasterGeometry& g, const uint6
     // kept.
     if (staged && !(cull && bound > far_depth)) {
 #pragma unroll
-      for (int k = 0; k < 3; ++k) s_tri[threadIdx.x][k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
+      for (int k = 0; k < 3; ++k)
+        s_tri[threadIdx.x][k] = make_float4(T.x[k], T.y[k], T.z[k], T.w[k]);
       T.reach_x = reach(T.x, T.w);
       T.reach_y = reach(T.y, T.w);
       int x_lo, x_hi, y_lo, y_hi;
