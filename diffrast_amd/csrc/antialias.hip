@@ -347,13 +347,17 @@ __device__ __forceinline__ Crossing crossing(const Triangle& T, uint8_t sil, boo
   return out;
 }
 
-// d t / d (x, y, w) of the two vertices of `edge`, t = e_s / (e_s - e_d) with
+// The two vertices i, j of a triangle's edge: rows and x, y, w.
+struct EdgeVerts {
+  int vi, vj;
+  float xi, yi, wi, xj, yj, wj;
+};
+
+// d t / d (x, y, w) of the edge's two vertices, t = e_s / (e_s - e_d) with
 // e = a_i c_j - a_j c_i, a = x - px w, c = y - py w. Order: x_i, y_i, w_i, x_j, y_j, w_j.
-__device__ __forceinline__ void crossing_grad(const Triangle& T, int edge, float sx, float sy,
+__device__ __forceinline__ void crossing_grad(const EdgeVerts& E, float sx, float sy,
                                               float dx, float dy, float (&g)[6]) {
-  const int i = (edge + 1) % 3, j = (edge + 2) % 3;
-  const float xi = pick3(T.x, i), yi = pick3(T.y, i), wi = pick3(T.w, i);
-  const float xj = pick3(T.x, j), yj = pick3(T.y, j), wj = pick3(T.w, j);
+  const float xi = E.xi, yi = E.yi, wi = E.wi, xj = E.xj, yj = E.yj, wj = E.wj;
   const float asi = xi - sx * wi, csi = yi - sy * wi;
   const float asj = xj - sx * wj, csj = yj - sy * wj;
   const float adi = xi - dx * wi, cdi = yi - dy * wi;
@@ -413,6 +417,23 @@ __device__ __forceinline__ void load_triangle(const DrAntialiasArgs& a, int b, i
   int v[3];
   load_rows(a, t, v);
   load_vertices(a, b, v, T);
+}
+
+// Rows and vertices of edge `edge` of triangle t: its vertices (edge + 1) mod 3 and
+// (edge + 2) mod 3, the only two the crossing's gradient needs.
+__device__ __forceinline__ void load_edge(const DrAntialiasArgs& a, int b, int t, int edge,
+                                          EdgeVerts& E) {
+  const int32_t* row = a.tri + 3 * (int64_t)t;
+  E.vi = row[edge == 2 ? 0 : edge + 1];
+  E.vj = row[edge == 0 ? 2 : edge - 1];
+  const float* P = a.pos + (int64_t)b * a.pos_batch_stride;
+  const float4 pi = load4(P + 4 * (int64_t)E.vi), pj = load4(P + 4 * (int64_t)E.vj);
+  E.xi = pi.x;
+  E.yi = pi.y;
+  E.wi = pi.w;
+  E.xj = pj.x;
+  E.yj = pj.y;
+  E.wj = pj.w;
 }
 
 // Pair record bits: the pair is active, the first pixel's triangle owns the edge, edge index.
@@ -798,13 +819,12 @@ __global__ __launch_bounds__(256) void aa_bwd_kernel(DrAntialiasArgs a, const fl
         const float qcx = pixel_centre(qx, a.width), qcy = pixel_centre(qy, a.height);
         float depth;
         const int owner = pixel_tri(a, owner_first ? tp.pixel : q, depth);
-        Triangle T;
-        load_triangle(a, tp.b, owner, T);
-        const int edge = info & 3;
+        EdgeVerts E;
+        load_edge(a, tp.b, owner, info & 3, E);
         float d[6];
-        crossing_grad(T, edge, owner_first ? px : qcx, owner_first ? py : qcy,
+        crossing_grad(E, owner_first ? px : qcx, owner_first ? py : qcy,
                       owner_first ? qcx : px, owner_first ? qcy : py, d);
-        const int vi = pick3(T.v, (edge + 1) % 3), vj = pick3(T.v, (edge + 2) % 3);
+        const int vi = E.vi, vj = E.vj;
         rows[2 * n] = (uint32_t)(row0 + vi);
         rows[2 * n + 1] = (uint32_t)(row0 + vj);
         vals[2 * n][0] = g_t * d[0];
