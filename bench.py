@@ -62,13 +62,13 @@ HBM_PEAK = 8.0e12  # bytes/s, MI355X
 METRIC = "ms per fwd+bwd render (4-op pipeline) at 8×1024², 1.3M tris; % HBM roofline"
 
 
-# Entry points that launch exactly one kernel, and that kernel.
+# Entry points that launch exactly one kernel, and that kernel. (dr_interpolate_backward
+# launches interp_bwd_kernel with an attribute gradient and interp_bwd_rast_kernel without.)
 SINGLE_KERNEL = {
     "dr_raster_visibility_tiles": "raster_tile_kernel",
     "dr_resolve_forward": "resolve_fwd_kernel",
     "dr_resolve_backward": "resolve_bwd_kernel",
     "dr_interpolate_forward": "interp_fwd_kernel",
-    "dr_interpolate_backward": "interp_bwd_kernel",
     "dr_texture_forward": "tex_fwd_kernel",
     "dr_texture_backward": "tex_bwd_kernel",
     "dr_antialias_backward": "aa_bwd_kernel",
