@@ -319,13 +319,13 @@ inline int64_t tile_blocks(int batch, int height, int width) {
   return (int64_t)batch * ((width + 15) / 16) * ((height + 15) / 16);
 }
 
-// The pixels of a thread in the gather kernels (resolve, interpolate forward), in one of two
-// layouts. Rows: PPT pixels 256 apart in pixel order, so every wave reads and writes runs of 64
+// The pixels of a thread in the gather kernels (resolve, interpolate), in one of two layouts.
+// Rows: PPT pixels 256 apart in pixel order, so every wave reads and writes runs of 64
 // consecutive pixels; best when what the pixels gather (index rows, vertices, attributes) stays
-// in the L2s anyway, or when the pass is bound by its writes. Tiles: a 16 x 16 PPT tile per
-// workgroup, the tiles in XCD order, pixel j at (x, y0 + 16 j); the pixels of a triangle and of
-// its neighbours, which share vertices, then gather into one XCD's L2 rather than one per image
-// row, which pays when the gathered data outgrows an L2.
+// in the L2s anyway, or when the pass is bound by its writes. Tiles: a TW x (256 / TW) PPT tile
+// per workgroup, the tiles in XCD order, pixel j at (x, y0 + 256 / TW j); the pixels of a
+// triangle and of its neighbours, which share vertices, then gather into one XCD's L2 rather
+// than one per image row, which pays when the gathered data outgrows an L2.
 template <int PPT>
 struct PixelSlots {
   int64_t pixel[PPT];
@@ -333,21 +333,23 @@ struct PixelSlots {
   bool inside[PPT];
 };
 
-template <int PPT, bool TILES>
+template <int PPT, bool TILES, int TW = 16>
 __device__ __forceinline__ PixelSlots<PPT> pixel_slots(int batch, int height, int width) {
+  static_assert(TW > 0 && 256 % TW == 0, "tile rows of whole waves' share");
   PixelSlots<PPT> s;
   if constexpr (TILES) {
-    const int tiles_x = (width + 15) / 16, tiles_y = (height + 16 * PPT - 1) / (16 * PPT);
+    constexpr int TR = 256 / TW;  // rows of the workgroup per pixel slot
+    const int tiles_x = (width + TW - 1) / TW, tiles_y = (height + TR * PPT - 1) / (TR * PPT);
     const int64_t tile = xcd_order(blockIdx.x, (int64_t)batch * tiles_x * tiles_y);
     const int b = (int)(tile / ((int64_t)tiles_x * tiles_y));
     const int in_image = (int)(tile - (int64_t)b * tiles_x * tiles_y);
-    const int x = (in_image % tiles_x) * 16 + (int)(threadIdx.x & 15);
-    const int y0 = (in_image / tiles_x) * 16 * PPT + (int)(threadIdx.x >> 4);
+    const int x = (in_image % tiles_x) * TW + (int)(threadIdx.x % TW);
+    const int y0 = (in_image / tiles_x) * TR * PPT + (int)(threadIdx.x / TW);
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
       s.b[j] = b;
       s.x[j] = x;
-      s.y[j] = y0 + 16 * j;
+      s.y[j] = y0 + TR * j;
       s.inside[j] = x < width && s.y[j] < height;
       s.pixel[j] = ((int64_t)b * height + s.y[j]) * width + x;
     }
@@ -371,9 +373,11 @@ __device__ __forceinline__ PixelSlots<PPT> pixel_slots(int batch, int height, in
   return s;
 }
 
-template <int PPT, bool TILES>
+template <int PPT, bool TILES, int TW = 16>
 inline int64_t pixel_slot_blocks(int batch, int height, int width) {
-  if (TILES) return (int64_t)batch * ((width + 15) / 16) * ((height + 16 * PPT - 1) / (16 * PPT));
+  constexpr int TR = 256 / TW;
+  if (TILES)
+    return (int64_t)batch * ((width + TW - 1) / TW) * ((height + TR * PPT - 1) / (TR * PPT));
   return blocks_for((int64_t)batch * height * width, 256 * PPT);
 }
 
