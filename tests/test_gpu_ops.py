@@ -81,6 +81,29 @@ def test_interpolate_gradients(layout, diff):
     assert_grads_close(ours[1], ref[1])
 
 
+@pytest.mark.parametrize("channels", [1, 2, 3, 5, 8, 33])
+@pytest.mark.parametrize("layout", ["shared", "per_view"])
+def test_interpolate_gradients_of_constant_attributes(channels, layout):
+    # Without an attribute gradient the backward pass has a kernel of its own (grad_rast and
+    # grad_rast_db only); its sums run in the order of the pass that also scatters the attribute
+    # gradient, so the two agree bit for bit, and both agree with the oracle.
+    attr, rast, db, tri = interp_scene(channels, layout, seed=3)
+    gen = torch.Generator().manual_seed(4)
+    a, t = attr.cuda(), tri.cuda()
+    for diff in ([], list(range(channels)), [channels - 1, 0], [0, 0]):
+        w_out = torch.randn(*rast.shape[:3], channels, generator=gen)
+        w_da = torch.randn(*rast.shape[:3], 2 * len(diff), generator=gen)
+        ref = grads_of(lambda r, d: R.interpolate(attr, r, tri, d, diff), [rast, db],
+                       [w_out, w_da], "cpu")
+        ours = grads_of(lambda r, d: hip.interpolate(a, r, t, d, diff), [rast, db],
+                        [w_out, w_da], "cuda")
+        assert_grads_close(ours[1], ref[1])
+        both = grads_of(lambda x, r, d: hip.interpolate(x, r, t, d, diff), [attr, rast, db],
+                        [w_out, w_da], "cuda")
+        assert torch.equal(ours[1][0], both[1][1]), diff
+        assert torch.equal(ours[1][1], both[1][2]), diff
+
+
 def test_interpolate_golden_fixture():
     g = {k: torch.from_numpy(v) for k, v in np.load(GOLDEN / "interpolate.npz").items()}
     outs, grads = grads_of(lambda a, r, d: hip.interpolate(a, r, g["tri"].cuda(), d, [3, 0]),
