@@ -307,9 +307,10 @@ __global__ __launch_bounds__(256) void interp_bwd_kernel(DrInterpolateArgs a,
 
 // The backward pass without an attribute gradient (constant attributes): grad_rast and, with
 // DIFF, grad_rast_db only, in the forward pass's gather layout and without the scatter table --
-// PPT pixels per thread, their rast and rast_db, then the index rows, then the upstream
-// gradients and the attribute rows, each level's loads issued together. The sums run in the
-// order of interp_bwd_kernel (channels in passes of N, derivatives in list order in a pass).
+// PPT pixels per thread, their rast, then the index rows, then the upstream gradients and the
+// attribute rows, each level's loads issued together (rast_db itself takes no part: only the
+// attribute gradient depends on it). The sums run in the order of interp_bwd_kernel (channels
+// in passes of N, derivatives in list order in a pass).
 template <int NC, int PPT, bool TILES, bool DIFF>
 __global__ __launch_bounds__(256) void interp_bwd_rast_kernel(DrInterpolateArgs a,
                                                               const float* __restrict__ grad_out,
@@ -323,12 +324,10 @@ __global__ __launch_bounds__(256) void interp_bwd_rast_kernel(DrInterpolateArgs 
   constexpr int N = NC > 0 && NC < 8 ? NC : 8;
   const int D = DIFF && grad_da != nullptr ? a.num_diff : 0;
   const int64_t* pixel = s.pixel;
-  float4 r[PPT], db[PPT];
+  float4 r[PPT];
 #pragma unroll
-  for (int j = 0; j < PPT; ++j) {
+  for (int j = 0; j < PPT; ++j)
     r[j] = s.inside[j] ? load4(a.rast + 4 * pixel[j]) : make_float4(0.f, 0.f, 0.f, 0.f);
-    db[j] = DIFF && s.inside[j] ? load4(a.rast_db + 4 * pixel[j]) : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
   Pixel p[PPT];
 #pragma unroll
   for (int j = 0; j < PPT; ++j) p[j] = pixel_of(a, r[j], s.b[j], rows_per_image);
