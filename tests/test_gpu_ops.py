@@ -104,6 +104,36 @@ def test_interpolate_gradients_of_constant_attributes(channels, layout):
         assert torch.equal(ours[1][1], both[1][2]), diff
 
 
+@pytest.mark.parametrize("channels", [2, 8])
+def test_interpolate_gather_tiles_on_partial_tiles(channels):
+    # Index rows of 400,000 triangles outgrow an L2, so the forward pass and the backward pass
+    # of constant attributes take the tiled gather layout; 2 x 45 x 70 pixels leave partial tiles
+    # at the right and lower edges. rast is synthetic (any barycentrics, ids, background).
+    gen = torch.Generator().manual_seed(9)
+    num_tri, num_vertices = 400_000, 150_000
+    tri = torch.randint(0, num_vertices, (num_tri, 3), generator=gen, dtype=torch.int32)
+    attr = torch.randn(num_vertices, channels, generator=gen)
+    shape = (2, 45, 70)
+    ids = torch.randint(0, num_tri + 1, shape, generator=gen).float()  # 0: background
+    rast = torch.cat([torch.rand(*shape, 3, generator=gen), ids[..., None]], -1)
+    db = torch.randn(*shape, 4, generator=gen)
+    diff = list(range(channels))
+    a, t = attr.cuda(), tri.cuda()
+    ref = R.interpolate(attr, rast, tri, db, diff)
+    out = hip.interpolate(a, rast.cuda(), t, db.cuda(), diff)
+    assert torch.equal(out[0].cpu(), ref[0]) and torch.equal(out[1].cpu(), ref[1])
+    w_out = torch.randn(*shape, channels, generator=gen)
+    w_da = torch.randn(*shape, 2 * channels, generator=gen)
+    expect = grads_of(lambda r, d: R.interpolate(attr, r, tri, d, diff), [rast, db],
+                      [w_out, w_da], "cpu")
+    ours = grads_of(lambda r, d: hip.interpolate(a, r, t, d, diff), [rast, db], [w_out, w_da],
+                    "cuda")
+    assert_grads_close(ours[1], expect[1])
+    both = grads_of(lambda x, r, d: hip.interpolate(x, r, t, d, diff), [attr, rast, db],
+                    [w_out, w_da], "cuda")
+    assert torch.equal(ours[1][0], both[1][1]) and torch.equal(ours[1][1], both[1][2])
+
+
 def test_interpolate_golden_fixture():
     g = {k: torch.from_numpy(v) for k, v in np.load(GOLDEN / "interpolate.npz").items()}
     outs, grads = grads_of(lambda a, r, d: hip.interpolate(a, r, g["tri"].cuda(), d, [3, 0]),
