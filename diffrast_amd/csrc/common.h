@@ -335,7 +335,7 @@ struct PixelSlots {
 
 template <int PPT, bool TILES, int TW = 16>
 __device__ __forceinline__ PixelSlots<PPT> pixel_slots(int batch, int height, int width) {
-  static_assert(TW > 0 && 256 % TW == 0, "tile rows of whole waves' share");
+  static_assert(TW > 0 && 256 % TW == 0, "the tile width must divide the 256 threads");
   PixelSlots<PPT> s;
   if constexpr (TILES) {
     constexpr int TR = 256 / TW;  // rows of the workgroup per pixel slot
